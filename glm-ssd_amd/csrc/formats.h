@@ -1,0 +1,391 @@
+// gfx950 device-side decoders of the ggml block formats.
+//
+// Two families:
+//   * deq8_*  : exact dequantization of the 8 elements [8g, 8g+8) of one block, bit-identical to
+//               the CPU reference (crates/quants/src/lib.rs:131-343). Used by gs_dequant_* and by
+//               the generic matmul path. The f32 operation order is the reference's and FP
+//               contraction is off in this section, so no multiply-add gets fused.
+//   * F*::dot : the fast integer paths for Q8_0 / Q4_K / Q6_K / IQ2_XXS. One call decodes one
+//               32-element "unit" of a weight row from LDS and dots it with up to NV q8_1 activation
+//               units held in registers (v_dot4_i32_i8), applying the block scales in f32.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "kargs.h"
+
+// ---- small helpers --------------------------------------------------------------------------
+__device__ __forceinline__ float h2f(uint32_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+    return (float)v;
+}
+__device__ __forceinline__ uint32_t f2h(float f) { // round to nearest even (v_cvt_f16_f32)
+    _Float16 v = (_Float16)f;
+    return (uint32_t)__builtin_bit_cast(uint16_t, v);
+}
+// byte-wise little-endian reads through any pointer (global or LDS), no alignment needed
+__device__ __forceinline__ uint32_t rb8(const uint8_t *p, int i) { return p[i]; }
+__device__ __forceinline__ uint32_t rb16(const uint8_t *p, int i) { return (uint32_t)p[i] | ((uint32_t)p[i + 1] << 8); }
+__device__ __forceinline__ uint32_t rb32(const uint8_t *p, int i) {
+    return (uint32_t)p[i] | ((uint32_t)p[i + 1] << 8) | ((uint32_t)p[i + 2] << 16) | ((uint32_t)p[i + 3] << 24);
+}
+
+// N unaligned 32-bit words starting at LDS byte offset `off`: N+1 aligned dword reads, then
+// v_alignbyte_b32 funnels each word out of its two neighbours.
+template <int N>
+__device__ __forceinline__ void lds_words(const uint8_t *L, uint32_t off, uint32_t (&w)[N]) {
+    const uint32_t a = off & ~3u, s = off & 3u;
+    const uint32_t *p = (const uint32_t *)(L + a);
+    uint32_t d[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; i++) d[i] = p[i];
+#pragma unroll
+    for (int i = 0; i < N; i++) w[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], s);
+}
+__device__ __forceinline__ uint32_t lds_word(const uint8_t *L, uint32_t off) {
+    uint32_t w[1];
+    lds_words<1>(L, off, w);
+    return w[0];
+}
+__device__ __forceinline__ float lds_half(const uint8_t *L, uint32_t off) { // off even
+    return h2f(*(const uint16_t *)(L + off));
+}
+
+// ggml tables live in the code object's read-only data
+#include "ggml_grids.h"
+
+// ksigns_iq2xs[i] == i | parity(i) << 7  (closed form of crates/quants/src/tables.rs:9-18)
+__device__ __forceinline__ uint32_t ksigns(uint32_t i) { return i | ((__builtin_popcount(i) & 1u) << 7); }
+
+// =============================================================================================
+// Exact decoders (bit-identical to crates/quants/src/lib.rs)
+// =============================================================================================
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t *q, uint32_t &sc, uint32_t &m) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// block_q8_0 { half d; int8 qs[32]; }  lib.rs:131-136
+__device__ __forceinline__ void deq8_q8_0(const uint8_t *b, int g, float *v) {
+    const float d = h2f(rb16(b, 0));
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)(int8_t)b[2 + 8 * g + i] * d;
+}
+// block_q2_K { u8 scales[16]; u8 qs[64]; half d; half dmin; }  lib.rs:139-160
+__device__ __forceinline__ void deq8_q2_k(const uint8_t *b, int g, float *v) {
+    const int e0 = 8 * g, half = e0 >> 7, r = e0 & 127, j = r >> 5, part = (r >> 4) & 1, l0 = r & 15;
+    const uint32_t sc = b[8 * half + 2 * j + part];
+    const float dl = h2f(rb16(b, 80)) * (float)(sc & 15), ml = h2f(rb16(b, 82)) * (float)(sc >> 4);
+    const uint8_t *q = b + 16 + 32 * half + 16 * part + l0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = dl * (float)((q[i] >> (2 * j)) & 3) - ml;
+}
+// block_q3_K { u8 hmask[32]; u8 qs[64]; u8 scales[12]; half d; }  lib.rs:163-201
+__device__ __forceinline__ void deq8_q3_k(const uint8_t *b, int g, float *v) {
+    const int e0 = 8 * g, half = e0 >> 7, r = e0 & 127, j = r >> 5, part = (r >> 4) & 1, l0 = r & 15;
+    const int is = 8 * half + 2 * j + part;
+    const uint8_t *raw = b + 96;
+    const int low = is < 8 ? (raw[is] & 15) : (raw[is - 8] >> 4);
+    const int high = (raw[8 + (is & 3)] >> (2 * (is >> 2))) & 3;
+    const float dl = h2f(rb16(b, 108)) * (float)((low | (high << 4)) - 32);
+    const uint32_t m = 1u << (4 * half + j);
+    const uint8_t *hm = b + 16 * part + l0;
+    const uint8_t *q = b + 32 + 32 * half + 16 * part + l0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = dl * (float)((int)((q[i] >> (2 * j)) & 3) - ((hm[i] & m) ? 0 : 4));
+}
+// block_q4_K { half d; half dmin; u8 scales[12]; u8 qs[128]; }  lib.rs:204-218
+__device__ __forceinline__ void deq8_q4_k(const uint8_t *b, int g, float *v) {
+    const int e0 = 8 * g, jb = e0 >> 6, hi = (e0 >> 5) & 1, l0 = e0 & 31;
+    uint32_t sc, mn;
+    scale_min_k4(2 * jb + hi, b + 4, sc, mn);
+    const float d = h2f(rb16(b, 0)) * (float)sc, m = h2f(rb16(b, 2)) * (float)mn;
+    const uint8_t *q = b + 16 + 32 * jb + l0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = d * (float)(hi ? (q[i] >> 4) : (q[i] & 15)) - m;
+}
+// block_q5_K { half d; half dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]; }  lib.rs:221-240
+__device__ __forceinline__ void deq8_q5_k(const uint8_t *b, int g, float *v) {
+    const int e0 = 8 * g, jb = e0 >> 6, hi = (e0 >> 5) & 1, l0 = e0 & 31;
+    uint32_t sc, mn;
+    scale_min_k4(2 * jb + hi, b + 4, sc, mn);
+    const float d = h2f(rb16(b, 0)) * (float)sc, m = h2f(rb16(b, 2)) * (float)mn;
+    const uint8_t *qh = b + 16 + l0, *q = b + 48 + 32 * jb + l0;
+    const int hb = 2 * jb + hi;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t lo = hi ? (q[i] >> 4) : (q[i] & 15);
+        v[i] = d * (float)(lo + (((qh[i] >> hb) & 1) << 4)) - m;
+    }
+}
+// block_q6_K { u8 ql[128]; u8 qh[64]; i8 scales[16]; half d; }  lib.rs:243-262
+__device__ __forceinline__ void deq8_q6_k(const uint8_t *b, int g, float *v) {
+    const int e0 = 8 * g, half = e0 >> 7, r = e0 & 127, quarter = r >> 5, l0 = r & 31;
+    const uint8_t *ql = b + 64 * half + l0 + 32 * (quarter & 1);
+    const uint8_t *qh = b + 128 + 32 * half + l0;
+    const float dsc = h2f(rb16(b, 208)) * (float)(int8_t)b[192 + 8 * half + (l0 >> 4) + 2 * quarter];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int nib = quarter >= 2 ? (ql[i] >> 4) : (ql[i] & 15);
+        const int hb = (qh[i] >> (2 * quarter)) & 3;
+        v[i] = dsc * (float)((nib | (hb << 4)) - 32);
+    }
+}
+__device__ __forceinline__ void grid8_signed(uint64_t grid, uint32_t signs, float db, float *v) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float x = db * (float)((grid >> (8 * j)) & 0xff);
+        v[j] = ((signs >> j) & 1) ? -x : x;
+    }
+}
+// block_iq2_xxs { half d; u16 qs[32]; }  lib.rs:274-288
+__device__ __forceinline__ void deq8_iq2_xxs(const uint8_t *b, int g, float *v) {
+    const int ib32 = g >> 2, l = g & 3;
+    const uint32_t a0 = rb32(b, 2 + 8 * ib32), a1 = rb32(b, 6 + 8 * ib32);
+    const float db = h2f(rb16(b, 0)) * (0.5f + (float)(a1 >> 28)) * 0.25f;
+    grid8_signed(iq2xxs_grid[(a0 >> (8 * l)) & 0xff], ksigns((a1 >> (7 * l)) & 127), db, v);
+}
+// block_iq2_s { half d; u8 qs[32]; u8 signs[32]; u8 qh[8]; u8 scales[8]; }  lib.rs:291-310
+__device__ __forceinline__ void deq8_iq2_s(const uint8_t *b, int g, float *v) {
+    const int ib32 = g >> 2, l = g & 3;
+    const float dl = h2f(rb16(b, 0)) * (0.5f + (float)((b[74 + ib32] >> (4 * (l >> 1))) & 15)) * 0.25f;
+    const int idx = b[2 + 4 * ib32 + l] | ((b[66 + ib32] << (8 - 2 * l)) & 0x300);
+    grid8_signed(iq2s_grid[idx], b[34 + 4 * ib32 + l], dl, v);
+}
+// block_iq3_xxs { half d; u8 qs[64]; u8 scales_and_signs[32]; }  lib.rs:312-328
+__device__ __forceinline__ void deq8_iq3_xxs(const uint8_t *b, int g, float *v) {
+    const int ib32 = g >> 2, l = g & 3;
+    const uint32_t aux = rb32(b, 66 + 4 * ib32);
+    const float db = h2f(rb16(b, 0)) * (0.5f + (float)(aux >> 28)) * 0.5f;
+    const uint64_t g1 = iq3xxs_grid[b[2 + 8 * ib32 + 2 * l]], g2 = iq3xxs_grid[b[2 + 8 * ib32 + 2 * l + 1]];
+    grid8_signed(g1 | (g2 << 32), ksigns((aux >> (7 * l)) & 127), db, v);
+}
+// block_iq4_xs { half d; u16 scales_h; u8 scales_l[4]; u8 qs[128]; }  lib.rs:331-343
+__device__ __forceinline__ void deq8_iq4_xs(const uint8_t *b, int g, float *v) {
+    const int e0 = 8 * g, ib = e0 >> 5, hi = (e0 >> 4) & 1, j0 = e0 & 15;
+    const uint32_t scales_h = rb16(b, 2);
+    const int ls = ((b[4 + (ib >> 1)] >> (4 * (ib & 1))) & 15) | (((scales_h >> (2 * ib)) & 3) << 4);
+    const float dl = h2f(rb16(b, 0)) * (float)(ls - 32);
+    const uint8_t *q = b + 8 + 16 * ib + j0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = dl * (float)kvalues_iq4nl[hi ? (q[i] >> 4) : (q[i] & 15)];
+}
+// 8 consecutive plain elements
+__device__ __forceinline__ void deq8_f32(const uint8_t *b, int, float *v) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(float, rb32(b, 4 * i));
+}
+__device__ __forceinline__ void deq8_f16(const uint8_t *b, int, float *v) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = h2f(rb16(b, 2 * i));
+}
+__device__ __forceinline__ void deq8_bf16(const uint8_t *b, int, float *v) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(float, rb16(b, 2 * i) << 16);
+}
+
+#pragma clang fp contract(fast)
+
+// Type traits. QK = elements per block, BB = bytes per block (types.rs:85-113).
+// For QK < 8 (plain types) one "block" here is 8 elements so deq8 always sees a whole group.
+// X(type id, QK, BB, decoder); the id is spelled as a number because it names kernels
+#define GS_TYPE_LIST(X)                                                                         \
+    X(0, 8, 32, deq8_f32) X(1, 8, 16, deq8_f16) X(30, 8, 16, deq8_bf16)                         \
+    X(8, 32, 34, deq8_q8_0) X(10, 256, 84, deq8_q2_k) X(11, 256, 110, deq8_q3_k)               \
+    X(12, 256, 144, deq8_q4_k) X(13, 256, 176, deq8_q5_k) X(14, 256, 210, deq8_q6_k)           \
+    X(16, 256, 66, deq8_iq2_xxs) X(22, 256, 82, deq8_iq2_s)                                    \
+    X(18, 256, 98, deq8_iq3_xxs) X(23, 256, 136, deq8_iq4_xs)
+
+// =============================================================================================
+// Fast unit dot products against q8_1 activations
+// =============================================================================================
+// One q8_1 activation unit (32 elements) in registers.
+struct XU {
+    uint32_t q[8];   // int8 x 32
+    float D;         // f16-rounded scale (times the routing weight for MoE down)
+    int slo, shi;    // sum of q over elements 0..15 / 16..31
+};
+
+// Per-format geometry of a unit (32 elements) within a row: byte offset of its block and the
+// unit index inside that block.
+template <int QK, int BB>
+struct UnitGeom {
+    static constexpr int UPB = QK >= 32 ? QK / 32 : 1;   // units per block
+    __device__ static __forceinline__ uint32_t off(int u) {
+        return QK >= 32 ? (uint32_t)(u / UPB) * BB : (uint32_t)u * (32 / QK) * BB;
+    }
+    __device__ static __forceinline__ int sub(int u) { return QK >= 32 ? u % UPB : 0; }
+};
+
+__device__ __forceinline__ int dot8(const uint32_t (&w)[8], const uint32_t (&q)[8]) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = __builtin_amdgcn_sdot4((int)w[i], (int)q[i], s, false);
+    return s;
+}
+
+struct FQ8_0 : UnitGeom<32, 34> {
+    static constexpr int TYPE = GS_Q8_0, QK = 32, BB = 34, TAB = 0;
+    __device__ static void init(uint8_t *, int) {}
+    template <int NV>
+    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int, const uint8_t *, const XU (&x)[NV],
+                                               int nv, float (&r)[NV]) {
+        const float d = lds_half(L, o);
+        uint32_t w[8];
+        lds_words<8>(L, o + 2, w);
+#pragma unroll
+        for (int t = 0; t < NV; t++)
+            if (t < nv) r[t] += (d * x[t].D) * (float)dot8(w, x[t].q);
+    }
+};
+
+struct FQ4_K : UnitGeom<256, 144> {
+    static constexpr int TYPE = GS_Q4_K, QK = 256, BB = 144, TAB = 0;
+    __device__ static void init(uint8_t *, int) {}
+    template <int NV>
+    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int j, const uint8_t *, const XU (&x)[NV],
+                                               int nv, float (&r)[NV]) {
+        uint32_t hd[4];
+        lds_words<4>(L, o, hd);   // d | dmin, scales[0..11]
+        const float d = h2f(hd[0] & 0xffff), dmin = h2f(hd[0] >> 16);
+        // bytes k of scales[] = byte (k+4) of the block
+        auto sb = [&](int k) -> uint32_t { return (hd[1 + (k >> 2)] >> (8 * (k & 3))) & 0xff; };
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = sb(j) & 63;
+            mn = sb(j + 4) & 63;
+        } else {
+            sc = (sb(j + 4) & 0xF) | ((sb(j - 4) >> 6) << 4);
+            mn = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
+        }
+        uint32_t w[8];
+        lds_words<8>(L, o + 16 + 32 * (j >> 1), w);
+        const int sh = (j & 1) * 4;
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = (w[i] >> sh) & 0x0F0F0F0Fu;
+        const float ds = d * (float)sc, dm = dmin * (float)mn;
+#pragma unroll
+        for (int t = 0; t < NV; t++)
+            if (t < nv) r[t] += x[t].D * (ds * (float)dot8(w, x[t].q) - dm * (float)(x[t].slo + x[t].shi));
+    }
+};
+
+struct FQ6_K : UnitGeom<256, 210> {
+    static constexpr int TYPE = GS_Q6_K, QK = 256, BB = 210, TAB = 0;
+    __device__ static void init(uint8_t *, int) {}
+    template <int NV>
+    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int j, const uint8_t *, const XU (&x)[NV],
+                                               int nv, float (&r)[NV]) {
+        const int half = j >> 2, quarter = j & 3;
+        uint32_t ql[8], qh[8];
+        lds_words<8>(L, o + 64 * half + 32 * (quarter & 1), ql);
+        lds_words<8>(L, o + 128 + 32 * half, qh);
+        const int nsh = quarter >= 2 ? 4 : 0, hsh = 2 * quarter;
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = ((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4);
+        const uint32_t scw = lds_word(L, o + 192 + 8 * half + 2 * quarter);
+        const int sc0 = (int8_t)(scw & 0xff), sc1 = (int8_t)((scw >> 8) & 0xff);
+        const float d = lds_half(L, o + 208);
+#pragma unroll
+        for (int t = 0; t < NV; t++) {
+            if (t < nv) {
+                int lo = 0, hi = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) lo = __builtin_amdgcn_sdot4((int)w[i], (int)x[t].q[i], lo, false);
+#pragma unroll
+                for (int i = 4; i < 8; i++) hi = __builtin_amdgcn_sdot4((int)w[i], (int)x[t].q[i], hi, false);
+                r[t] += (d * x[t].D) * (float)(sc0 * (lo - 32 * x[t].slo) + sc1 * (hi - 32 * x[t].shi));
+            }
+        }
+    }
+};
+
+// IQ2_XXS: the 256-entry grid (2 KiB) and a 128-entry table of v_perm_b32 selectors (1 KiB)
+// live in LDS. A selector picks, per byte, the grid byte (sel = i) or its negation (sel = i+4)
+// from the pair {-grid, grid}; -grid bytes come from one subtraction (0x01010100 - grid) since
+// every grid byte is nonzero.
+struct FIQ2_XXS : UnitGeom<256, 66> {
+    static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 2048 + 1024;
+    __device__ static void init(uint8_t *tab, int tid) {
+        uint64_t *g = (uint64_t *)tab;
+        for (int i = tid; i < 256; i += GS_WG) g[i] = iq2xxs_grid[i];
+        uint32_t *s = (uint32_t *)(tab + 2048);
+        for (int i = tid; i < 128; i += GS_WG) {
+            const uint32_t k = ksigns((uint32_t)i);
+            uint32_t lo = 0x03020100u, hi = 0x03020100u;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                lo += ((k >> b) & 1u) << (8 * b + 2);
+                hi += ((k >> (b + 4)) & 1u) << (8 * b + 2);
+            }
+            s[2 * i] = lo;
+            s[2 * i + 1] = hi;
+        }
+    }
+    template <int NV>
+    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int j, const uint8_t *tab,
+                                               const XU (&x)[NV], int nv, float (&r)[NV]) {
+        const float d = lds_half(L, o);
+        uint32_t a[2];
+        lds_words<2>(L, o + 2 + 8 * j, a);
+        const float db = d * (0.5f + (float)(a[1] >> 28)) * 0.25f;
+        const uint2 *grid = (const uint2 *)tab;
+        const uint2 *sel = (const uint2 *)(tab + 2048);
+        uint32_t w[8];
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint2 g = grid[(a[0] >> (8 * l)) & 0xff];
+            const uint2 s = sel[(a[1] >> (7 * l)) & 127];
+            w[2 * l] = __builtin_amdgcn_perm(0x01010100u - g.x, g.x, s.x);
+            w[2 * l + 1] = __builtin_amdgcn_perm(0x01010100u - g.y, g.y, s.y);
+        }
+#pragma unroll
+        for (int t = 0; t < NV; t++)
+            if (t < nv) r[t] += (db * x[t].D) * (float)dot8(w, x[t].q);
+    }
+};
+
+// Generic path for the remaining types: exact f32 decode of the unit, f32 dot with the
+// dequantized activations (D * q). Slower, used for the non-hot formats.
+template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float *)>
+struct FGeneric : UnitGeom<QK_, BB_> {
+    static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0;
+    __device__ static void init(uint8_t *, int) {}
+    template <int NV>
+    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int j, const uint8_t *, const XU (&x)[NV],
+                                               int nv, float (&r)[NV]) {
+        float v[32];
+        if (QK >= 32) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) DEQ(L + o, 4 * j + g, v + 8 * g);
+        } else {
+#pragma unroll
+            for (int g = 0; g < 4; g++) DEQ(L + o + g * BB, 0, v + 8 * g);
+        }
+#pragma unroll
+        for (int t = 0; t < NV; t++) {
+            if (t < nv) {
+                float s = 0.f;
+#pragma unroll
+                for (int i = 0; i < 32; i++) s += v[i] * (float)(int8_t)((x[t].q[i >> 2] >> (8 * (i & 3))) & 0xff);
+                r[t] += x[t].D * s;
+            }
+        }
+    }
+};
+using FF32 = FGeneric<GS_F32, 8, 32, deq8_f32>;
+using FF16 = FGeneric<GS_F16, 8, 16, deq8_f16>;
+using FBF16 = FGeneric<GS_BF16, 8, 16, deq8_bf16>;
+using FQ2_K = FGeneric<GS_Q2_K, 256, 84, deq8_q2_k>;
+using FQ3_K = FGeneric<GS_Q3_K, 256, 110, deq8_q3_k>;
+using FQ5_K = FGeneric<GS_Q5_K, 256, 176, deq8_q5_k>;
+using FIQ2_S = FGeneric<GS_IQ2_S, 256, 82, deq8_iq2_s>;
+using FIQ3_XXS = FGeneric<GS_IQ3_XXS, 256, 98, deq8_iq3_xxs>;
+using FIQ4_XS = FGeneric<GS_IQ4_XS, 256, 136, deq8_iq4_xs>;

@@ -1,0 +1,498 @@
+// Host side of libglmssd_hip.so: the gs_* C ABI (include/glmssd.h) over the HIP module API.
+//
+// The gfx950 code objects are embedded in the library (blobs.S) and loaded per device with
+// hipModuleLoadData on first use; kernels are looked up by name and launched with
+// hipModuleLaunchKernel, each with a single by-value argument block (kargs.h). Argument
+// validation mirrors the reference's (crates/cuda/kernels/quants.cu:223-256,378-409,
+// gemm.cu:107-152) and returns hipErrorInvalidValue without launching on bad input.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/glmssd.h"
+#include "kargs.h"
+
+#define GS_EXPORT extern "C" __attribute__((visibility("default")))
+
+// ---- embedded code objects --------------------------------------------------------------------
+#define GS_BLOB(NAME)                                 \
+    extern "C" const unsigned char gs_blob_##NAME##_start[]; \
+    extern "C" const unsigned char gs_blob_##NAME##_end[];
+#define GS_BLOB_LIST(X) X(common) X(t0) X(t1) X(t8) X(t10) X(t11) X(t12) X(t13) X(t14) X(t16) X(t18) X(t22) X(t23) X(t30)
+GS_BLOB_LIST(GS_BLOB)
+
+namespace {
+
+struct Blob {
+    const unsigned char *p;
+    size_t n;
+};
+std::vector<Blob> blobs() {
+    std::vector<Blob> v;
+#define GS_BLOB_ITEM(NAME) v.push_back({gs_blob_##NAME##_start, (size_t)(gs_blob_##NAME##_end - gs_blob_##NAME##_start)});
+    GS_BLOB_LIST(GS_BLOB_ITEM)
+#undef GS_BLOB_ITEM
+    return v;
+}
+
+struct DeviceCtx {
+    std::vector<hipModule_t> mods;
+    std::map<std::string, hipFunction_t> fns;
+    int cu_count = 0;
+    size_t max_lds = 0;
+    hipError_t init_err = hipSuccess;
+    std::map<std::pair<std::string, int>, int> occ;  // (kernel, lds) -> blocks per CU
+};
+
+std::mutex g_mu;
+std::map<int, DeviceCtx *> g_ctx;
+
+DeviceCtx *ctx(hipError_t *err) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        *err = e;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_ctx.find(dev);
+    if (it != g_ctx.end()) {
+        *err = it->second->init_err;
+        return it->second->init_err == hipSuccess ? it->second : nullptr;
+    }
+    DeviceCtx *c = new DeviceCtx();
+    g_ctx[dev] = c;
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, dev);
+    if (e == hipSuccess) {
+        c->cu_count = p.multiProcessorCount;
+        c->max_lds = p.sharedMemPerBlock;
+        if (!strstr(p.gcnArchName, "gfx950")) {
+            fprintf(stderr, "glmssd: device %d is %s; this library carries gfx950 code only\n", dev, p.gcnArchName);
+            e = hipErrorNoBinaryForGpu;
+        }
+    }
+    if (e == hipSuccess) {
+        for (const Blob &b : blobs()) {
+            hipModule_t m;
+            e = hipModuleLoadData(&m, b.p);
+            if (e != hipSuccess) break;
+            c->mods.push_back(m);
+        }
+    }
+    c->init_err = e;
+    *err = e;
+    return e == hipSuccess ? c : nullptr;
+}
+
+hipError_t get_fn(DeviceCtx *c, const std::string &name, hipFunction_t *f) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = c->fns.find(name);
+    if (it != c->fns.end()) {
+        *f = it->second;
+        return hipSuccess;
+    }
+    for (hipModule_t m : c->mods) {
+        if (hipModuleGetFunction(f, m, name.c_str()) == hipSuccess) {
+            c->fns[name] = *f;
+            return hipSuccess;
+        }
+    }
+    (void)hipGetLastError();  // clear the lookup misses
+    fprintf(stderr, "glmssd: kernel %s not found in the embedded code objects\n", name.c_str());
+    return hipErrorNotFound;
+}
+
+template <class A>
+hipError_t launch(const std::string &name, dim3 grid, dim3 block, size_t lds, hipStream_t s, const A &args) {
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    hipFunction_t f;
+    if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
+    if (lds > c->max_lds) return hipErrorInvalidValue;
+    size_t sz = sizeof(A);
+    void *cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *)&args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                   HIP_LAUNCH_PARAM_END};
+    return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, (unsigned)lds, s, nullptr, cfg);
+}
+
+// ---- ggml geometry (crates/gguf/src/types.rs:85-113); plain types use 8-element "blocks" ------
+bool geometry(int ty, int &qk, int &bb) {
+    switch (ty) {
+        case GS_F32: qk = 8; bb = 32; return true;
+        case GS_F16: case GS_BF16: qk = 8; bb = 16; return true;
+        case GS_Q8_0: qk = 32; bb = 34; return true;
+        case GS_Q2_K: qk = 256; bb = 84; return true;
+        case GS_Q3_K: qk = 256; bb = 110; return true;
+        case GS_Q4_K: qk = 256; bb = 144; return true;
+        case GS_Q5_K: qk = 256; bb = 176; return true;
+        case GS_Q6_K: qk = 256; bb = 210; return true;
+        case GS_IQ2_XXS: qk = 256; bb = 66; return true;
+        case GS_IQ2_S: qk = 256; bb = 82; return true;
+        case GS_IQ3_XXS: qk = 256; bb = 98; return true;
+        case GS_IQ4_XS: qk = 256; bb = 136; return true;
+        default: return false;
+    }
+}
+int ggml_block_elems(int ty) {  // elements per ggml block (1 for plain types)
+    return ty == GS_F32 || ty == GS_F16 || ty == GS_BF16 ? 1 : (ty == GS_Q8_0 ? 32 : 256);
+}
+int table_bytes(int ty) { return ty == GS_IQ2_XXS ? 2048 + 1024 : 0; }
+
+struct StreamLaunch {
+    StreamArgs a;
+    uint32_t cps_magic;
+    int cps;
+};
+
+// Plan and launch one streaming kernel (kind 0 GEMV, 1 MoE gate/up, 2 MoE down).
+hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 1) {
+    int qk, bb;
+    if (!geometry(ty, qk, bb)) return hipErrorInvalidValue;
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    const int NS = kind == 0 ? 1 : (kind == 1 ? 2 : a.nseg);
+    const int NVt = a.nvec <= 1 ? 1 : a.nvec <= 2 ? 2 : a.nvec <= 4 ? 4 : 8;
+    const int UMAX = 8 / NVt;
+    a.row_bytes = (int)((int64_t)a.K / qk * bb);
+    a.nu = a.K / 32;
+    a.contig = a.row_stride == a.row_bytes;
+    const int tot = NS * a.nu;
+    const int tab = (table_bytes(ty) + 15) & ~15;
+    const int xq_bytes = (kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
+    const int budget = (int)std::min<size_t>(c->max_lds, 160 * 1024);
+    int best = -1;
+    for (int lpr : {16, 32, 64}) {
+        const int upl = (tot + lpr - 1) / lpr;
+        if (upl > UMAX) continue;
+        const int G = GS_WG / lpr;
+        int rt = a.contig ? std::min(G, a.rows) : 1;
+        const int pitch = ((rt * a.row_bytes + 15 + 16) + 15) & ~15;
+        const int cps = (rt * a.row_bytes + 15 + 15) / 16;
+        if (NS * cps > GS_WG * GS_LD_MAX) continue;
+        if (tab + std::max(xq_bytes, NS * pitch + 16) > budget) continue;
+        best = lpr;
+        a.lpr = lpr;
+        a.upl = upl;
+        a.rt = rt;
+        a.span_pitch = pitch;
+        break;
+    }
+    if (best < 0) return hipErrorInvalidValue;
+    const int cps = (a.rt * a.row_bytes + 15 + 15) / 16;
+    a.n_row_tiles = (a.rows + a.rt - 1) / a.rt;
+    a.n_tiles = kind == 1 ? a.nseg * a.n_row_tiles : a.n_row_tiles;
+    a.lds_tile = NS * a.span_pitch;
+    const size_t lds = (size_t)tab + std::max(xq_bytes, NS * a.span_pitch + 16);
+    StreamLaunch L;
+    L.a = a;
+    L.cps = cps;
+    L.cps_magic = (uint32_t)((0x100000000ull + cps - 1) / cps);
+    const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" + std::to_string(NVt);
+    hipFunction_t f;
+    if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
+    int per_cu = 1;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto key = std::make_pair(name, (int)lds);
+        auto it = c->occ.find(key);
+        if (it != c->occ.end()) {
+            per_cu = it->second;
+        } else {
+            int nb = 0;
+            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, GS_WG, lds) != hipSuccess || nb < 1) nb = 1;
+            c->occ[key] = nb;
+            per_cu = nb;
+        }
+    }
+    const int grid = std::max(1, std::min(a.n_tiles, c->cu_count * per_cu));
+    return launch(name, dim3(grid, n_batch, 1), dim3(GS_WG, 1, 1), lds, s, L);
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+int check_w(const void *W, int64_t row_stride) { return ((uintptr_t)W & 1) == 0 && (row_stride & 1) == 0; }
+
+}  // namespace
+
+// =============================================================================================
+// runtime (crates/cuda/kernels/runtime.cu:16-91)
+// =============================================================================================
+GS_EXPORT int gs_device_info(int dev, GsDeviceInfo *out) {
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess) return e;
+    if ((e = hipSetDevice(dev)) != hipSuccess) return e;
+    size_t fr = 0, tot = 0;
+    if ((e = hipMemGetInfo(&fr, &tot)) != hipSuccess) return e;
+    memset(out, 0, sizeof(*out));
+    {
+        const char *nm = p.name[0] ? p.name : p.gcnArchName;
+        memcpy(out->name, nm, std::min(strlen(nm), sizeof(out->name) - 1));
+    }
+    out->cc_major = p.major;
+    out->cc_minor = p.minor;
+    out->sm_count = p.multiProcessorCount;
+    out->total_mem = tot;
+    out->free_mem = fr;
+    out->pci_bus = p.pciBusID;
+    out->pci_device = p.pciDeviceID;
+    out->async_engines = p.asyncEngineCount;
+    out->can_map_host = p.canMapHostMemory;
+    return 0;
+}
+GS_EXPORT const char *gs_error_string(int e) { return hipGetErrorString((hipError_t)e); }
+GS_EXPORT int gs_malloc(void **p, size_t n) { return hipMalloc(p, n); }
+GS_EXPORT int gs_free(void *p) { return hipFree(p); }
+GS_EXPORT int gs_host_alloc(void **p, size_t n) { return hipHostMalloc(p, n, hipHostMallocDefault); }
+GS_EXPORT int gs_host_free(void *p) { return hipHostFree(p); }
+GS_EXPORT int gs_host_register(void *p, size_t n) { return hipHostRegister(p, n, hipHostRegisterDefault); }
+GS_EXPORT int gs_host_unregister(void *p) { return hipHostUnregister(p); }
+GS_EXPORT int gs_stream_create(void **s) { return hipStreamCreateWithFlags((hipStream_t *)s, hipStreamNonBlocking); }
+GS_EXPORT int gs_stream_destroy(void *s) { return hipStreamDestroy((hipStream_t)s); }
+GS_EXPORT int gs_stream_sync(void *s) { return hipStreamSynchronize((hipStream_t)s); }
+GS_EXPORT int gs_device_sync(void) { return hipDeviceSynchronize(); }
+GS_EXPORT int gs_device_reset(void) {
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        int dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            auto it = g_ctx.find(dev);
+            if (it != g_ctx.end()) {   // modules die with the context; forget them
+                delete it->second;
+                g_ctx.erase(it);
+            }
+        }
+    }
+    return hipDeviceReset();
+}
+GS_EXPORT int gs_memcpy_h2d(void *dst, const void *src, size_t n, void *s) {
+    return hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, (hipStream_t)s);
+}
+GS_EXPORT int gs_memcpy_d2h(void *dst, const void *src, size_t n, void *s) {
+    return hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, (hipStream_t)s);
+}
+GS_EXPORT int gs_memcpy_d2d(void *dst, const void *src, size_t n, void *s) {
+    return hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)s);
+}
+GS_EXPORT int gs_event_create(void **e) { return hipEventCreateWithFlags((hipEvent_t *)e, hipEventDisableTiming); }
+GS_EXPORT int gs_event_create_timed(void **e) { return hipEventCreate((hipEvent_t *)e); }
+GS_EXPORT int gs_event_destroy(void *e) { return hipEventDestroy((hipEvent_t)e); }
+GS_EXPORT int gs_event_record(void *e, void *s) { return hipEventRecord((hipEvent_t)e, (hipStream_t)s); }
+GS_EXPORT int gs_event_sync(void *e) { return hipEventSynchronize((hipEvent_t)e); }
+GS_EXPORT int gs_event_query(void *e) { return hipEventQuery((hipEvent_t)e); }
+GS_EXPORT int gs_stream_wait_event(void *s, void *e) { return hipStreamWaitEvent((hipStream_t)s, (hipEvent_t)e, 0); }
+GS_EXPORT int gs_event_elapsed_ms(float *ms, void *a, void *b) {
+    return hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b);
+}
+GS_EXPORT int gs_memset(void *p, int v, size_t n, void *s) { return hipMemsetAsync(p, v, n, (hipStream_t)s); }
+GS_EXPORT int gs_saxpy(int n, float a, const float *x, float *y, void *s) {
+    if (n <= 0) return 0;
+    EltArgs g{x, nullptr, y, n, a};
+    return launch("gs_k_saxpy", dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)s, g);
+}
+
+// =============================================================================================
+// dequantization (quants.cu:21-47)
+// =============================================================================================
+static int dequant(int ty, const void *src, int64_t n, void *dst, void *s, const char *suffix) {
+    int qk, bb;
+    if (n <= 0 || n % 8 != 0 || !geometry(ty, qk, bb) || n % ggml_block_elems(ty) != 0) return hipErrorInvalidValue;
+    DequantArgs a{(const uint8_t *)src, dst, n / 8};
+    const std::string name = std::string("gs_k_dequant_") + suffix + "_" + std::to_string(ty);
+    return launch(name, dim3((unsigned)((a.n_groups + 255) / 256)), dim3(256), 0, (hipStream_t)s, a);
+}
+GS_EXPORT int gs_dequant_f32(int ty, const void *src, int64_t n, float *dst, void *s) {
+    return dequant(ty, src, n, dst, s, "f32");
+}
+GS_EXPORT int gs_dequant_f16(int ty, const void *src, int64_t n, void *dst, void *s) {
+    return dequant(ty, src, n, dst, s, "f16");
+}
+
+GS_EXPORT int gs_quant_q8_1(const float *x, void *q, int64_t n, void *s) {
+    if (n <= 0 || n % 32 != 0) return hipErrorInvalidValue;
+    QuantArgs a{x, (uint8_t *)q, n / 32};
+    return launch("gs_k_quant_q8_1", dim3((unsigned)((a.n_blocks + 255) / 256)), dim3(256), 0, (hipStream_t)s, a);
+}
+
+// =============================================================================================
+// GEMV (quants.cu:223-256)
+// =============================================================================================
+static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
+                     float *y, int64_t y_stride, int B, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs,
+                     int64_t y_bs, void *s) {
+    int qk, bb;
+    if (!geometry(ty, qk, bb)) return hipErrorInvalidValue;
+    if (K <= 0 || K % 8 != 0 || K % ggml_block_elems(ty) != 0 || K % 32 != 0) return hipErrorInvalidValue;
+    if (B < 1 || B > 8 || rows < 0 || n_batch < 1) return hipErrorInvalidValue;
+    if (!check_w(W, row_stride) || (n_batch > 1 && (w_bs & 1))) return hipErrorInvalidValue;
+    if (rows == 0) return 0;
+    // split K so one lane's q8_1 activation units fit in registers: K <= 64 lanes x (8/NV) units x 32
+    const int NVt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
+    const int kmax_units = 64 * (8 / NVt);
+    const int step = std::max(qk, 32);
+    int kc = std::min(K, kmax_units * 32);
+    kc -= kc % step;
+    if (kc <= 0) return hipErrorInvalidValue;
+    const bool xal = aligned16(x) && (x_stride % 4 == 0) && (x_bs % 4 == 0);
+    for (int k0 = 0; k0 < K; k0 += kc) {
+        const int kk = std::min(kc, K - k0);
+        StreamArgs a;
+        memset(&a, 0, sizeof(a));
+        a.w0[0] = (const uint8_t *)W + (int64_t)k0 / qk * bb;
+        a.x = x + k0;
+        a.y = y;
+        a.row_stride = row_stride;
+        a.x_stride = x_stride;
+        a.y_stride = y_stride;
+        a.w_bs = w_bs;
+        a.x_bs = x_bs;
+        a.y_bs = y_bs;
+        a.K = kk;
+        a.rows = rows;
+        a.nvec = B;
+        a.nseg = 1;
+        a.accumulate = (k0 > 0) ? 1 : accumulate;
+        a.x_aligned = xal && ((k0 * 4) % 16 == 0);
+        if (kk != K) a.row_stride = row_stride;  // sub-row spans: contig is false, one row per tile
+        hipError_t e = stream(0, ty, a, (hipStream_t)s, n_batch);
+        if (e != hipSuccess) return e;
+    }
+    return 0;
+}
+
+GS_EXPORT int gs_gemv(int ty, const void *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
+                      float *y, int64_t y_stride, int B, int accumulate, void *s) {
+    return gemv_impl(ty, W, row_stride, K, rows, x, x_stride, y, y_stride, B, accumulate, 1, 0, 0, 0, s);
+}
+
+GS_EXPORT int gs_gemv_batched(int ty, const void *W, int64_t row_stride, int K, int rows, const float *x, float *y,
+                              int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs, void *s) {
+    return gemv_impl(ty, W, row_stride, K, rows, x, 0, y, 0, 1, 0, n_batch, w_bs, x_bs, y_bs, s);
+}
+
+// =============================================================================================
+// fused routed-expert FFN (quants.cu:378-409)
+// =============================================================================================
+static int moe_check(int ty, const GsMoeBatch *b, int nt, int K, int rows, int64_t row_stride) {
+    int qk, bb;
+    if (!b || b->n <= 0 || b->n > GS_MOE_MAX || nt < 1 || nt > GS_MOE_NT) return hipErrorInvalidValue;
+    if (K <= 0 || rows <= 0 || K % 8 != 0 || K % 32 != 0) return hipErrorInvalidValue;
+    if (!geometry(ty, qk, bb) || K % ggml_block_elems(ty) != 0 || (row_stride & 1)) return hipErrorInvalidValue;
+    return 0;
+}
+
+GS_EXPORT int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *x,
+                            float *h, float lim, void *s) {
+    int rc = moe_check(ty, b, nt, K, rows, row_stride);
+    if (rc) return rc;
+    StreamArgs a;
+    memset(&a, 0, sizeof(a));
+    for (int e = 0; e < b->n; e++) {
+        if (((uintptr_t)b->gate[e] | (uintptr_t)b->up[e]) & 1) return hipErrorInvalidValue;
+        a.w0[e] = b->gate[e];
+        a.w1[e] = b->up[e];
+    }
+    a.x = x;
+    a.y = h;
+    a.row_stride = row_stride;
+    a.x_stride = K;
+    a.K = K;
+    a.rows = rows;
+    a.nvec = nt;
+    a.nseg = b->n;
+    a.lim = lim;
+    a.x_aligned = aligned16(x) && K % 4 == 0;
+    return stream(1, ty, a, (hipStream_t)s);
+}
+
+GS_EXPORT int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *h,
+                          float *y, void *s) {
+    int rc = moe_check(ty, b, nt, K, rows, row_stride);
+    if (rc) return rc;
+    // one launch covers as many experts as fit one lane's register budget (64 lanes x 8/NV units)
+    const int NVt = nt <= 1 ? 1 : 2;
+    const int per = std::max(1, 64 * (8 / NVt) / (K / 32));
+    for (int e0 = 0; e0 < b->n; e0 += per) {
+        const int n = std::min(per, b->n - e0);
+        StreamArgs a;
+        memset(&a, 0, sizeof(a));
+        for (int e = 0; e < n; e++) {
+            if ((uintptr_t)b->down[e0 + e] & 1) return hipErrorInvalidValue;
+            a.w0[e] = b->down[e0 + e];
+            for (int t = 0; t < nt; t++) a.wt[t][e] = b->w[t][e0 + e];
+        }
+        a.x = h + (int64_t)e0 * nt * K;
+        a.y = y;
+        a.row_stride = row_stride;
+        a.y_stride = rows;
+        a.K = K;
+        a.rows = rows;
+        a.nvec = nt;
+        a.nseg = n;
+        a.x_aligned = aligned16(a.x) && K % 4 == 0;
+        hipError_t e = stream(2, ty, a, (hipStream_t)s);
+        if (e != hipSuccess) return e;
+    }
+    return 0;
+}
+
+// =============================================================================================
+// GEMM (gemm.cu:107-123): token batches of 8 through the streaming kernel
+// =============================================================================================
+GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride,
+                      float *Y, int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs,
+                      int64_t y_bs, void *s) {
+    if (K % 32 != 0 || N < 1 || n_batch < 1 || x_stride % 4 != 0) return hipErrorInvalidValue;
+    int qk, bb;
+    if (!geometry(ty, qk, bb) || K % ggml_block_elems(ty) != 0) return hipErrorInvalidValue;
+    for (int z = 0; z < n_batch; z++) {
+        for (int n0 = 0; n0 < N; n0 += 8) {
+            const int nb = std::min(8, N - n0);
+            int rc = gemv_impl(ty, (const uint8_t *)W + z * w_bs, row_stride, K, rows, X + z * x_bs + n0 * x_stride,
+                               x_stride, Y + z * y_bs + n0 * y_stride, y_stride, nb, accumulate, 1, 0, 0, 0, s);
+            if (rc) return rc;
+        }
+    }
+    return 0;
+}
+
+// =============================================================================================
+// element-wise / row glue (ops.cu:101-125; gemm.cu:125-163)
+// =============================================================================================
+GS_EXPORT int gs_swiglu(const float *g, const float *u, float *y, int64_t n, float lim, void *s) {
+    if (n <= 0) return 0;
+    EltArgs a{g, u, y, n, lim};
+    return launch("gs_k_swiglu", dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s, a);
+}
+GS_EXPORT int gs_axpy(float *y, const float *x, float alpha, int64_t n, void *s) {
+    if (n <= 0) return 0;
+    EltArgs a{x, nullptr, y, n, alpha};
+    return launch("gs_k_axpy", dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s, a);
+}
+GS_EXPORT int gs_f32_to_f16(const float *x, void *y, int64_t n, void *s) {
+    if (n <= 0) return 0;
+    EltArgs a{x, nullptr, (float *)y, n, 0.f};
+    return launch("gs_k_f32_to_f16", dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s, a);
+}
+GS_EXPORT int gs_gather_rows(const float *x, const int *idx, float *y, int rows, int n, void *s) {
+    if (rows <= 0) return 0;
+    if (n <= 0) return hipErrorInvalidValue;
+    RowsArgs a{x, idx, nullptr, y, rows, n};
+    return launch("gs_k_gather_rows", dim3((n + 255) / 256, rows), dim3(256), 0, (hipStream_t)s, a);
+}
+GS_EXPORT int gs_scatter_add_rows(float *acc, const int *idx, const float *w, const float *y, int rows, int n, void *s) {
+    if (rows <= 0) return 0;
+    if (n <= 0) return hipErrorInvalidValue;
+    RowsArgs a{y, idx, w, acc, rows, n};
+    return launch("gs_k_scatter_add_rows", dim3((n + 255) / 256, rows), dim3(256), 0, (hipStream_t)s, a);
+}

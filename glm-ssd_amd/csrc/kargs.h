@@ -1,0 +1,81 @@
+// Kernel argument blocks shared by the host launcher (host.cpp) and the gfx950 kernels
+// (kernels.hip). Plain C layout: each kernel takes exactly one of these by value, so the
+// host packs it once and hands its address to hipModuleLaunchKernel.
+#pragma once
+#include <stdint.h>
+
+// ggml type ids (crates/gguf/src/types.rs:74-82)
+enum GsType {
+    GS_F32 = 0, GS_F16 = 1, GS_Q8_0 = 8, GS_Q2_K = 10, GS_Q3_K = 11, GS_Q4_K = 12, GS_Q5_K = 13,
+    GS_Q6_K = 14, GS_IQ2_XXS = 16, GS_IQ3_XXS = 18, GS_IQ2_S = 22, GS_IQ4_XS = 23, GS_BF16 = 30,
+};
+
+#define GS_WG 256          // threads per workgroup of the streaming kernels (4 wave64)
+#define GS_SEG_MAX 32      // weight matrices (experts) per fused-MoE launch
+#define GS_NT_MAX 8        // activation vectors (tokens) per launch
+#define GS_LD_MAX 12       // 16-byte loads per thread per weight tile (tile <= 48 KiB)
+
+// Matrix-vector work description ("stream" kernels). One launch streams the rows of one or
+// more quantized matrices ("segments") through LDS in tiles of `rt` rows.
+//   kind 0 (GEMV):   y[b][r] (+)= W[r] . xq[b]                      seg = 1 (blockIdx.y batches)
+//   kind 1 (GATEUP): h[e][t][r] = swiglu(gate_e[r] . xq[t], up_e[r] . xq[t])
+//   kind 2 (DOWN):   y[t][r] += sum_e w[t][e] * (down_e[r] . hq[e][t])
+struct StreamArgs {
+    const uint8_t *w0[GS_SEG_MAX];   // GEMV: w0[0]; GATEUP: gate; DOWN: down
+    const uint8_t *w1[GS_SEG_MAX];   // GATEUP: up
+    float wt[GS_NT_MAX][GS_SEG_MAX]; // DOWN: combine weights (0 = token not routed)
+    const float *x;                  // activations (f32; quantized to q8_1 in the prologue)
+    float *y;                        // output
+    int64_t row_stride;              // bytes between rows
+    int64_t x_stride;                // floats between activation vectors
+    int64_t y_stride;                // floats between output vectors
+    int64_t w_bs, x_bs, y_bs;        // GEMV batch strides (bytes / floats / floats) per blockIdx.y
+    int K;                           // row length (elements)
+    int rows;                        // rows per matrix
+    int nvec;                        // activation vectors (B or tokens)
+    int nseg;                        // segments (experts) in this launch
+    int accumulate;                  // GEMV only: y += result
+    float lim;                       // SwiGLU clamp (<= 0: none)
+    int row_bytes;                   // bytes of one row's data
+    int nu;                          // q8_1 units (32 elements) per row = K/32
+    int lpr;                         // lanes per row (16, 32 or 64)
+    int upl;                         // units per lane = ceil(nu/lpr)
+    int rt;                          // rows per tile
+    int n_row_tiles;                 // ceil(rows/rt)
+    int n_tiles;                     // total tiles (GATEUP: nseg * n_row_tiles)
+    int contig;                      // rows of a tile are one contiguous span (row_stride == row_bytes)
+    int x_aligned;                   // x and x_stride allow 16-byte loads
+    int lds_tile;                    // bytes reserved for one tile (per segment span: span_pitch)
+    int span_pitch;                  // LDS bytes between segment spans of a tile
+};
+
+// Whole-tensor dequantization
+struct DequantArgs {
+    const uint8_t *src;
+    void *dst;
+    int64_t n_groups;   // 8-element groups
+};
+
+// q8_1 quantization of f32 rows: out = n/32 blocks of {f16 d; f16 s; int8 qs[32]}
+struct QuantArgs {
+    const float *x;
+    uint8_t *out;
+    int64_t n_blocks;
+};
+
+struct EltArgs {
+    const float *a;
+    const float *b;
+    float *y;
+    int64_t n;
+    float s;       // lim (swiglu) or alpha (axpy)
+};
+
+struct RowsArgs {
+    const float *x;
+    const int *idx;
+    const float *w;
+    float *y;
+    int rows;
+    int n;
+};

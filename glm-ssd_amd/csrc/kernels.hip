@@ -1,0 +1,388 @@
+// gfx950 kernels of the quantized-matmul hot path. Compiled to one code object
+// (hipcc --genco --offload-arch=gfx950) that host.cpp loads with hipModuleLoadData; every
+// kernel is extern "C" with a fixed name and takes one argument block from kargs.h by value.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "kargs.h"
+#include "formats.h"
+
+// =============================================================================================
+// q8_1 activation quantization of one 32-element unit, in registers.
+//   d = amax/127 (correctly rounded), id = d ? 1/d : 0, q = roundf(x*id) (half away from zero),
+//   stored scale D = f16(d) read back as f32; s = f16(d * sum q) for the ggml block layout.
+// =============================================================================================
+struct Q81 {
+    uint32_t q[8];
+    float d;       // unrounded f32 scale
+    int slo, shi;
+};
+
+__device__ __forceinline__ Q81 quant_unit(const float (&v)[32]) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    Q81 r;
+    r.d = amax / 127.0f;
+    const float id = r.d != 0.f ? 1.0f / r.d : 0.f;
+    r.slo = r.shi = 0;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float p = v[4 * w + b] * id;
+            const int q = (int)__builtin_roundf(p);
+            word |= ((uint32_t)q & 0xffu) << (8 * b);
+            if (w < 4) r.slo += q; else r.shi += q;
+        }
+        r.q[w] = word;
+    }
+    return r;
+}
+
+__device__ __forceinline__ void load32(const float *src, bool aligned, float (&v)[32]) {
+    if (aligned) {
+        const float4 *p = (const float4 *)src;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 f = p[i];
+            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = src[i];
+    }
+}
+
+// =============================================================================================
+// Cross-lane sum over groups of 16/32/64 lanes with DPP; the group's last lane ends with the total.
+// =============================================================================================
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_plus(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xF, false));
+}
+__device__ __forceinline__ float group_sum(float v, int lpr) {
+    v = dpp_plus<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_plus<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v = dpp_plus<0x141, 0xF>(v);  // row_half_mirror
+    v = dpp_plus<0x140, 0xF>(v);  // row_mirror: every lane of a 16-lane row holds the row sum
+    if (lpr >= 32) v = dpp_plus<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
+    if (lpr >= 64) v = dpp_plus<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
+__device__ __forceinline__ float swiglu(float g, float u, float lim) { // ops.cu:101-115
+    if (lim > 0.f) {
+        g = fminf(g, lim);
+        u = fminf(fmaxf(u, -lim), lim);
+    }
+    return g / (1.f + expf(-g)) * u;
+}
+
+// =============================================================================================
+// Streaming matrix-vector kernel (GEMV / fused MoE gate-up / fused MoE down).
+//
+// Work is cut into tiles of `rt` rows. Per tile each segment (matrix) contributes one span of
+// bytes; spans are copied HBM -> VGPR -> LDS with aligned 16-byte loads (whatever the block
+// alignment), the next tile's loads are issued before the current tile is decoded, so one tile
+// per workgroup is always in flight. Lanes are split into groups of `lpr` lanes; a group owns a
+// row of the tile at a time and each lane owns the same `upl` 32-element units of every row,
+// so its q8_1 activation units stay in registers for the whole launch. Row partials are summed
+// across the group with DPP.
+// =============================================================================================
+template <class F, int KIND, int NV, int UMAX>
+__device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t cps_magic, int cps) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x;
+    uint8_t *tab = smem;
+    uint8_t *work = smem + ((F::TAB + 15) & ~15);
+    F::init(tab, tid);
+
+    const uint8_t *wb = a.w0[0];
+    const float *x = a.x;
+    float *y = a.y;
+    if (KIND == 0) {
+        wb += (int64_t)blockIdx.y * a.w_bs;
+        x += (int64_t)blockIdx.y * a.x_bs;
+        y += (int64_t)blockIdx.y * a.y_bs;
+    }
+    const int K = a.K, nu = a.nu, nv = a.nvec;
+    const int NS = KIND == 0 ? 1 : (KIND == 1 ? 2 : a.nseg);
+    const int nxv = KIND == 2 ? a.nseg * nv : nv;
+
+    // ---- prologue: q8_1-quantize every activation vector into LDS ----------------------------
+    uint8_t *xq = work;
+    uint32_t *xm = (uint32_t *)(work + (size_t)nxv * K);
+    for (int i = tid; i < nxv * nu; i += GS_WG) {
+        const int v = i / nu, u = i - v * nu;
+        const float *src = (KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u;
+        float f[32];
+        load32(src, a.x_aligned != 0, f);
+        const Q81 q = quant_unit(f);
+        uint4 *dst = (uint4 *)(xq + (size_t)v * K + 32 * u);
+        dst[0] = make_uint4(q.q[0], q.q[1], q.q[2], q.q[3]);
+        dst[1] = make_uint4(q.q[4], q.q[5], q.q[6], q.q[7]);
+        xm[2 * i] = __builtin_bit_cast(uint32_t, h2f(f2h(q.d)));
+        xm[2 * i + 1] = ((uint32_t)q.slo & 0xffffu) | ((uint32_t)q.shi << 16);
+    }
+    __syncthreads();
+
+    const int lpr = a.lpr, lane = tid & (lpr - 1), grp = tid / lpr, G = GS_WG / lpr;
+    const int tot = NS * nu;
+    XU xr[UMAX][NV];
+    int uspan[UMAX], usub[UMAX];
+    uint32_t uoff[UMAX];
+    bool uval[UMAX];
+#pragma unroll
+    for (int j = 0; j < UMAX; j++) {
+        const int u = lane + lpr * j;
+        const bool valid = j < a.upl && u < tot;
+        const int s = valid ? u / nu : 0, up = valid ? u - s * nu : 0;
+        uval[j] = valid;
+        uspan[j] = s;
+        uoff[j] = F::off(up);
+        usub[j] = F::sub(up);
+#pragma unroll
+        for (int t = 0; t < NV; t++) {
+            const int v = KIND == 2 ? s * nv + t : t;
+            XU z;
+            if (valid && t < nv) {
+                const uint4 *src = (const uint4 *)(xq + (size_t)v * K + 32 * up);
+                const uint4 lo = src[0], hi = src[1];
+                z.q[0] = lo.x; z.q[1] = lo.y; z.q[2] = lo.z; z.q[3] = lo.w;
+                z.q[4] = hi.x; z.q[5] = hi.y; z.q[6] = hi.z; z.q[7] = hi.w;
+                const int mi = v * nu + up;
+                z.D = __builtin_bit_cast(float, xm[2 * mi]);
+                const uint32_t ss = xm[2 * mi + 1];
+                z.slo = (int)(int16_t)(ss & 0xffff);
+                z.shi = (int)(int16_t)(ss >> 16);
+                if (KIND == 2) {
+                    const float w = a.wt[t][s];
+                    if (w == 0.f) {
+                        z.D = 0.f;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) z.q[i] = 0;
+                        z.slo = z.shi = 0;
+                    } else {
+                        z.D *= w;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) z.q[i] = 0;
+                z.D = 0.f;
+                z.slo = z.shi = 0;
+            }
+            xr[j][t] = z;
+        }
+    }
+    __syncthreads();   // the tile buffer below reuses the activation area
+
+    // ---- tile loop ---------------------------------------------------------------------------
+    const int rbytes = a.row_bytes, pitch = a.span_pitch;
+    const int nchunks = NS * cps;
+    auto span_base = [&](int tile, int s, int &r0, int &nr) -> const uint8_t * {
+        int e = 0, rtile = tile;
+        if (KIND == 1) {
+            e = tile / a.n_row_tiles;
+            rtile = tile - e * a.n_row_tiles;
+        }
+        r0 = rtile * a.rt;
+        nr = min(a.rt, a.rows - r0);
+        const uint8_t *b = KIND == 0 ? wb : (KIND == 1 ? (s == 0 ? a.w0[e] : a.w1[e]) : a.w0[s]);
+        return b + (int64_t)r0 * a.row_stride;
+    };
+    uint4 buf[GS_LD_MAX];
+    auto load_tile = [&](int tile) {
+#pragma unroll
+        for (int k = 0; k < GS_LD_MAX; k++) {
+            const int i = tid + GS_WG * k;
+            if (i < nchunks) {
+                const int s = (int)__umulhi((uint32_t)i, cps_magic);
+                const int c = i - s * cps;
+                int r0, nr;
+                const uint8_t *p = span_base(tile, s, r0, nr);
+                const uintptr_t pa = (uintptr_t)p & ~(uintptr_t)15;
+                const int nch = (int)((((uintptr_t)p & 15) + (uintptr_t)nr * rbytes + 15) >> 4);
+                if (c < nch) buf[k] = *(const uint4 *)(pa + 16 * (uintptr_t)c);
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int k = 0; k < GS_LD_MAX; k++) {
+            const int i = tid + GS_WG * k;
+            if (i < nchunks) {
+                const int s = (int)__umulhi((uint32_t)i, cps_magic);
+                const int c = i - s * cps;
+                *(uint4 *)(work + s * pitch + 16 * c) = buf[k];
+            }
+        }
+    };
+
+    int tile = blockIdx.x;
+    if (tile < a.n_tiles) load_tile(tile);
+    for (; tile < a.n_tiles; tile += gridDim.x) {
+        store_tile();
+        __syncthreads();
+        const int next = tile + gridDim.x;
+        if (next < a.n_tiles) load_tile(next);
+
+        int r0 = 0, nr = 0, e = 0;
+        if (KIND == 1) e = tile / a.n_row_tiles;
+        uint32_t ubase[UMAX];
+#pragma unroll
+        for (int j = 0; j < UMAX; j++) {
+            const uint8_t *p = span_base(tile, uspan[j], r0, nr);
+            ubase[j] = (uint32_t)(uspan[j] * pitch) + (uint32_t)((uintptr_t)p & 15) + uoff[j];
+        }
+        for (int i = grp; i < nr; i += G) {
+            float acc0[NV], acc1[NV];
+#pragma unroll
+            for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
+#pragma unroll
+            for (int j = 0; j < UMAX; j++) {
+                if (uval[j]) {
+                    float r[NV];
+#pragma unroll
+                    for (int t = 0; t < NV; t++) r[t] = 0.f;
+                    F::template dot<NV>(work, ubase[j] + (uint32_t)(i * rbytes), usub[j], tab, xr[j], nv, r);
+#pragma unroll
+                    for (int t = 0; t < NV; t++) {
+                        if (KIND == 1 && uspan[j] == 1) acc1[t] += r[t];
+                        else acc0[t] += r[t];
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NV; t++) {
+                acc0[t] = group_sum(acc0[t], lpr);
+                if (KIND == 1) acc1[t] = group_sum(acc1[t], lpr);
+            }
+            if (lane == lpr - 1) {
+                const int row = r0 + i;
+#pragma unroll
+                for (int t = 0; t < NV; t++) {
+                    if (t < nv) {
+                        if (KIND == 0) {
+                            float *dst = y + (int64_t)t * a.y_stride + row;
+                            *dst = a.accumulate ? *dst + acc0[t] : acc0[t];
+                        } else if (KIND == 1) {
+                            y[((int64_t)e * nv + t) * a.rows + row] = swiglu(acc0[t], acc1[t], a.lim);
+                        } else {
+                            y[(int64_t)t * a.y_stride + row] += acc0[t];
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// cps (max 16-byte chunks per span) and its division magic ride in the dynamic part of the
+// launch: they are appended after StreamArgs by the host.
+struct StreamLaunch {
+    StreamArgs a;
+    uint32_t cps_magic;
+    int cps;
+};
+
+#define GS_STREAM_KERNEL(F, NAME, KIND, NV)                                                      \
+    extern "C" __global__ void __launch_bounds__(GS_WG) gs_k_stream_##NAME##_##KIND##_##NV(StreamLaunch L) { \
+        stream_body<F, KIND, NV, 8 / NV>(L.a, L.cps_magic, L.cps);                              \
+    }
+#define GS_STREAM_NV(F, NAME, KIND)                                                             \
+    GS_STREAM_KERNEL(F, NAME, KIND, 1) GS_STREAM_KERNEL(F, NAME, KIND, 2)                       \
+    GS_STREAM_KERNEL(F, NAME, KIND, 4) GS_STREAM_KERNEL(F, NAME, KIND, 8)
+#define GS_STREAM_ALL(F, NAME) GS_STREAM_NV(F, NAME, 0) GS_STREAM_NV(F, NAME, 1) GS_STREAM_NV(F, NAME, 2)
+
+// One code object per format keeps the build parallel: the Makefile compiles this file once
+// per GS_STREAM_TYPE (F-struct, type id) and once with GS_COMMON for the kernels below.
+#if defined(GS_STREAM_F)
+GS_STREAM_ALL(GS_STREAM_F, GS_STREAM_ID)
+#endif
+
+#if defined(GS_COMMON)
+
+// =============================================================================================
+// Whole-tensor dequantization (gs_dequant_f32 / gs_dequant_f16): one thread per 8 elements.
+// =============================================================================================
+#define GS_DEQ_KERNEL(TY, QK, BB, DEQ)                                                           \
+    extern "C" __global__ void __launch_bounds__(256) gs_k_dequant_f32_##TY(DequantArgs a) {    \
+        const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;                        \
+        if (g >= a.n_groups) return;                                                            \
+        constexpr int GPB = QK / 8;                                                             \
+        float v[8];                                                                             \
+        DEQ(a.src + (g / GPB) * BB, (int)(g % GPB), v);                                         \
+        float4 *d = (float4 *)((float *)a.dst + g * 8);                                         \
+        d[0] = make_float4(v[0], v[1], v[2], v[3]);                                             \
+        d[1] = make_float4(v[4], v[5], v[6], v[7]);                                             \
+    }                                                                                           \
+    extern "C" __global__ void __launch_bounds__(256) gs_k_dequant_f16_##TY(DequantArgs a) {    \
+        const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;                        \
+        if (g >= a.n_groups) return;                                                            \
+        constexpr int GPB = QK / 8;                                                             \
+        float v[8];                                                                             \
+        DEQ(a.src + (g / GPB) * BB, (int)(g % GPB), v);                                         \
+        uint4 o;                                                                                \
+        o.x = f2h(v[0]) | (f2h(v[1]) << 16);                                                    \
+        o.y = f2h(v[2]) | (f2h(v[3]) << 16);                                                    \
+        o.z = f2h(v[4]) | (f2h(v[5]) << 16);                                                    \
+        o.w = f2h(v[6]) | (f2h(v[7]) << 16);                                                    \
+        *(uint4 *)((uint16_t *)a.dst + g * 8) = o;                                              \
+    }
+GS_TYPE_LIST(GS_DEQ_KERNEL)
+
+// =============================================================================================
+// q8_1 quantization to the ggml block layout {f16 d; f16 s; int8 qs[32]} (gs_quant_q8_1)
+// =============================================================================================
+extern "C" __global__ void __launch_bounds__(256) gs_k_quant_q8_1(QuantArgs a) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= a.n_blocks) return;
+    float v[32];
+    load32(a.x + 32 * b, false, v);
+    const Q81 q = quant_unit(v);
+    uint8_t *o = a.out + 36 * b;
+    const uint32_t hd = f2h(q.d), hs = f2h((float)(q.slo + q.shi) * q.d);
+    uint32_t *ow = (uint32_t *)o;   // 36-byte blocks are 4-byte aligned
+    ow[0] = hd | (hs << 16);
+#pragma unroll
+    for (int i = 0; i < 8; i++) ow[1 + i] = q.q[i];
+}
+
+// =============================================================================================
+// Element-wise and row kernels of the MoE glue (ops.cu:101-125, gemm.cu:125-163)
+// =============================================================================================
+extern "C" __global__ void __launch_bounds__(256) gs_k_swiglu(EltArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.n) a.y[i] = swiglu(a.a[i], a.b[i], a.s);
+}
+extern "C" __global__ void __launch_bounds__(256) gs_k_axpy(EltArgs a) {   // y += s * x
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.n) a.y[i] += a.s * a.a[i];
+}
+extern "C" __global__ void __launch_bounds__(256) gs_k_f32_to_f16(EltArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.n) ((uint16_t *)a.y)[i] = (uint16_t)f2h(a.a[i]);
+}
+extern "C" __global__ void __launch_bounds__(256) gs_k_saxpy(EltArgs a) {  // y = s*x + y
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.n) a.y[i] = a.s * a.a[i] + a.y[i];
+}
+// y[i][:] = x[idx[i]][:]
+extern "C" __global__ void __launch_bounds__(256) gs_k_gather_rows(RowsArgs a) {
+    const int i = blockIdx.y;
+    const float *src = a.x + (int64_t)a.idx[i] * a.n;
+    float *dst = a.y + (int64_t)i * a.n;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < a.n; c += gridDim.x * blockDim.x) dst[c] = src[c];
+}
+// acc[idx[i]][:] += w[i] * y[i][:]  (idx unique within one call); acc passed as .y, rows as .x
+extern "C" __global__ void __launch_bounds__(256) gs_k_scatter_add_rows(RowsArgs a) {
+    const int i = blockIdx.y;
+    float *dst = a.y + (int64_t)a.idx[i] * a.n;
+    const float *src = a.x + (int64_t)i * a.n;
+    const float s = a.w[i];
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < a.n; c += gridDim.x * blockDim.x) dst[c] += s * src[c];
+}
+#endif  // GS_COMMON

@@ -1,0 +1,135 @@
+/* glmssd.h — C ABI of libglmssd_hip.so, the MI355X (gfx950) drop-in for GLM-SSD's quantized
+ * matmul hot path.
+ *
+ * Every symbol below keeps the name, signature, argument meaning and error behaviour of the
+ * entry point the GLM-SSD engine binds in crates/cuda/src/lib.rs (the `extern "C"` block at
+ * lib.rs:24-124); each declaration cites it. Return value: 0 on success, else a HIP error code
+ * (hipErrorInvalidValue == 1 for bad arguments, as cudaErrorInvalidValue is in the reference;
+ * crates/cuda/kernels/common.cuh:6-14). Pointers are device pointers unless noted; `stream` is a
+ * hipStream_t (NULL = default stream). Calls are asynchronous on `stream`.
+ *
+ * Activations entering a quantized matmul are quantized to q8_1 inside the kernels (blocks of
+ * 32: f16 scale d = amax/127, int8 q = round(x/d)); the f32 activation ABI is unchanged.
+ * Constraints beyond the reference's: K % 32 == 0 for the matmul entry points, weight rows
+ * 2-byte aligned (every ggml tensor is).
+ */
+#ifndef GLMSSD_H
+#define GLMSSD_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (crates/gguf/src/types.rs:74-82) */
+enum {
+    GS_TYPE_F32 = 0, GS_TYPE_F16 = 1, GS_TYPE_Q8_0 = 8, GS_TYPE_Q2_K = 10, GS_TYPE_Q3_K = 11, GS_TYPE_Q4_K = 12,
+    GS_TYPE_Q5_K = 13, GS_TYPE_Q6_K = 14, GS_TYPE_IQ2_XXS = 16, GS_TYPE_IQ3_XXS = 18, GS_TYPE_IQ2_S = 22,
+    GS_TYPE_IQ4_XS = 23, GS_TYPE_BF16 = 30,
+};
+
+#define GS_MOE_MAX 16 /* experts per fused batch  (crates/cuda/src/lib.rs:411) */
+#define GS_MOE_NT 2   /* tokens per fused batch   (crates/cuda/src/lib.rs:413) */
+
+/* Fused-MoE batch, passed by pointer and copied by value into the kernel arguments
+ * (crates/cuda/src/lib.rs:417-429 == crates/cuda/kernels/quants.cu:265-273). w[t][e] == 0 marks
+ * token t as not routed to expert e. 516 bytes. */
+typedef struct GsMoeBatch {
+    const uint8_t *gate[GS_MOE_MAX];
+    const uint8_t *up[GS_MOE_MAX];
+    const uint8_t *down[GS_MOE_MAX];
+    float w[GS_MOE_NT][GS_MOE_MAX];
+    int n;
+} GsMoeBatch;
+
+/* crates/cuda/src/lib.rs:11-22 (runtime.cu:6-14) */
+typedef struct GsDeviceInfo {
+    char name[256];
+    int cc_major, cc_minor;
+    int sm_count; /* compute units */
+    uint64_t total_mem, free_mem;
+    int pci_bus, pci_device;
+    int async_engines;
+    int can_map_host;
+} GsDeviceInfo;
+
+/* ---- runtime (crates/cuda/src/lib.rs:25-51; crates/cuda/kernels/runtime.cu:16-91) ---------- */
+int gs_device_info(int dev, GsDeviceInfo *out);              /* lib.rs:25 */
+const char *gs_error_string(int e);                          /* lib.rs:26 */
+int gs_malloc(void **p, size_t n);                           /* lib.rs:27 */
+int gs_free(void *p);                                        /* lib.rs:28 */
+int gs_host_alloc(void **p, size_t n);                       /* lib.rs:29 */
+int gs_host_free(void *p);                                   /* lib.rs:30 */
+int gs_host_register(void *p, size_t n);                     /* lib.rs:31 */
+int gs_host_unregister(void *p);                             /* lib.rs:32 */
+int gs_stream_create(void **s);                              /* lib.rs:33 */
+int gs_stream_destroy(void *s);                              /* lib.rs:34 */
+int gs_stream_sync(void *s);                                 /* lib.rs:35 */
+int gs_device_sync(void);                                    /* lib.rs:36 */
+int gs_device_reset(void);                                   /* lib.rs:37 */
+int gs_memcpy_h2d(void *dst, const void *src, size_t n, void *s); /* lib.rs:38 */
+int gs_memcpy_d2h(void *dst, const void *src, size_t n, void *s); /* lib.rs:39 */
+int gs_memcpy_d2d(void *dst, const void *src, size_t n, void *s); /* lib.rs:40 */
+int gs_event_create(void **e);                               /* lib.rs:41 */
+int gs_event_create_timed(void **e);                         /* lib.rs:42 */
+int gs_event_destroy(void *e);                               /* lib.rs:43 */
+int gs_event_record(void *e, void *s);                       /* lib.rs:44 */
+int gs_event_sync(void *e);                                  /* lib.rs:45 */
+int gs_event_query(void *e);                                 /* lib.rs:46 */
+int gs_stream_wait_event(void *s, void *e);                  /* lib.rs:47 */
+int gs_event_elapsed_ms(float *ms, void *a, void *b);        /* lib.rs:48 */
+int gs_memset(void *p, int v, size_t n, void *s);            /* lib.rs:49 */
+int gs_saxpy(int n, float a, const float *x, float *y, void *s); /* lib.rs:50 */
+
+/* ---- quantized ops (crates/cuda/src/lib.rs:52-69; kernels/quants.cu) ---------------------- */
+/* dequantize n elements (a whole number of blocks) to f32 / f16, bit-exact with crates/quants
+ * (lib.rs:52; quants.cu:21-47) */
+int gs_dequant_f32(int ty, const void *src, int64_t n, float *dst, void *s);
+int gs_dequant_f16(int ty, const void *src, int64_t n, void *dst, void *s); /* lib.rs:53 */
+
+/* y[b*y_stride + r] (+)= W[r] . x[b*x_stride + :], b < B (1..8); W: rows rows of K elements,
+ * row_stride bytes apart (lib.rs:54-57; quants.cu:223-243) */
+int gs_gemv(int ty, const void *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride, float *y,
+            int64_t y_stride, int B, int accumulate, void *s);
+
+/* n_batch independent GEMVs: matrix b at W + b*w_bs bytes, x + b*x_bs, y + b*y_bs floats
+ * (lib.rs:58-61; quants.cu:246-256) */
+int gs_gemv_batched(int ty, const void *W, int64_t row_stride, int K, int rows, const float *x, float *y, int n_batch,
+                    int64_t w_bs, int64_t x_bs, int64_t y_bs, void *s);
+
+/* fused routed-expert gate/up + SwiGLU: h[e][t][r] = swiglu(gate_e[r].x[t], up_e[r].x[t]);
+ * x [nt][K], h [b->n][nt][rows] (lib.rs:62-65; quants.cu:378-393) */
+int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *x, float *h,
+                  float lim, void *s);
+
+/* fused routed-expert down + weighted combine: y[t][r] += sum_e w[t][e] * down_e[r].h[e][t]
+ * (always accumulates; lib.rs:66-69; quants.cu:394-409) */
+int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *h, float *y,
+                void *s);
+
+/* ---- GEMM and MoE glue (crates/cuda/src/lib.rs:71-74,115-122; kernels/gemm.cu, ops.cu) ---- */
+/* SwiGLU with clamp: y = silu(min(g,L)) * clamp(u,-L,L); L <= 0: no clamp (lib.rs:76; ops.cu:101-115) */
+int gs_swiglu(const float *g, const float *u, float *y, int64_t n, float lim, void *s);
+/* y += a*x (lib.rs:77; ops.cu:117-125) */
+int gs_axpy(float *y, const float *x, float a, int64_t n, void *s);
+/* Y[n*y_stride + m] (+)= W[m] . X[n*x_stride + :], n < N tokens; z-batched (lib.rs:115-118; gemm.cu:107-123) */
+int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
+            int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs, void *s);
+/* y[i][:] = x[idx[i]][:] (lib.rs:119; gemm.cu:125-138) */
+int gs_gather_rows(const float *x, const int *idx, float *y, int rows, int n, void *s);
+/* acc[idx[i]][:] += w[i] * y[i][:], idx unique within a call (lib.rs:120-122; gemm.cu:139-152) */
+int gs_scatter_add_rows(float *acc, const int *idx, const float *w, const float *y, int rows, int n, void *s);
+/* f32 -> f16 (lib.rs:123; gemm.cu:155-163) */
+int gs_f32_to_f16(const float *x, void *y, int64_t n, void *s);
+
+/* ---- additive entry points (no counterpart in the reference) ------------------------------ */
+/* q8_1 quantization of n f32 values (n % 32 == 0) to ggml block_q8_1 {f16 d; f16 s; int8 qs[32]}
+ * (36 bytes per 32). The same quantizer the matmul kernels apply to their activations; exposed
+ * for bit-exact testing. */
+int gs_quant_q8_1(const float *x, void *q, int64_t n, void *s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

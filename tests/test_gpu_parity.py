@@ -1,0 +1,221 @@
+"""GPU parity: the HIP library (called through its C ABI) against the CPU oracle on identical
+seeded inputs. Integer/byte work (dequantization, q8_1) must be bit-exact; matmul outputs must be
+within rel-L2 <= 1e-3 of the oracle's f64 result (per type)."""
+import sys
+
+import numpy as np
+import pytest
+
+import glmssd as G
+from glmssd import GgmlType as T
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+REL_L2 = 1e-3
+ALL = [T.F32, T.F16, T.BF16, T.Q8_0, T.Q2_K, T.Q3_K, T.Q4_K, T.Q5_K, T.Q6_K, T.IQ2_XXS, T.IQ2_S, T.IQ3_XXS, T.IQ4_XS]
+HOT = [T.Q8_0, T.Q4_K, T.Q6_K, T.IQ2_XXS]
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel_l2(got, want):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def stream():
+    return G.Stream()
+
+
+@pytest.mark.parametrize("ty", ALL)
+def test_dequant_bit_exact(ty, stream):
+    say("dequant", G.TYPE_NAMES[ty])
+    n = 256 * 257
+    raw = O.Rng(0x9E3779B97F4A7C15 + ty).random_blocks(ty, n)
+    want = O.dequantize(ty, raw, n)
+    dw = G.DeviceBuffer.from_array(raw)
+    dy = G.DeviceBuffer(n * 4)
+    G.ops.dequant_f32(ty, dw, n, dy, stream)
+    got = dy.download(np.float32, n, stream)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    dh = G.DeviceBuffer(n * 2)
+    G.ops.dequant_f16(ty, dw, n, dh, stream)
+    goth = dh.download(np.uint16, n, stream)
+    assert np.array_equal(goth, want.astype(np.float16).view(np.uint16))
+
+
+def test_quant_q8_1_bit_exact(stream):
+    say("quant_q8_1")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(32 * 4099).astype(np.float32)
+    x[:32] = 0
+    x[32:64] = np.linspace(-3, 3, 32)
+    x[64:96] = 1e-30
+    x[96:128] = rng.standard_normal(32).astype(np.float32) * 1e4
+    want = O.quantize_q8_1(x)
+    dx = G.DeviceBuffer.from_array(x)
+    dq = G.DeviceBuffer(want.nbytes)
+    G.ops.quant_q8_1(dx, dq, x.size, stream)
+    got = dq.download(np.uint8, want.size, stream)
+    assert np.array_equal(got, want)
+
+
+def _gemv_case(ty, rows, K, B, stream, seed, x_stride=None, accumulate=False, row_stride=None):
+    rb = G.row_bytes(ty, K)
+    rs = rb if row_stride is None else row_stride
+    raw = O.Rng(seed).random_blocks(ty, rows * K)
+    if rs != rb:  # spread rows apart
+        big = np.zeros(rows * rs, dtype=np.uint8)
+        for r in range(rows):
+            big[r * rs:r * rs + rb] = raw[r * rb:(r + 1) * rb]
+        wbytes = big
+    else:
+        wbytes = raw
+    xs = K if x_stride is None else x_stride
+    rng = np.random.default_rng(seed)
+    x = np.zeros(B * xs, dtype=np.float32)
+    for b in range(B):
+        x[b * xs:b * xs + K] = rng.standard_normal(K).astype(np.float32)
+    want = O.gemv(ty, wbytes, rs, K, rows, x, B=B, x_stride=xs)
+    y0 = rng.standard_normal(B * rows).astype(np.float32)
+    dw = G.DeviceBuffer.from_array(wbytes)
+    dx = G.DeviceBuffer.from_array(x)
+    dy = G.DeviceBuffer.from_array(y0)
+    G.ops.gemv(ty, dw, rs, K, rows, dx, xs, dy, rows, B, accumulate, stream)
+    got = dy.download(np.float32, B * rows, stream).reshape(B, rows)
+    if accumulate:
+        got = got.astype(np.float64) - y0.reshape(B, rows)
+    e = rel_l2(got, want)
+    say(f"  gemv {G.TYPE_NAMES[ty]} rows={rows} K={K} B={B} rs={rs} acc={accumulate}: rel-L2 {e:.2e}")
+    return e
+
+
+@pytest.mark.parametrize("ty", ALL)
+@pytest.mark.parametrize("rows,K", [(101, 4096), (3001, 2048), (257, 1536)])
+def test_gemv_matches_oracle(ty, rows, K, stream):
+    for B in (1, 3, 8):
+        assert _gemv_case(ty, rows, K, B, stream, seed=1000 * ty + rows + B) <= REL_L2
+
+
+@pytest.mark.parametrize("ty", HOT)
+def test_gemv_accumulate_and_strides(ty, stream):
+    K = 1024
+    assert _gemv_case(ty, 77, K, 2, stream, 7, accumulate=True) <= REL_L2
+    assert _gemv_case(ty, 77, K, 2, stream, 8, x_stride=K + 3) <= REL_L2       # unaligned x rows
+    assert _gemv_case(ty, 33, K, 1, stream, 9, row_stride=G.row_bytes(ty, K) + 2) <= REL_L2  # sparse rows
+
+
+@pytest.mark.parametrize("ty", [T.Q6_K, T.Q8_0])
+def test_gemv_long_rows_split(ty, stream):
+    # K beyond one launch's register-resident activation (K > 16384 at B=1) takes the K-split path
+    assert _gemv_case(ty, 64, 24576, 1, stream, 11) <= REL_L2
+    assert _gemv_case(ty, 64, 12288, 4, stream, 12) <= REL_L2
+
+
+def test_gemv_batched(stream):
+    ty, K, rows, nb = T.Q4_K, 512, 96, 5
+    rb = G.row_bytes(ty, K)
+    raw = O.Rng(77).random_blocks(ty, nb * rows * K)
+    x = np.random.default_rng(1).standard_normal(nb * K).astype(np.float32)
+    dw, dx = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(x)
+    dy = G.DeviceBuffer(nb * rows * 4)
+    G.ops.gemv_batched(ty, dw, rb, K, rows, dx, dy, nb, rows * rb, K, rows, stream)
+    got = dy.download(np.float32, nb * rows, stream).reshape(nb, rows)
+    for b in range(nb):
+        want = O.gemv(ty, raw[b * rows * rb:(b + 1) * rows * rb], rb, K, rows, x[b * K:(b + 1) * K])
+        assert rel_l2(got[b], want[0]) <= REL_L2
+
+
+def _experts(ty_gu, ty_dn, n_exp, n_embd, n_ff, seed):
+    rng = O.Rng(seed)
+    gate = [rng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(n_exp)]
+    up = [rng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(n_exp)]
+    down = [rng.random_blocks(ty_dn, n_embd * n_ff) for _ in range(n_exp)]
+    return gate, up, down
+
+
+@pytest.mark.parametrize("ty,nt,n,lim", [(T.IQ2_XXS, 1, 8, 0.0), (T.IQ2_XXS, 2, 16, 0.0), (T.Q4_K, 2, 5, 7.0),
+                                         (T.Q8_0, 1, 3, 0.0), (T.Q6_K, 2, 4, 3.0)])
+def test_moe_fused_matches_oracle(ty, nt, n, lim, stream):
+    say(f"moe {G.TYPE_NAMES[ty]} nt={nt} n={n} lim={lim}")
+    n_embd, n_ff = 2048, 1536 if ty != T.Q8_0 else 1024
+    gate, up, down = _experts(ty, ty, n, n_embd, n_ff, 4242 + ty)
+    rng = np.random.default_rng(ty)
+    x = rng.standard_normal((nt, n_embd)).astype(np.float32)
+    w = rng.random((nt, n)).astype(np.float32)
+    w[0, 1] = 0.0                                   # token 0 not routed to expert 1
+    pt, pe, pw = [], [], []
+    for t in range(nt):
+        for e in range(n):
+            pt.append(t); pe.append(e); pw.append(w[t, e])
+    rbg, rbd = G.row_bytes(ty, n_embd), G.row_bytes(ty, n_ff)
+    want, hwant = O.moe_ffn(ty, ty, gate, up, down, rbg, rbd, n_embd, n_ff, x, pt, pe, pw, lim=lim, want_h=True,
+                            nthreads=8)
+    bufs = [G.DeviceBuffer.from_array(a) for a in gate + up + down]
+    b = G.MoeBatch()
+    b.n = n
+    for e in range(n):
+        b.gate[e], b.up[e], b.down[e] = bufs[e].p.value, bufs[n + e].p.value, bufs[2 * n + e].p.value
+        for t in range(nt):
+            b.w[t][e] = w[t, e]
+    dx = G.DeviceBuffer.from_array(x)
+    dh = G.DeviceBuffer(n * nt * n_ff * 4)
+    y0 = rng.standard_normal((nt, n_embd)).astype(np.float32)
+    dy = G.DeviceBuffer.from_array(y0)
+    G.ops.moe_gateup(ty, b, nt, rbg, n_embd, n_ff, dx, dh, lim, stream)
+    G.ops.moe_down(ty, b, nt, rbd, n_ff, n_embd, dh, dy, stream)
+    h = dh.download(np.float32, n * nt * n_ff, stream).reshape(n, nt, n_ff)
+    hw = hwant.reshape(nt, n, n_ff).transpose(1, 0, 2)
+    eh = rel_l2(h, hw)
+    got = dy.download(np.float32, nt * n_embd, stream).reshape(nt, n_embd).astype(np.float64) - y0
+    ey = rel_l2(got, want)
+    say(f"  h rel-L2 {eh:.2e}  y rel-L2 {ey:.2e}")
+    assert eh <= REL_L2 and ey <= REL_L2
+
+
+def test_elementwise_and_rows(stream):
+    rng = np.random.default_rng(3)
+    n = 10007
+    g, u = rng.standard_normal(n).astype(np.float32) * 4, rng.standard_normal(n).astype(np.float32) * 4
+    dg, du, dy = G.DeviceBuffer.from_array(g), G.DeviceBuffer.from_array(u), G.DeviceBuffer(n * 4)
+    for lim in (0.0, 2.5):
+        G.ops.swiglu(dg, du, dy, n, lim, stream)
+        want = np.array([O.lib().or_swiglu(float(a), float(b), lim) for a, b in zip(g, u)])
+        assert np.allclose(dy.download(np.float32, n, stream), want, rtol=1e-5, atol=1e-6)
+    y0 = rng.standard_normal(n).astype(np.float32)
+    dy.upload(y0)
+    G.ops.axpy(dy, dg, 0.5, n, stream)
+    assert np.allclose(dy.download(np.float32, n, stream), y0 + np.float32(0.5) * g, rtol=1e-6, atol=1e-6)
+    rows, width = 37, 4096
+    x = rng.standard_normal((64, width)).astype(np.float32)
+    idx = rng.permutation(64)[:rows].astype(np.int32)
+    wv = rng.random(rows).astype(np.float32)
+    dx, di, dwv = G.DeviceBuffer.from_array(x), G.DeviceBuffer.from_array(idx), G.DeviceBuffer.from_array(wv)
+    dg2 = G.DeviceBuffer(rows * width * 4)
+    G.ops.gather_rows(dx, di, dg2, rows, width, stream)
+    gathered = dg2.download(np.float32, rows * width, stream).reshape(rows, width)
+    assert np.array_equal(gathered, x[idx])
+    acc = rng.standard_normal((64, width)).astype(np.float32)
+    da = G.DeviceBuffer.from_array(acc)
+    G.ops.scatter_add_rows(da, di, dwv, dg2, rows, width, stream)
+    want = acc.copy()
+    want[idx] += wv[:, None] * x[idx]
+    assert np.allclose(da.download(np.float32, 64 * width, stream).reshape(64, width), want, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("ty", [T.IQ2_XXS, T.Q4_K])
+def test_gemm_matches_oracle(ty, stream):
+    K, rows, N = 1024, 160, 37
+    rb = G.row_bytes(ty, K)
+    raw = O.Rng(31).random_blocks(ty, rows * K)
+    X = np.random.default_rng(2).standard_normal((N, K)).astype(np.float32)
+    want = O.gemv(ty, raw, rb, K, rows, X, B=N)
+    dw, dx, dy = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(N * rows * 4)
+    G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, stream)
+    got = dy.download(np.float32, N * rows, stream).reshape(N, rows)
+    assert rel_l2(got, want) <= REL_L2
