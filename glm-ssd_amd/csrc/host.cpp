@@ -170,22 +170,31 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     const int tab = (table_bytes(ty) + 15) & ~15;
     const int xq_bytes = (kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
     const int budget = (int)std::min<size_t>(c->max_lds, 160 * 1024);
+    // lanes per row: the smallest group whose per-lane unit count fits the register budget and
+    // whose tile (one row per group, all segments) fits the 16-byte-load budget and LDS
     int best = -1;
+    double best_score = -1.0;
     for (int lpr : {16, 32, 64}) {
         const int upl = (tot + lpr - 1) / lpr;
         if (upl > UMAX) continue;
         const int G = GS_WG / lpr;
         int rt = a.contig ? std::min(G, a.rows) : 1;
-        const int pitch = ((rt * a.row_bytes + 15 + 16) + 15) & ~15;
-        const int cps = (rt * a.row_bytes + 15 + 15) / 16;
-        if (NS * cps > GS_WG * GS_LD_MAX) continue;
-        if (tab + std::max(xq_bytes, NS * pitch + 16) > budget) continue;
-        best = lpr;
-        a.lpr = lpr;
-        a.upl = upl;
-        a.rt = rt;
-        a.span_pitch = pitch;
-        break;
+        auto fits = [&](int r) {
+            const int pitch = ((r * a.row_bytes + 15 + 16) + 15) & ~15;
+            const int cps = (r * a.row_bytes + 15 + 15) / 16;
+            return NS * cps <= GS_WG * GS_LD_MAX && tab + std::max(xq_bytes, NS * pitch + 16) <= budget;
+        };
+        while (rt > 1 && !fits(rt)) rt--;
+        if (!fits(rt)) continue;
+        const double score = (double)std::min(rt, std::min(G, a.rows)) / std::min(G, a.rows);
+        if (score > best_score + 1e-9) {
+            best_score = score;
+            best = lpr;
+            a.lpr = lpr;
+            a.upl = upl;
+            a.rt = rt;
+            a.span_pitch = ((rt * a.row_bytes + 15 + 16) + 15) & ~15;
+        }
     }
     if (best < 0) return hipErrorInvalidValue;
     const int cps = (a.rt * a.row_bytes + 15 + 15) / 16;

@@ -325,6 +325,9 @@ GS_STREAM_ALL(GS_STREAM_F, GS_STREAM_ID)
         constexpr int GPB = QK / 8;                                                             \
         float v[8];                                                                             \
         DEQ(a.src + (g / GPB) * BB, (int)(g % GPB), v);                                         \
+        /* opaque to the optimizer: keeps the f32 value (and the sign of a zero) intact before  \
+           the single f32 -> f16 rounding */                                                   \
+        for (int i = 0; i < 8; i++) asm volatile("" : "+v"(v[i]));                              \
         uint4 o;                                                                                \
         o.x = f2h(v[0]) | (f2h(v[1]) << 16);                                                    \
         o.y = f2h(v[2]) | (f2h(v[3]) << 16);                                                    \

@@ -46,7 +46,15 @@ def test_dequant_bit_exact(ty, stream):
     dh = G.DeviceBuffer(n * 2)
     G.ops.dequant_f16(ty, dw, n, dh, stream)
     goth = dh.download(np.uint16, n, stream)
-    assert np.array_equal(goth, want.astype(np.float16).view(np.uint16))
+    with np.errstate(over="ignore"):
+        wh = want.astype(np.float16)
+    nan = np.isnan(wh)           # NaN payloads are not specified by the conversion
+    assert np.array_equal(np.isnan(goth.view(np.float16)), nan)
+    bad = np.nonzero(goth[~nan] != wh.view(np.uint16)[~nan])[0]
+    if bad.size:
+        i = bad[:5]
+        say("  f16 mismatches", bad.size, want[~nan][i], goth[~nan][i], wh.view(np.uint16)[~nan][i])
+    assert bad.size == 0
 
 
 def test_quant_q8_1_bit_exact(stream):
@@ -95,7 +103,8 @@ def _gemv_case(ty, rows, K, B, stream, seed, x_stride=None, accumulate=False, ro
     return e
 
 
-@pytest.mark.parametrize("ty", ALL)
+# BF16 is left out like in the reference harness (qtest.rs:12-25): its random blocks hold NaN/Inf
+@pytest.mark.parametrize("ty", [t for t in ALL if t != T.BF16])
 @pytest.mark.parametrize("rows,K", [(101, 4096), (3001, 2048), (257, 1536)])
 def test_gemv_matches_oracle(ty, rows, K, stream):
     for B in (1, 3, 8):
