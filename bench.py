@@ -1,0 +1,215 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Headline: routed-expert FFN for one decode token, 8 IQ2_XXS experts of
+288 resident in HBM (hidden 4096, intermediate 1536). One step = gs_moe_gateup + gs_moe_down (the
+engine's fused decode path) for one token; each step routes to the next 8 experts of a seeded
+permutation, so an expert's 4.87 MB come back only after all 288 (1.4 GB) were read: no step is
+served from the 256 MB last-level cache. value = algorithmic weight bytes per step / step time.
+
+Also reported (secondary): config 1 (Q8_0 GEMV), config 3 (Q4_K / Q6_K GEMV), weight copies
+rotated over > 512 MB. The CPU baseline is the oracle's C port of the reference CPU path
+(crates/quants dequantize + f64 dot, crates/engine/src/qtest.rs:77-108) on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 500] [--warmup 50] [--no-cpu] [--calib]
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "glm-ssd_amd"))
+
+METRIC = "quant-GEMV weight GB/s (% HBM peak); MoE grouped-GEMM TFLOP/s at 512 tok"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bench_lib():
+    import glmssd
+    glmssd.lib()
+    L = C.CDLL(os.path.join(ROOT, "glm-ssd_amd", "libglmssd_bench.so"))
+    P, I64 = C.c_void_p, C.c_int64
+    L.bn_moe_decode.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, I64, C.c_int, C.c_int, I64, P, P, P, C.c_int,
+                                C.c_int, P, C.POINTER(C.c_float), C.POINTER(C.c_float)]
+    L.bn_gemv.argtypes = [C.c_int, P, C.c_int, I64, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P,
+                          C.POINTER(C.c_float)]
+    L.bn_copy.argtypes = [P, P, C.c_size_t, C.c_int, P, C.POINTER(C.c_float)]
+    return L
+
+
+def run_moe_decode(L, s, steps, warmup, n_expert=288, n_embd=4096, n_ff=1536, seed=2):
+    import glmssd as G
+    from glmssd import synth
+    ty = G.GgmlType.IQ2_XXS
+    rng = np.random.default_rng(seed)
+    rbg, rbd = G.row_bytes(ty, n_embd), G.row_bytes(ty, n_ff)
+    mat = n_ff * rbg                       # bytes of one gate (= up = down) matrix
+    gate = G.DeviceBuffer(n_expert * mat)
+    up = G.DeviceBuffer(n_expert * mat)
+    down = G.DeviceBuffer(n_expert * mat)
+    log(f"config 2: generating {3 * n_expert * mat / 1e9:.2f} GB of IQ2_XXS experts")
+    for e in range(n_expert):
+        g, u, d = synth.iq2_xxs_expert(rng, n_embd, n_ff)
+        gate.upload(g, s, e * mat)
+        up.upload(u, s, e * mat)
+        down.upload(d, s, e * mat)
+    x = rng.standard_normal(n_embd).astype(np.float32)
+    dx = G.DeviceBuffer.from_array(x, s)
+    dh = G.DeviceBuffer(8 * n_ff * 4)
+    dy = G.DeviceBuffer(n_embd * 4)
+    dy.zero(s)
+    # 36 batches = one pass over a permutation of all 288 experts, 8 distinct per step
+    perm = rng.permutation(n_expert)
+    nb = n_expert // 8
+    batches = (G.MoeBatch * nb)()
+    for i in range(nb):
+        b = batches[i]
+        b.n = 8
+        w = synth.softmax(rng.standard_normal(8))
+        for j in range(8):
+            e = int(perm[8 * i + j])
+            b.gate[j] = gate.p.value + e * mat
+            b.up[j] = up.p.value + e * mat
+            b.down[j] = down.p.value + e * mat
+            b.w[0][j] = w[j]
+    ms, msg = C.c_float(), C.c_float()
+    rc = L.bn_moe_decode(ty, ty, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p, steps,
+                         warmup, s.raw(), C.byref(ms), C.byref(msg))
+    G.check(rc)
+    step_bytes = 8 * 3 * mat
+    gu_bytes = 8 * 2 * mat
+    keep = (gate, up, down, dx, dh, dy, batches)
+    return dict(ms_step=ms.value, ms_gateup=msg.value, step_bytes=step_bytes, gateup_bytes=gu_bytes,
+                flops=8 * 3 * 2 * n_ff * n_embd), keep
+
+
+def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 20):
+    import glmssd as G
+    rng = np.random.default_rng(seed)
+    raw = make(rng, rows, K)
+    n = max(2, -(-min_rot_bytes // raw.nbytes))
+    buf = G.DeviceBuffer(n * raw.nbytes)
+    buf.upload(raw, s)
+    for i in range(1, n):
+        G.check(G.lib().gs_memcpy_d2d(buf.ptr(i * raw.nbytes), buf.p, raw.nbytes, s.raw()))
+    s.sync()
+    ptrs = (C.c_void_p * n)(*[buf.p.value + i * raw.nbytes for i in range(n)])
+    x = G.DeviceBuffer.from_array(rng.standard_normal(K).astype(np.float32), s)
+    y = G.DeviceBuffer(rows * 4)
+    ms = C.c_float()
+    G.check(L.bn_gemv(ty, C.cast(ptrs, C.c_void_p), n, G.row_bytes(ty, K), K, rows, x.p, y.p, 1, steps, warmup,
+                      s.raw(), C.byref(ms)))
+    return dict(ms=ms.value, bytes=raw.nbytes, gbps=raw.nbytes / (ms.value * 1e-3) / 1e9, copies=n)
+
+
+def cpu_baseline(budget_s=12.0, n_embd=4096, n_ff=1536, seed=2):
+    """Oracle (C port of crates/quants dequantize + f64 dot) on the config-2 FFN, all host cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    from glmssd import synth
+    import glmssd as G
+    ty = G.GgmlType.IQ2_XXS
+    rng = np.random.default_rng(seed)
+    experts = [synth.iq2_xxs_expert(rng, n_embd, n_ff) for _ in range(8)]
+    gate, up, down = [e[0] for e in experts], [e[1] for e in experts], [e[2] for e in experts]
+    x = rng.standard_normal((1, n_embd)).astype(np.float32)
+    w = synth.softmax(rng.standard_normal(8))
+    cores = min(16, os.cpu_count() or 1)
+    rbg, rbd = G.row_bytes(ty, n_embd), G.row_bytes(ty, n_ff)
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        O.moe_ffn(ty, ty, gate, up, down, rbg, rbd, n_embd, n_ff, x, [0] * 8, list(range(8)), w, nthreads=cores)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= 200:
+            break
+    step_bytes = 8 * 3 * n_ff * rbg
+    return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{steps} config-2 steps (8 IQ2_XXS experts, 1 token) in {el:.1f} s, oracle C port "
+                      f"(dequantize + f64 dot), {cores} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--calib", action="store_true", help="also run a 1 GiB d2d copy (HBM counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU (the hot path has no multi-GPU part); --gpus {args.gpus} "
+              "is not supported", file=sys.stderr)
+        sys.exit(2)
+    import glmssd as G
+    L = bench_lib()
+    s = G.Stream()
+    info = G.device_info(0)
+    log(f"device: {info.name.decode()} CUs={info.sm_count}")
+
+    res, keep = run_moe_decode(L, s, args.steps, args.warmup)
+    value = res["step_bytes"] / (res["ms_step"] * 1e-3) / 1e9
+    gu_gbps = res["gateup_bytes"] / (res["ms_gateup"] * 1e-3) / 1e9
+    log(f"config 2: {res['ms_step'] * 1e3:.2f} us/step, {value:.1f} GB/s; gate/up kernel {res['ms_gateup'] * 1e3:.2f} us "
+        f"= {gu_gbps:.1f} GB/s")
+    del keep
+
+    secondary = {}
+    if not args.no_secondary:
+        from glmssd import synth
+        r1 = run_gemv(L, s, G.GgmlType.Q8_0, 4096, 4096, synth.q8_0_matrix, args.steps, args.warmup, 1)
+        r3a = run_gemv(L, s, G.GgmlType.Q4_K, 12288, 4096, synth.q4_k_matrix, args.steps, args.warmup, 3)
+        r3b = run_gemv(L, s, G.GgmlType.Q6_K, 4096, 12288, synth.q6_k_matrix, args.steps, args.warmup, 4)
+        for name, r in [("config1_q8_0_gemv_4096x4096", r1), ("config3_q4_k_gemv_k4096_rows12288", r3a),
+                        ("config3_q6_k_gemv_k12288_rows4096", r3b)]:
+            secondary[name] = {"GB/s": round(r["gbps"], 1), "us_per_call": round(r["ms"] * 1e3, 2),
+                               "frac_hbm_peak": round(r["gbps"] / HBM_PEAK_GBPS, 4), "weight_bytes": r["bytes"],
+                               "rotated_copies": r["copies"]}
+            log(f"{name}: {r['ms'] * 1e3:.2f} us, {r['gbps']:.1f} GB/s")
+    if args.calib:
+        src, dst = G.DeviceBuffer(1 << 30), G.DeviceBuffer(1 << 30)
+        ms = C.c_float()
+        G.check(L.bn_copy(dst.p, src.p, 1 << 30, 5, s.raw(), C.byref(ms)))
+        log(f"calib: 1 GiB d2d copy {ms.value:.3f} ms")
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "iq2_xxs x q8_1 (int8 dot4, f32 accumulate)",
+        "data": "synthetic (seeded random IQ2_XXS blocks, d~|N(0,0.02)|; x~N(0,1))",
+        "config": {"workload": "config 2: routed-expert FFN, 1 decode token, 8 of 288 resident IQ2_XXS experts "
+                               "(hidden 4096, intermediate 1536), gate/up+SwiGLU then down+weighted combine",
+                   "weight_bytes_per_step": res["step_bytes"], "frac_hbm_peak": round(value / HBM_PEAK_GBPS, 4),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "gs_moe_gateup (gs_k_stream_16_1_1)",
+                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": res["gateup_bytes"],
+                     "avg_launch_us": round(res["ms_gateup"] * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,94 @@
+// Native timing loops for bench.py. Each loop drives the gs_* C ABI exactly as the engine's
+// decode path does (crates/engine/src/forward.rs:1067-1107: one gs_moe_gateup + one gs_moe_down
+// per expert batch) and brackets the timed launches with HIP events on the launch stream, so the
+// host-side Python loop adds no gaps between kernels.
+#include <stdint.h>
+#include "../../include/glmssd.h"
+
+#define BN_EXPORT extern "C" __attribute__((visibility("default")))
+#define CK(x)                  \
+    do {                       \
+        int _e = (x);          \
+        if (_e) return _e;     \
+    } while (0)
+
+namespace {
+struct Timer {
+    void *a = nullptr, *b = nullptr;
+    int init() {
+        CK(gs_event_create_timed(&a));
+        return gs_event_create_timed(&b);
+    }
+    ~Timer() {
+        if (a) gs_event_destroy(a);
+        if (b) gs_event_destroy(b);
+    }
+};
+}  // namespace
+
+// Decode step = gs_moe_gateup + gs_moe_down over batch (i % nb). ms_step: mean per step;
+// ms_gateup: mean of a separate loop of gs_moe_gateup alone (dominant kernel).
+BN_EXPORT int bn_moe_decode(int ty_gu, int ty_dn, const GsMoeBatch *batches, int nb, int nt, int64_t rs_gu, int n_embd,
+                            int n_ff, int64_t rs_dn, const float *x, float *h, float *y, int steps, int warmup,
+                            void *s, float *ms_step, float *ms_gateup) {
+    Timer t;
+    CK(t.init());
+    for (int i = 0; i < warmup; i++) {
+        const GsMoeBatch *b = &batches[i % nb];
+        CK(gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, 0.0f, s));
+        CK(gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y, s));
+    }
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    for (int i = 0; i < steps; i++) {
+        const GsMoeBatch *b = &batches[(warmup + i) % nb];
+        CK(gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, 0.0f, s));
+        CK(gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y, s));
+    }
+    CK(gs_event_record(t.b, s));
+    CK(gs_event_sync(t.b));
+    CK(gs_event_elapsed_ms(ms_step, t.a, t.b));
+    *ms_step /= steps;
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    for (int i = 0; i < steps; i++) {
+        const GsMoeBatch *b = &batches[i % nb];
+        CK(gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, 0.0f, s));
+    }
+    CK(gs_event_record(t.b, s));
+    CK(gs_event_sync(t.b));
+    CK(gs_event_elapsed_ms(ms_gateup, t.a, t.b));
+    *ms_gateup /= steps;
+    return 0;
+}
+
+// GEMV over rotating weight copies Ws[i % nw] (defeats the last-level cache); mean ms per call.
+BN_EXPORT int bn_gemv(int ty, const void *const *Ws, int nw, int64_t rs, int K, int rows, const float *x, float *y,
+                      int B, int steps, int warmup, void *s, float *ms) {
+    Timer t;
+    CK(t.init());
+    for (int i = 0; i < warmup; i++) CK(gs_gemv(ty, Ws[i % nw], rs, K, rows, x, K, y, rows, B, 0, s));
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    for (int i = 0; i < steps; i++) CK(gs_gemv(ty, Ws[i % nw], rs, K, rows, x, K, y, rows, B, 0, s));
+    CK(gs_event_record(t.b, s));
+    CK(gs_event_sync(t.b));
+    CK(gs_event_elapsed_ms(ms, t.a, t.b));
+    *ms /= steps;
+    return 0;
+}
+
+// Device-to-device copy of n bytes, reps times: the known-size reference for HBM byte counters.
+BN_EXPORT int bn_copy(void *dst, const void *src, size_t n, int reps, void *s, float *ms) {
+    Timer t;
+    CK(t.init());
+    CK(gs_memcpy_d2d(dst, src, n, s));
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    for (int i = 0; i < reps; i++) CK(gs_memcpy_d2d(dst, src, n, s));
+    CK(gs_event_record(t.b, s));
+    CK(gs_event_sync(t.b));
+    CK(gs_event_elapsed_ms(ms, t.a, t.b));
+    *ms /= reps;
+    return 0;
+}
