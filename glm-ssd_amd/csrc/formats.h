@@ -5,9 +5,10 @@
 //               the CPU reference (crates/quants/src/lib.rs:131-343). Used by gs_dequant_* and by
 //               the generic matmul path. The f32 operation order is the reference's and FP
 //               contraction is off in this section, so no multiply-add gets fused.
-//   * F*::dot : the fast integer paths for Q8_0 / Q4_K / Q6_K / IQ2_XXS. One call decodes one
-//               32-element "unit" of a weight row from LDS and dots it with up to NV q8_1 activation
-//               units held in registers (v_dot4_i32_i8), applying the block scales in f32.
+//   * F*::load/dot : the fast integer paths for Q8_0 / Q4_K / Q6_K / IQ2_XXS. load() fetches one
+//               32-element "unit" of a weight row straight from HBM into registers; dot() decodes it
+//               and dots it with up to NV q8_1 activation units held in registers (v_dot4_i32_i8),
+//               applying the block scales in f32.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -27,27 +28,6 @@ __device__ __forceinline__ uint32_t rb8(const uint8_t *p, int i) { return p[i]; 
 __device__ __forceinline__ uint32_t rb16(const uint8_t *p, int i) { return (uint32_t)p[i] | ((uint32_t)p[i + 1] << 8); }
 __device__ __forceinline__ uint32_t rb32(const uint8_t *p, int i) {
     return (uint32_t)p[i] | ((uint32_t)p[i + 1] << 8) | ((uint32_t)p[i + 2] << 16) | ((uint32_t)p[i + 3] << 24);
-}
-
-// N unaligned 32-bit words starting at LDS byte offset `off`: N+1 aligned dword reads, then
-// v_alignbyte_b32 funnels each word out of its two neighbours.
-template <int N>
-__device__ __forceinline__ void lds_words(const uint8_t *L, uint32_t off, uint32_t (&w)[N]) {
-    const uint32_t a = off & ~3u, s = off & 3u;
-    const uint32_t *p = (const uint32_t *)(L + a);
-    uint32_t d[N + 1];
-#pragma unroll
-    for (int i = 0; i <= N; i++) d[i] = p[i];
-#pragma unroll
-    for (int i = 0; i < N; i++) w[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], s);
-}
-__device__ __forceinline__ uint32_t lds_word(const uint8_t *L, uint32_t off) {
-    uint32_t w[1];
-    lds_words<1>(L, off, w);
-    return w[0];
-}
-__device__ __forceinline__ float lds_half(const uint8_t *L, uint32_t off) { // off even
-    return h2f(*(const uint16_t *)(L + off));
 }
 
 // ggml tables live in the code object's read-only data
@@ -230,32 +210,52 @@ __device__ __forceinline__ int dot8(const uint32_t (&w)[8], const uint32_t (&q)[
     return s;
 }
 
+// Unaligned loads straight from HBM: every block field is 2-byte aligned and gfx950 serves
+// unaligned global loads (the driver runs the GPU in unaligned-access mode), so a lane reads its
+// unit's bytes with one 8- or 16-byte load whatever the block size.
+__device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *(const uint4 *)p; }
+__device__ __forceinline__ uint2 ldg8(const uint8_t *p) { return *(const uint2 *)p; }
+__device__ __forceinline__ uint32_t ldg4(const uint8_t *p) { return *(const uint32_t *)p; }
+__device__ __forceinline__ uint32_t ldg2(const uint8_t *p) { return *(const uint16_t *)p; }
+
+// Each format: Raw = the registers one unit needs from memory; load() issues the loads for unit
+// `j` of the block at `b`; dot() decodes Raw and accumulates r[t] += W_unit . x_t for t < nv.
 struct FQ8_0 : UnitGeom<32, 34> {
-    static constexpr int TYPE = GS_Q8_0, QK = 32, BB = 34, TAB = 0;
+    static constexpr int TYPE = GS_Q8_0, QK = 32, BB = 34, TAB = 0, RAW = 9;
+    struct Raw { uint4 lo, hi; uint32_t d; };
     __device__ static void init(uint8_t *, int) {}
+    __device__ static __forceinline__ void load(const uint8_t *b, int, Raw &w) {
+        w.d = ldg2(b);
+        w.lo = ldg16(b + 2);
+        w.hi = ldg16(b + 18);
+    }
     template <int NV>
-    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int, const uint8_t *, const XU (&x)[NV],
-                                               int nv, float (&r)[NV]) {
-        const float d = lds_half(L, o);
-        uint32_t w[8];
-        lds_words<8>(L, o + 2, w);
+    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const float d = h2f(w.d);
+        const uint32_t q[8] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w, w.hi.x, w.hi.y, w.hi.z, w.hi.w};
 #pragma unroll
         for (int t = 0; t < NV; t++)
-            if (t < nv) r[t] += (d * x[t].D) * (float)dot8(w, x[t].q);
+            if (t < nv) r[t] += (d * x[t].D) * (float)dot8(q, x[t].q);
     }
 };
 
 struct FQ4_K : UnitGeom<256, 144> {
-    static constexpr int TYPE = GS_Q4_K, QK = 256, BB = 144, TAB = 0;
+    static constexpr int TYPE = GS_Q4_K, QK = 256, BB = 144, TAB = 0, RAW = 12;
+    struct Raw { uint4 hd, lo, hi; };   // bytes 0..15 (d, dmin, scales[12]); 32 quant bytes
     __device__ static void init(uint8_t *, int) {}
+    __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
+        w.hd = ldg16(b);
+        w.lo = ldg16(b + 16 + 32 * (j >> 1));
+        w.hi = ldg16(b + 32 + 32 * (j >> 1));
+    }
     template <int NV>
-    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int j, const uint8_t *, const XU (&x)[NV],
-                                               int nv, float (&r)[NV]) {
-        uint32_t hd[4];
-        lds_words<4>(L, o, hd);   // d | dmin, scales[0..11]
-        const float d = h2f(hd[0] & 0xffff), dmin = h2f(hd[0] >> 16);
-        // bytes k of scales[] = byte (k+4) of the block
-        auto sb = [&](int k) -> uint32_t { return (hd[1 + (k >> 2)] >> (8 * (k & 3))) & 0xff; };
+    __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const float d = h2f(w.hd.x & 0xffff), dmin = h2f(w.hd.x >> 16);
+        const uint32_t hs[3] = {w.hd.y, w.hd.z, w.hd.w};
+        // byte k of scales[] (crates/quants/src/lib.rs:87-93 scale_min_k4)
+        auto sb = [&](int k) -> uint32_t { return (hs[k >> 2] >> (8 * (k & 3))) & 0xff; };
         uint32_t sc, mn;
         if (j < 4) {
             sc = sb(j) & 63;
@@ -264,43 +264,53 @@ struct FQ4_K : UnitGeom<256, 144> {
             sc = (sb(j + 4) & 0xF) | ((sb(j - 4) >> 6) << 4);
             mn = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
         }
-        uint32_t w[8];
-        lds_words<8>(L, o + 16 + 32 * (j >> 1), w);
         const int sh = (j & 1) * 4;
+        const uint32_t q0[8] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w, w.hi.x, w.hi.y, w.hi.z, w.hi.w};
+        uint32_t q[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) w[i] = (w[i] >> sh) & 0x0F0F0F0Fu;
+        for (int i = 0; i < 8; i++) q[i] = (q0[i] >> sh) & 0x0F0F0F0Fu;
         const float ds = d * (float)sc, dm = dmin * (float)mn;
 #pragma unroll
         for (int t = 0; t < NV; t++)
-            if (t < nv) r[t] += x[t].D * (ds * (float)dot8(w, x[t].q) - dm * (float)(x[t].slo + x[t].shi));
+            if (t < nv) r[t] += x[t].D * (ds * (float)dot8(q, x[t].q) - dm * (float)(x[t].slo + x[t].shi));
     }
 };
 
 struct FQ6_K : UnitGeom<256, 210> {
-    static constexpr int TYPE = GS_Q6_K, QK = 256, BB = 210, TAB = 0;
+    static constexpr int TYPE = GS_Q6_K, QK = 256, BB = 210, TAB = 0, RAW = 18;
+    struct Raw { uint4 l0, l1, h0, h1; uint32_t sc, d; };
     __device__ static void init(uint8_t *, int) {}
-    template <int NV>
-    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int j, const uint8_t *, const XU (&x)[NV],
-                                               int nv, float (&r)[NV]) {
+    __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
         const int half = j >> 2, quarter = j & 3;
-        uint32_t ql[8], qh[8];
-        lds_words<8>(L, o + 64 * half + 32 * (quarter & 1), ql);
-        lds_words<8>(L, o + 128 + 32 * half, qh);
+        const uint8_t *ql = b + 64 * half + 32 * (quarter & 1), *qh = b + 128 + 32 * half;
+        w.l0 = ldg16(ql);
+        w.l1 = ldg16(ql + 16);
+        w.h0 = ldg16(qh);
+        w.h1 = ldg16(qh + 16);
+        w.sc = ldg2(b + 192 + 8 * half + 2 * quarter);
+        w.d = ldg2(b + 208);
+    }
+    template <int NV>
+    __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const int quarter = j & 3;
         const int nsh = quarter >= 2 ? 4 : 0, hsh = 2 * quarter;
-        uint32_t w[8];
+        const uint32_t ql[8] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w, w.l1.x, w.l1.y, w.l1.z, w.l1.w};
+        const uint32_t qh[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
+        uint32_t q[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) w[i] = ((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4);
-        const uint32_t scw = lds_word(L, o + 192 + 8 * half + 2 * quarter);
-        const int sc0 = (int8_t)(scw & 0xff), sc1 = (int8_t)((scw >> 8) & 0xff);
-        const float d = lds_half(L, o + 208);
+        for (int i = 0; i < 8; i++) q[i] = ((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4);
+        const int sc0 = (int8_t)(w.sc & 0xff), sc1 = (int8_t)((w.sc >> 8) & 0xff);
+        const float d = h2f(w.d);
 #pragma unroll
         for (int t = 0; t < NV; t++) {
             if (t < nv) {
                 int lo = 0, hi = 0;
 #pragma unroll
-                for (int i = 0; i < 4; i++) lo = __builtin_amdgcn_sdot4((int)w[i], (int)x[t].q[i], lo, false);
+                for (int i = 0; i < 4; i++) lo = __builtin_amdgcn_sdot4((int)q[i], (int)x[t].q[i], lo, false);
 #pragma unroll
-                for (int i = 4; i < 8; i++) hi = __builtin_amdgcn_sdot4((int)w[i], (int)x[t].q[i], hi, false);
+                for (int i = 4; i < 8; i++) hi = __builtin_amdgcn_sdot4((int)q[i], (int)x[t].q[i], hi, false);
+                // sum (q-32) x = sum q x - 32 sum x, per 16-element half with its own scale
                 r[t] += (d * x[t].D) * (float)(sc0 * (lo - 32 * x[t].slo) + sc1 * (hi - 32 * x[t].shi));
             }
         }
@@ -312,7 +322,8 @@ struct FQ6_K : UnitGeom<256, 210> {
 // from the pair {-grid, grid}; -grid bytes come from one subtraction (0x01010100 - grid) since
 // every grid byte is nonzero.
 struct FIQ2_XXS : UnitGeom<256, 66> {
-    static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 2048 + 1024;
+    static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 2048 + 1024, RAW = 3;
+    struct Raw { uint2 a; uint32_t d; };
     __device__ static void init(uint8_t *tab, int tid) {
         uint64_t *g = (uint64_t *)tab;
         for (int i = tid; i < 256; i += GS_WG) g[i] = iq2xxs_grid[i];
@@ -329,45 +340,48 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
             s[2 * i + 1] = hi;
         }
     }
+    __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
+        w.d = ldg2(b);
+        w.a = ldg8(b + 2 + 8 * j);
+    }
     template <int NV>
-    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int j, const uint8_t *tab,
-                                               const XU (&x)[NV], int nv, float (&r)[NV]) {
-        const float d = lds_half(L, o);
-        uint32_t a[2];
-        lds_words<2>(L, o + 2 + 8 * j, a);
-        const float db = d * (0.5f + (float)(a[1] >> 28)) * 0.25f;
+    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *tab, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const float db = h2f(w.d) * (0.5f + (float)(w.a.y >> 28)) * 0.25f;
         const uint2 *grid = (const uint2 *)tab;
         const uint2 *sel = (const uint2 *)(tab + 2048);
-        uint32_t w[8];
+        uint32_t q[8];
 #pragma unroll
         for (int l = 0; l < 4; l++) {
-            const uint2 g = grid[(a[0] >> (8 * l)) & 0xff];
-            const uint2 s = sel[(a[1] >> (7 * l)) & 127];
-            w[2 * l] = __builtin_amdgcn_perm(0x01010100u - g.x, g.x, s.x);
-            w[2 * l + 1] = __builtin_amdgcn_perm(0x01010100u - g.y, g.y, s.y);
+            const uint2 g = grid[(w.a.x >> (8 * l)) & 0xff];
+            const uint2 s = sel[(w.a.y >> (7 * l)) & 127];
+            q[2 * l] = __builtin_amdgcn_perm(0x01010100u - g.x, g.x, s.x);
+            q[2 * l + 1] = __builtin_amdgcn_perm(0x01010100u - g.y, g.y, s.y);
         }
 #pragma unroll
         for (int t = 0; t < NV; t++)
-            if (t < nv) r[t] += (db * x[t].D) * (float)dot8(w, x[t].q);
+            if (t < nv) r[t] += (db * x[t].D) * (float)dot8(q, x[t].q);
     }
 };
 
-// Generic path for the remaining types: exact f32 decode of the unit, f32 dot with the
-// dequantized activations (D * q). Slower, used for the non-hot formats.
+// Generic path for the remaining types: exact f32 decode of the unit straight from global
+// memory, f32 dot with the dequantized activations (D * q). Slower; used for the non-hot formats.
 template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float *)>
 struct FGeneric : UnitGeom<QK_, BB_> {
-    static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0;
+    static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0, RAW = 2;
+    struct Raw { const uint8_t *p; };
     __device__ static void init(uint8_t *, int) {}
+    __device__ static __forceinline__ void load(const uint8_t *b, int, Raw &w) { w.p = b; }
     template <int NV>
-    __device__ static __forceinline__ void dot(const uint8_t *L, uint32_t o, int j, const uint8_t *, const XU (&x)[NV],
-                                               int nv, float (&r)[NV]) {
+    __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
         float v[32];
         if (QK >= 32) {
 #pragma unroll
-            for (int g = 0; g < 4; g++) DEQ(L + o, 4 * j + g, v + 8 * g);
+            for (int g = 0; g < 4; g++) DEQ(w.p, 4 * j + g, v + 8 * g);
         } else {
 #pragma unroll
-            for (int g = 0; g < 4; g++) DEQ(L + o + g * BB, 0, v + 8 * g);
+            for (int g = 0; g < 4; g++) DEQ(w.p + g * BB, 0, v + 8 * g);
         }
 #pragma unroll
         for (int t = 0; t < NV; t++) {

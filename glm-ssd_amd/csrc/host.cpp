@@ -147,12 +147,6 @@ int ggml_block_elems(int ty) {  // elements per ggml block (1 for plain types)
 }
 int table_bytes(int ty) { return ty == GS_IQ2_XXS ? 2048 + 1024 : 0; }
 
-struct StreamLaunch {
-    StreamArgs a;
-    uint32_t cps_magic;
-    int cps;
-};
-
 // Plan and launch one streaming kernel (kind 0 GEMV, 1 MoE gate/up, 2 MoE down).
 hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 1) {
     int qk, bb;
@@ -160,53 +154,42 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
-    const int NS = kind == 0 ? 1 : (kind == 1 ? 2 : a.nseg);
     const int NVt = a.nvec <= 1 ? 1 : a.nvec <= 2 ? 2 : a.nvec <= 4 ? 4 : 8;
-    const int UMAX = 8 / NVt;
     a.row_bytes = (int)((int64_t)a.K / qk * bb);
     a.nu = a.K / 32;
-    a.contig = a.row_stride == a.row_bytes;
-    const int tot = NS * a.nu;
-    const int tab = (table_bytes(ty) + 15) & ~15;
-    const int xq_bytes = (kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
-    const int budget = (int)std::min<size_t>(c->max_lds, 160 * 1024);
-    // lanes per row: the smallest group whose per-lane unit count fits the register budget and
-    // whose tile (one row per group, all segments) fits the 16-byte-load budget and LDS
-    int best = -1;
-    double best_score = -1.0;
-    for (int lpr : {16, 32, 64}) {
+    // units one lane must cover per row: GEMV one row, GATEUP the same units of gate and up
+    // (two per activation unit), DOWN the concatenated rows of every expert in the batch
+    const int tot = kind == 2 ? a.nseg * a.nu : a.nu;
+    const int mult = kind == 1 ? 2 : 1;
+    // instantiated weight-unit budgets per lane (kernels.hip GS_STREAM_MV / GS_STREAM_GU)
+    std::vector<int> umaxes;
+    if (kind == 1) umaxes = NVt == 1 ? std::vector<int>{2, 4, 8} : NVt == 2 ? std::vector<int>{2, 4}
+                          : NVt == 4 ? std::vector<int>{2, 4} : std::vector<int>{2};
+    else umaxes = NVt == 1 ? std::vector<int>{2, 4, 6, 8} : NVt == 2 ? std::vector<int>{2, 4}
+                : NVt == 4 ? std::vector<int>{1, 2} : std::vector<int>{1};
+    int best_lpr = -1, best_um = 0;
+    double best_eff = -1.0;
+    for (int lpr : {64, 32, 16}) {
         const int upl = (tot + lpr - 1) / lpr;
-        if (upl > UMAX) continue;
-        const int G = GS_WG / lpr;
-        int rt = a.contig ? std::min(G, a.rows) : 1;
-        auto fits = [&](int r) {
-            const int pitch = ((r * a.row_bytes + 15 + 16) + 15) & ~15;
-            const int cps = (r * a.row_bytes + 15 + 15) / 16;
-            return NS * cps <= GS_WG * GS_LD_MAX && tab + std::max(xq_bytes, NS * pitch + 16) <= budget;
-        };
-        while (rt > 1 && !fits(rt)) rt--;
-        if (!fits(rt)) continue;
-        const double score = (double)std::min(rt, std::min(G, a.rows)) / std::min(G, a.rows);
-        if (score > best_score + 1e-9) {
-            best_score = score;
-            best = lpr;
-            a.lpr = lpr;
-            a.upl = upl;
-            a.rt = rt;
-            a.span_pitch = ((rt * a.row_bytes + 15 + 16) + 15) & ~15;
+        int um = 0;
+        for (int u : umaxes)
+            if (u >= upl * mult) { um = u; break; }
+        if (!um) continue;
+        const double eff = (double)tot * mult / ((double)lpr * um);
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best_lpr = lpr;
+            best_um = um;
         }
     }
-    if (best < 0) return hipErrorInvalidValue;
-    const int cps = (a.rt * a.row_bytes + 15 + 15) / 16;
-    a.n_row_tiles = (a.rows + a.rt - 1) / a.rt;
-    a.n_tiles = kind == 1 ? a.nseg * a.n_row_tiles : a.n_row_tiles;
-    a.lds_tile = NS * a.span_pitch;
-    const size_t lds = (size_t)tab + std::max(xq_bytes, NS * a.span_pitch + 16);
-    StreamLaunch L;
-    L.a = a;
-    L.cps = cps;
-    L.cps_magic = (uint32_t)((0x100000000ull + cps - 1) / cps);
-    const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" + std::to_string(NVt);
+    if (best_lpr < 0) return hipErrorInvalidValue;
+    a.lpr = best_lpr;
+    a.upl = (tot + best_lpr - 1) / best_lpr;
+    const int tab = (table_bytes(ty) + 15) & ~15;
+    const size_t lds = (size_t)tab + (size_t)(kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
+    if (lds > std::min<size_t>(c->max_lds, 160 * 1024)) return hipErrorInvalidValue;
+    const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" +
+                             std::to_string(NVt) + "_" + std::to_string(best_um);
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
     int per_cu = 1;
@@ -223,8 +206,10 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
             per_cu = nb;
         }
     }
-    const int grid = std::max(1, std::min(a.n_tiles, c->cu_count * per_cu));
-    return launch(name, dim3(grid, n_batch, 1), dim3(GS_WG, 1, 1), lds, s, L);
+    const int G = GS_WG / a.lpr;
+    const int nrow = kind == 1 ? a.nseg * a.rows : a.rows;
+    const int grid = std::max(1, std::min((nrow + G - 1) / G, c->cu_count * per_cu));
+    return launch(name, dim3(grid, n_batch, 1), dim3(GS_WG, 1, 1), lds, s, a);
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -372,7 +357,6 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
         a.nseg = 1;
         a.accumulate = (k0 > 0) ? 1 : accumulate;
         a.x_aligned = xal && ((k0 * 4) % 16 == 0);
-        if (kk != K) a.row_stride = row_stride;  // sub-row spans: contig is false, one row per tile
         hipError_t e = stream(0, ty, a, (hipStream_t)s, n_batch);
         if (e != hipSuccess) return e;
     }

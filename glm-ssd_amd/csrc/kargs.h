@@ -13,10 +13,9 @@ enum GsType {
 #define GS_WG 256          // threads per workgroup of the streaming kernels (4 wave64)
 #define GS_SEG_MAX 32      // weight matrices (experts) per fused-MoE launch
 #define GS_NT_MAX 8        // activation vectors (tokens) per launch
-#define GS_LD_MAX 12       // 16-byte loads per thread per weight tile (tile <= 48 KiB)
 
 // Matrix-vector work description ("stream" kernels). One launch streams the rows of one or
-// more quantized matrices ("segments") through LDS in tiles of `rt` rows.
+// more quantized matrices ("segments") from HBM.
 //   kind 0 (GEMV):   y[b][r] (+)= W[r] . xq[b]                      seg = 1 (blockIdx.y batches)
 //   kind 1 (GATEUP): h[e][t][r] = swiglu(gate_e[r] . xq[t], up_e[r] . xq[t])
 //   kind 2 (DOWN):   y[t][r] += sum_e w[t][e] * (down_e[r] . hq[e][t])
@@ -38,15 +37,9 @@ struct StreamArgs {
     float lim;                       // SwiGLU clamp (<= 0: none)
     int row_bytes;                   // bytes of one row's data
     int nu;                          // q8_1 units (32 elements) per row = K/32
-    int lpr;                         // lanes per row (16, 32 or 64)
-    int upl;                         // units per lane = ceil(nu/lpr)
-    int rt;                          // rows per tile
-    int n_row_tiles;                 // ceil(rows/rt)
-    int n_tiles;                     // total tiles (GATEUP: nseg * n_row_tiles)
-    int contig;                      // rows of a tile are one contiguous span (row_stride == row_bytes)
+    int lpr;                         // lanes per row group (16, 32 or 64)
+    int upl;                         // units per lane = ceil(segments*nu/lpr)
     int x_aligned;                   // x and x_stride allow 16-byte loads
-    int lds_tile;                    // bytes reserved for one tile (per segment span: span_pitch)
-    int span_pitch;                  // LDS bytes between segment spans of a tile
 };
 
 // Whole-tensor dequantization

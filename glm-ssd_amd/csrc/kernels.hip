@@ -82,21 +82,56 @@ __device__ __forceinline__ float swiglu(float g, float u, float lim) { // ops.cu
 // =============================================================================================
 // Streaming matrix-vector kernel (GEMV / fused MoE gate-up / fused MoE down).
 //
-// Work is cut into tiles of `rt` rows. Per tile each segment (matrix) contributes one span of
-// bytes; spans are copied HBM -> VGPR -> LDS with aligned 16-byte loads (whatever the block
-// alignment), the next tile's loads are issued before the current tile is decoded, so one tile
-// per workgroup is always in flight. Lanes are split into groups of `lpr` lanes; a group owns a
-// row of the tile at a time and each lane owns the same `upl` 32-element units of every row,
-// so its q8_1 activation units stay in registers for the whole launch. Row partials are summed
-// across the group with DPP.
+// Lanes form groups of `lpr` (16, 32 or 64) lanes; a group computes one output row at a time and
+// every lane owns the same `upl` 32-element units of every row it visits, so the lane's q8_1
+// activation units are quantized once (workgroup prologue, through LDS) and then stay in VGPRs.
+// Weight bytes go straight from HBM to VGPRs with unaligned 8/16-byte loads; rows are software-
+// pipelined PF deep (the loads of row i+PF are issued before row i is decoded). Row partials are
+// summed across the group with DPP. A "row" spans several matrices for the fused MoE kernels:
+//   kind 0 GEMV:    units of one matrix row
+//   kind 1 GATEUP:  units of gate_e[r] then up_e[r] (two sums, SwiGLU epilogue)
+//   kind 2 DOWN:    units of down_e[r] for every expert e of the batch (one weighted sum)
 // =============================================================================================
+template <class F, int UMAX>
+__device__ __forceinline__ constexpr int pf_depth() {
+    return F::RAW * UMAX <= 16 ? 4 : (F::RAW * UMAX <= 36 ? 2 : 1);
+}
+
+// Load activation unit (vector v, unit up) from the LDS q8_1 staging area.
+__device__ __forceinline__ XU load_xu(const uint8_t *xq, const uint32_t *xm, int K, int nu, int v, int up, float scale,
+                                      bool valid) {
+    XU z;
+    if (valid && scale != 0.f) {
+        const uint4 *src = (const uint4 *)(xq + (size_t)v * K + 32 * up);
+        const uint4 lo = src[0], hi = src[1];
+        z.q[0] = lo.x; z.q[1] = lo.y; z.q[2] = lo.z; z.q[3] = lo.w;
+        z.q[4] = hi.x; z.q[5] = hi.y; z.q[6] = hi.z; z.q[7] = hi.w;
+        const int mi = v * nu + up;
+        z.D = __builtin_bit_cast(float, xm[2 * mi]) * scale;
+        const uint32_t ss = xm[2 * mi + 1];
+        z.slo = (int)(int16_t)(ss & 0xffff);
+        z.shi = (int)(int16_t)(ss >> 16);
+    } else {   // padding unit or routing weight 0: contributes nothing
+#pragma unroll
+        for (int i = 0; i < 8; i++) z.q[i] = 0;
+        z.D = 0.f;
+        z.slo = z.shi = 0;
+    }
+    return z;
+}
+
+// UMAX = weight units per lane per row. GEMV / DOWN: units j of the (concatenated) row.
+// GATEUP: j < UMAX/2 are units of the gate row, j >= UMAX/2 the same units of the up row, so
+// the lane holds UMAX/2 activation units.
 template <class F, int KIND, int NV, int UMAX>
-__device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t cps_magic, int cps) {
+__device__ __forceinline__ void stream_body(const StreamArgs &a) {
+    constexpr int PF = pf_depth<F, UMAX>();
+    constexpr int UX = KIND == 1 ? UMAX / 2 : UMAX;       // activation units per lane
+    static_assert(KIND != 1 || UMAX % 2 == 0, "gate/up needs an even unit count");
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x;
     uint8_t *tab = smem;
-    uint8_t *work = smem + ((F::TAB + 15) & ~15);
-    F::init(tab, tid);
+    uint8_t *xq = smem + ((F::TAB + 15) & ~15);
 
     const uint8_t *wb = a.w0[0];
     const float *x = a.x;
@@ -106,13 +141,78 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t cps_ma
         x += (int64_t)blockIdx.y * a.x_bs;
         y += (int64_t)blockIdx.y * a.y_bs;
     }
-    const int K = a.K, nu = a.nu, nv = a.nvec;
-    const int NS = KIND == 0 ? 1 : (KIND == 1 ? 2 : a.nseg);
-    const int nxv = KIND == 2 ? a.nseg * nv : nv;
+    const int K = a.K, nu = a.nu, nv = a.nvec, rows = a.rows;
+    const int lpr = a.lpr, lane = tid & (lpr - 1), grp = tid / lpr, G = GS_WG / lpr;
+    const int tot = KIND == 2 ? a.nseg * nu : nu;          // units along the (concatenated) row
+    const int nrow = KIND == 1 ? a.nseg * rows : rows;     // output rows of this launch
+    const int ngroups = gridDim.x * G;
+    const int gid = blockIdx.x * G + grp;
+    const int64_t rs = a.row_stride;
 
-    // ---- prologue: q8_1-quantize every activation vector into LDS ----------------------------
-    uint8_t *xq = work;
-    uint32_t *xm = (uint32_t *)(work + (size_t)nxv * K);
+    // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
+    int uspan[UX], usub[UX];
+    uint32_t uoff[UX];
+    bool uval[UX];
+#pragma unroll
+    for (int j = 0; j < UX; j++) {
+        const int u0 = lane + lpr * j;
+        const bool valid = j < a.upl && u0 < tot;
+        const int u = valid ? u0 : (lane < tot ? lane : 0);
+        const int s = KIND == 2 ? u / nu : 0;
+        const int up = u - s * nu;
+        uval[j] = valid;
+        uspan[j] = s;
+        uoff[j] = F::off(up);
+        usub[j] = F::sub(up);
+    }
+    const uint8_t *ubase[UX];
+#pragma unroll
+    for (int j = 0; j < UX; j++) ubase[j] = (KIND == 2 ? a.w0[uspan[j]] : wb) + uoff[j];
+
+    // pipeline slots: output row (GATEUP: expert and row) advance by PF*ngroups rows
+    const int step = PF * ngroups;
+    int srow[PF], se[PF], sr[PF];
+    typename F::Raw R[PF][UMAX];
+    auto load_slot = [&](int p) {
+        if (KIND == 1) {
+            const int64_t roff = (int64_t)sr[p] * rs;
+            const uint8_t *g = a.w0[se[p]] + roff, *u = a.w1[se[p]] + roff;
+#pragma unroll
+            for (int j = 0; j < UX; j++) {
+                F::load(g + uoff[j], usub[j], R[p][j]);
+                F::load(u + uoff[j], usub[j], R[p][UX + j]);
+            }
+        } else {
+            const int64_t roff = (int64_t)srow[p] * rs;
+#pragma unroll
+            for (int j = 0; j < UX; j++) F::load(ubase[j] + roff, usub[j], R[p][j]);
+        }
+    };
+    auto advance = [&](int p) {
+        srow[p] += step;
+        if (KIND == 1) {
+            sr[p] += step;
+            while (sr[p] >= rows) {
+                sr[p] -= rows;
+                se[p]++;
+            }
+        }
+    };
+    // the first PF rows' weight loads go out before the activation prologue
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+        srow[p] = gid + p * ngroups;
+        if (KIND == 1) {
+            se[p] = srow[p] / rows;
+            sr[p] = srow[p] - se[p] * rows;
+        }
+        if (srow[p] < nrow) load_slot(p);
+    }
+
+    // ---- prologue: tables + q8_1 quantization of every activation vector into LDS ----------
+    F::init(tab, tid);
+    const int nxv = KIND == 2 ? a.nseg * nv : nv;
+    uint32_t *xm = (uint32_t *)(xq + (size_t)nxv * K);
     for (int i = tid; i < nxv * nu; i += GS_WG) {
         const int v = i / nu, u = i - v * nu;
         const float *src = (KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u;
@@ -126,176 +226,78 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t cps_ma
         xm[2 * i + 1] = ((uint32_t)q.slo & 0xffffu) | ((uint32_t)q.shi << 16);
     }
     __syncthreads();
-
-    const int lpr = a.lpr, lane = tid & (lpr - 1), grp = tid / lpr, G = GS_WG / lpr;
-    const int tot = NS * nu;
-    XU xr[UMAX][NV];
-    int uspan[UMAX], usub[UMAX];
-    uint32_t uoff[UMAX];
-    bool uval[UMAX];
+    XU xr[UX][NV];
 #pragma unroll
-    for (int j = 0; j < UMAX; j++) {
-        const int u = lane + lpr * j;
-        const bool valid = j < a.upl && u < tot;
-        const int s = valid ? u / nu : 0, up = valid ? u - s * nu : 0;
-        uval[j] = valid;
-        uspan[j] = s;
-        uoff[j] = F::off(up);
-        usub[j] = F::sub(up);
+    for (int j = 0; j < UX; j++) {
+        const int up = lane + lpr * j - uspan[j] * nu;
 #pragma unroll
         for (int t = 0; t < NV; t++) {
-            const int v = KIND == 2 ? s * nv + t : t;
-            XU z;
-            if (valid && t < nv) {
-                const uint4 *src = (const uint4 *)(xq + (size_t)v * K + 32 * up);
-                const uint4 lo = src[0], hi = src[1];
-                z.q[0] = lo.x; z.q[1] = lo.y; z.q[2] = lo.z; z.q[3] = lo.w;
-                z.q[4] = hi.x; z.q[5] = hi.y; z.q[6] = hi.z; z.q[7] = hi.w;
-                const int mi = v * nu + up;
-                z.D = __builtin_bit_cast(float, xm[2 * mi]);
-                const uint32_t ss = xm[2 * mi + 1];
-                z.slo = (int)(int16_t)(ss & 0xffff);
-                z.shi = (int)(int16_t)(ss >> 16);
-                if (KIND == 2) {
-                    const float w = a.wt[t][s];
-                    if (w == 0.f) {
-                        z.D = 0.f;
-#pragma unroll
-                        for (int i = 0; i < 8; i++) z.q[i] = 0;
-                        z.slo = z.shi = 0;
-                    } else {
-                        z.D *= w;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) z.q[i] = 0;
-                z.D = 0.f;
-                z.slo = z.shi = 0;
-            }
-            xr[j][t] = z;
+            const int v = KIND == 2 ? uspan[j] * nv + t : t;
+            const float w = KIND == 2 ? a.wt[t][uspan[j]] : 1.f;   // routing weight folded into D
+            xr[j][t] = load_xu(xq, xm, K, nu, v, up, w, uval[j] && t < nv);
         }
     }
-    __syncthreads();   // the tile buffer below reuses the activation area
 
-    // ---- tile loop ---------------------------------------------------------------------------
-    const int rbytes = a.row_bytes, pitch = a.span_pitch;
-    const int nchunks = NS * cps;
-    auto span_base = [&](int tile, int s, int &r0, int &nr) -> const uint8_t * {
-        int e = 0, rtile = tile;
-        if (KIND == 1) {
-            e = tile / a.n_row_tiles;
-            rtile = tile - e * a.n_row_tiles;
-        }
-        r0 = rtile * a.rt;
-        nr = min(a.rt, a.rows - r0);
-        const uint8_t *b = KIND == 0 ? wb : (KIND == 1 ? (s == 0 ? a.w0[e] : a.w1[e]) : a.w0[s]);
-        return b + (int64_t)r0 * a.row_stride;
-    };
-    uint4 buf[GS_LD_MAX];
-    auto load_tile = [&](int tile) {
+    // ---- row loop, PF rows in flight ---------------------------------------------------------
+    while (srow[0] < nrow) {
 #pragma unroll
-        for (int k = 0; k < GS_LD_MAX; k++) {
-            const int i = tid + GS_WG * k;
-            if (i < nchunks) {
-                const int s = (int)__umulhi((uint32_t)i, cps_magic);
-                const int c = i - s * cps;
-                int r0, nr;
-                const uint8_t *p = span_base(tile, s, r0, nr);
-                const uintptr_t pa = (uintptr_t)p & ~(uintptr_t)15;
-                const int nch = (int)((((uintptr_t)p & 15) + (uintptr_t)nr * rbytes + 15) >> 4);
-                if (c < nch) buf[k] = *(const uint4 *)(pa + 16 * (uintptr_t)c);
-            }
-        }
-    };
-    auto store_tile = [&]() {
+        for (int p = 0; p < PF; p++) {
+            const int rr = srow[p];
+            if (rr < nrow) {
+                const int e = KIND == 1 ? se[p] : 0, r = KIND == 1 ? sr[p] : rr;
+                float acc0[NV], acc1[NV];
 #pragma unroll
-        for (int k = 0; k < GS_LD_MAX; k++) {
-            const int i = tid + GS_WG * k;
-            if (i < nchunks) {
-                const int s = (int)__umulhi((uint32_t)i, cps_magic);
-                const int c = i - s * cps;
-                *(uint4 *)(work + s * pitch + 16 * c) = buf[k];
-            }
-        }
-    };
-
-    int tile = blockIdx.x;
-    if (tile < a.n_tiles) load_tile(tile);
-    for (; tile < a.n_tiles; tile += gridDim.x) {
-        store_tile();
-        __syncthreads();
-        const int next = tile + gridDim.x;
-        if (next < a.n_tiles) load_tile(next);
-
-        int r0 = 0, nr = 0, e = 0;
-        if (KIND == 1) e = tile / a.n_row_tiles;
-        uint32_t ubase[UMAX];
+                for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
 #pragma unroll
-        for (int j = 0; j < UMAX; j++) {
-            const uint8_t *p = span_base(tile, uspan[j], r0, nr);
-            ubase[j] = (uint32_t)(uspan[j] * pitch) + (uint32_t)((uintptr_t)p & 15) + uoff[j];
-        }
-        for (int i = grp; i < nr; i += G) {
-            float acc0[NV], acc1[NV];
-#pragma unroll
-            for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
-#pragma unroll
-            for (int j = 0; j < UMAX; j++) {
-                if (uval[j]) {
-                    float r[NV];
-#pragma unroll
-                    for (int t = 0; t < NV; t++) r[t] = 0.f;
-                    F::template dot<NV>(work, ubase[j] + (uint32_t)(i * rbytes), usub[j], tab, xr[j], nv, r);
-#pragma unroll
-                    for (int t = 0; t < NV; t++) {
-                        if (KIND == 1 && uspan[j] == 1) acc1[t] += r[t];
-                        else acc0[t] += r[t];
-                    }
+                for (int j = 0; j < UX; j++) {
+                    F::template dot<NV>(R[p][j], usub[j], tab, xr[j], nv, acc0);
+                    if (KIND == 1) F::template dot<NV>(R[p][UX + j], usub[j], tab, xr[j], nv, acc1);
                 }
-            }
-#pragma unroll
-            for (int t = 0; t < NV; t++) {
-                acc0[t] = group_sum(acc0[t], lpr);
-                if (KIND == 1) acc1[t] = group_sum(acc1[t], lpr);
-            }
-            if (lane == lpr - 1) {
-                const int row = r0 + i;
+                advance(p);
+                if (srow[p] < nrow) load_slot(p);
 #pragma unroll
                 for (int t = 0; t < NV; t++) {
-                    if (t < nv) {
-                        if (KIND == 0) {
-                            float *dst = y + (int64_t)t * a.y_stride + row;
-                            *dst = a.accumulate ? *dst + acc0[t] : acc0[t];
-                        } else if (KIND == 1) {
-                            y[((int64_t)e * nv + t) * a.rows + row] = swiglu(acc0[t], acc1[t], a.lim);
-                        } else {
-                            y[(int64_t)t * a.y_stride + row] += acc0[t];
+                    acc0[t] = group_sum(acc0[t], lpr);
+                    if (KIND == 1) acc1[t] = group_sum(acc1[t], lpr);
+                }
+                if (lane == lpr - 1) {
+#pragma unroll
+                    for (int t = 0; t < NV; t++) {
+                        if (t < nv) {
+                            if (KIND == 0) {
+                                float *dst = y + (int64_t)t * a.y_stride + rr;
+                                *dst = a.accumulate ? *dst + acc0[t] : acc0[t];
+                            } else if (KIND == 1) {
+                                y[((int64_t)e * nv + t) * rows + r] = swiglu(acc0[t], acc1[t], a.lim);
+                            } else {
+                                y[(int64_t)t * a.y_stride + rr] += acc0[t];
+                            }
                         }
                     }
                 }
             }
         }
-        __syncthreads();
     }
 }
 
-// cps (max 16-byte chunks per span) and its division magic ride in the dynamic part of the
-// launch: they are appended after StreamArgs by the host.
-struct StreamLaunch {
-    StreamArgs a;
-    uint32_t cps_magic;
-    int cps;
-};
-
-#define GS_STREAM_KERNEL(F, NAME, KIND, NV)                                                      \
-    extern "C" __global__ void __launch_bounds__(GS_WG) gs_k_stream_##NAME##_##KIND##_##NV(StreamLaunch L) { \
-        stream_body<F, KIND, NV, 8 / NV>(L.a, L.cps_magic, L.cps);                              \
+#define GS_STREAM_KERNEL(F, NAME, KIND, NV, UM)                                                  \
+    extern "C" __global__ void __launch_bounds__(GS_WG)                                         \
+        gs_k_stream_##NAME##_##KIND##_##NV##_##UM(StreamArgs a) {                                \
+        stream_body<F, KIND, NV, UM>(a);                                                        \
     }
-#define GS_STREAM_NV(F, NAME, KIND)                                                             \
-    GS_STREAM_KERNEL(F, NAME, KIND, 1) GS_STREAM_KERNEL(F, NAME, KIND, 2)                       \
-    GS_STREAM_KERNEL(F, NAME, KIND, 4) GS_STREAM_KERNEL(F, NAME, KIND, 8)
-#define GS_STREAM_ALL(F, NAME) GS_STREAM_NV(F, NAME, 0) GS_STREAM_NV(F, NAME, 1) GS_STREAM_NV(F, NAME, 2)
+// instantiated (activation vectors, weight units per lane) pairs; host.cpp keeps the same table
+#define GS_STREAM_MV(F, NAME, KIND)                                                             \
+    GS_STREAM_KERNEL(F, NAME, KIND, 1, 2) GS_STREAM_KERNEL(F, NAME, KIND, 1, 4)                 \
+    GS_STREAM_KERNEL(F, NAME, KIND, 1, 6) GS_STREAM_KERNEL(F, NAME, KIND, 1, 8)                 \
+    GS_STREAM_KERNEL(F, NAME, KIND, 2, 2)                                                       \
+    GS_STREAM_KERNEL(F, NAME, KIND, 2, 4) GS_STREAM_KERNEL(F, NAME, KIND, 4, 1)                 \
+    GS_STREAM_KERNEL(F, NAME, KIND, 4, 2) GS_STREAM_KERNEL(F, NAME, KIND, 8, 1)
+#define GS_STREAM_GU(F, NAME)                                                                   \
+    GS_STREAM_KERNEL(F, NAME, 1, 1, 2) GS_STREAM_KERNEL(F, NAME, 1, 1, 4)                       \
+    GS_STREAM_KERNEL(F, NAME, 1, 1, 8) GS_STREAM_KERNEL(F, NAME, 1, 2, 2)                       \
+    GS_STREAM_KERNEL(F, NAME, 1, 2, 4) GS_STREAM_KERNEL(F, NAME, 1, 4, 2)                       \
+    GS_STREAM_KERNEL(F, NAME, 1, 4, 4) GS_STREAM_KERNEL(F, NAME, 1, 8, 2)
+#define GS_STREAM_ALL(F, NAME) GS_STREAM_MV(F, NAME, 0) GS_STREAM_GU(F, NAME) GS_STREAM_MV(F, NAME, 2)
 
 // One code object per format keeps the build parallel: the Makefile compiles this file once
 // per GS_STREAM_TYPE (F-struct, type id) and once with GS_COMMON for the kernels below.
