@@ -188,8 +188,21 @@ __device__ __forceinline__ void deq8_bf16(const uint8_t *b, int, float *v) {
 // One q8_1 activation unit (32 elements) in registers.
 struct XU {
     uint32_t q[8];   // int8 x 32
-    float D;         // f16-rounded scale (times the routing weight for MoE down)
+    uint32_t nq[8];  // -q per byte (only formats with NEG_X read it)
+    float D;         // f16-rounded scale (x the routing weight for MoE down, x the format's XSCALE)
     int slo, shi;    // sum of q over elements 0..15 / 16..31
+};
+// Traits defaults: formats opt in to negated activations / a folded constant scale.
+template <class F, class = void> struct NegX { static constexpr bool value = false; };
+template <class F> struct NegX<F, decltype((void)F::NEG_X, void())> { static constexpr bool value = F::NEG_X; };
+template <class F, class = void> struct XScale { static constexpr float value = 1.0f; };
+template <class F> struct XScale<F, decltype((void)F::XSCALE, void())> { static constexpr float value = F::XSCALE; };
+
+// Formats without lookup tables: empty table hooks.
+struct NoTable {
+    struct TabReg {};
+    __device__ static __forceinline__ void tab_load(int, TabReg &) {}
+    __device__ static __forceinline__ void tab_store(int, const TabReg &) {}
 };
 
 // Per-format geometry of a unit (32 elements) within a row: byte offset of its block and the
@@ -220,36 +233,34 @@ __device__ __forceinline__ uint32_t ldg2(const uint8_t *p) { return *(const uint
 
 // Each format: Raw = the registers one unit needs from memory; load() issues the loads for unit
 // `j` of the block at `b`; dot() decodes Raw and accumulates r[t] += W_unit . x_t for t < nv.
-struct FQ8_0 : UnitGeom<32, 34> {
+struct FQ8_0 : UnitGeom<32, 34>, NoTable {
     static constexpr int TYPE = GS_Q8_0, QK = 32, BB = 34, TAB = 0, RAW = 9;
     struct Raw { uint4 lo, hi; uint32_t d; };
-    __device__ static void init(uint8_t *, int) {}
     __device__ static __forceinline__ void load(const uint8_t *b, int, Raw &w) {
         w.d = ldg2(b);
         w.lo = ldg16(b + 2);
         w.hi = ldg16(b + 18);
     }
-    template <int NV>
+    template <int NV, bool XNEG = false>
     __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {
         const float d = h2f(w.d);
         const uint32_t q[8] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w, w.hi.x, w.hi.y, w.hi.z, w.hi.w};
 #pragma unroll
         for (int t = 0; t < NV; t++)
-            if (t < nv) r[t] += (d * x[t].D) * (float)dot8(q, x[t].q);
+            if (NV == 1 || t < nv) r[t] += (d * x[t].D) * (float)dot8(q, x[t].q);
     }
 };
 
-struct FQ4_K : UnitGeom<256, 144> {
+struct FQ4_K : UnitGeom<256, 144>, NoTable {
     static constexpr int TYPE = GS_Q4_K, QK = 256, BB = 144, TAB = 0, RAW = 12;
     struct Raw { uint4 hd, lo, hi; };   // bytes 0..15 (d, dmin, scales[12]); 32 quant bytes
-    __device__ static void init(uint8_t *, int) {}
     __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
         w.hd = ldg16(b);
         w.lo = ldg16(b + 16 + 32 * (j >> 1));
         w.hi = ldg16(b + 32 + 32 * (j >> 1));
     }
-    template <int NV>
+    template <int NV, bool XNEG = false>
     __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {
         const float d = h2f(w.hd.x & 0xffff), dmin = h2f(w.hd.x >> 16);
@@ -272,14 +283,13 @@ struct FQ4_K : UnitGeom<256, 144> {
         const float ds = d * (float)sc, dm = dmin * (float)mn;
 #pragma unroll
         for (int t = 0; t < NV; t++)
-            if (t < nv) r[t] += x[t].D * (ds * (float)dot8(q, x[t].q) - dm * (float)(x[t].slo + x[t].shi));
+            if (NV == 1 || t < nv) r[t] += x[t].D * (ds * (float)dot8(q, x[t].q) - dm * (float)(x[t].slo + x[t].shi));
     }
 };
 
-struct FQ6_K : UnitGeom<256, 210> {
+struct FQ6_K : UnitGeom<256, 210>, NoTable {
     static constexpr int TYPE = GS_Q6_K, QK = 256, BB = 210, TAB = 0, RAW = 18;
     struct Raw { uint4 l0, l1, h0, h1; uint32_t sc, d; };
-    __device__ static void init(uint8_t *, int) {}
     __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
         const int half = j >> 2, quarter = j & 3;
         const uint8_t *ql = b + 64 * half + 32 * (quarter & 1), *qh = b + 128 + 32 * half;
@@ -290,7 +300,7 @@ struct FQ6_K : UnitGeom<256, 210> {
         w.sc = ldg2(b + 192 + 8 * half + 2 * quarter);
         w.d = ldg2(b + 208);
     }
-    template <int NV>
+    template <int NV, bool XNEG = false>
     __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {
         const int quarter = j & 3;
@@ -318,61 +328,85 @@ struct FQ6_K : UnitGeom<256, 210> {
 };
 
 // IQ2_XXS: the 256-entry grid (2 KiB) and a 128-entry table of v_perm_b32 selectors (1 KiB)
-// live in LDS. A selector picks, per byte, the grid byte (sel = i) or its negation (sel = i+4)
-// from the pair {-grid, grid}; -grid bytes come from one subtraction (0x01010100 - grid) since
-// every grid byte is nonzero.
+// live in LDS at fixed addresses (folded into the ds_read offsets). The signs are applied to the
+// activations, not the weights: a selector picks, per byte, q (sel = i) or -q (sel = i+4) from
+// the pair {-q, q}, and -q is computed once per activation unit (XU::nq), so a group of 8
+// elements costs 2 table reads, 2 v_perm_b32 and 2 v_dot4_i32_i8.
+__shared__ uint2 gs_iq2xxs_grid_lds[256];
+__shared__ uint2 gs_iq2xxs_sel_lds[128];
+
 struct FIQ2_XXS : UnitGeom<256, 66> {
-    static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 2048 + 1024, RAW = 3;
+    static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 0, RAW = 3;
+    static constexpr bool NEG_X = true;
+    static constexpr float XSCALE = 0.25f;   // the format's /4, folded into the activation scale
     struct Raw { uint2 a; uint32_t d; };
-    __device__ static void init(uint8_t *tab, int tid) {
-        uint64_t *g = (uint64_t *)tab;
-        for (int i = tid; i < 256; i += GS_WG) g[i] = iq2xxs_grid[i];
-        uint32_t *s = (uint32_t *)(tab + 2048);
-        for (int i = tid; i < 128; i += GS_WG) {
-            const uint32_t k = ksigns((uint32_t)i);
+    // table setup split in two so the global read can be issued before the weight prefetch
+    struct TabReg { uint64_t g; };
+    __device__ static __forceinline__ void tab_load(int tid, TabReg &r) { r.g = tid < 256 ? iq2xxs_grid[tid] : 0; }
+    __device__ static __forceinline__ void tab_store(int tid, const TabReg &r) {
+        if (tid < 256) gs_iq2xxs_grid_lds[tid] = make_uint2((uint32_t)r.g, (uint32_t)(r.g >> 32));
+        if (tid < 128) {
+            const uint32_t k = ksigns((uint32_t)tid);
             uint32_t lo = 0x03020100u, hi = 0x03020100u;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 lo += ((k >> b) & 1u) << (8 * b + 2);
                 hi += ((k >> (b + 4)) & 1u) << (8 * b + 2);
             }
-            s[2 * i] = lo;
-            s[2 * i + 1] = hi;
+            gs_iq2xxs_sel_lds[tid] = make_uint2(lo, hi);
         }
     }
     __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
         w.d = ldg2(b);
         w.a = ldg8(b + 2 + 8 * j);
     }
-    template <int NV>
-    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *tab, const XU (&x)[NV], int nv,
+    // XNEG: the activation units carry -q (signs applied on the activation side, 2 ops per 8
+    // elements); otherwise the signs are applied to the grid bytes (one more op per 4 elements,
+    // 8 fewer registers per activation unit).
+    template <int NV, bool XNEG = true>
+    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {
-        const float db = h2f(w.d) * (0.5f + (float)(w.a.y >> 28)) * 0.25f;
-        const uint2 *grid = (const uint2 *)tab;
-        const uint2 *sel = (const uint2 *)(tab + 2048);
-        uint32_t q[8];
+        // db = d * (0.5 + s) * 0.25 (lib.rs:279); the 0.25 is already in x.D
+        const float db = h2f(w.d) * (0.5f + (float)(w.a.y >> 28));
+        uint2 g[4], s[4];
 #pragma unroll
         for (int l = 0; l < 4; l++) {
-            const uint2 g = grid[(w.a.x >> (8 * l)) & 0xff];
-            const uint2 s = sel[(w.a.y >> (7 * l)) & 127];
-            q[2 * l] = __builtin_amdgcn_perm(0x01010100u - g.x, g.x, s.x);
-            q[2 * l + 1] = __builtin_amdgcn_perm(0x01010100u - g.y, g.y, s.y);
+            g[l] = gs_iq2xxs_grid_lds[(w.a.x >> (8 * l)) & 0xff];
+            s[l] = gs_iq2xxs_sel_lds[(w.a.y >> (7 * l)) & 127];
+        }
+        if (!XNEG) {   // signed grid: every grid byte is nonzero, so 0x01010100 - g negates bytewise
+#pragma unroll
+            for (int l = 0; l < 4; l++) {
+                g[l].x = __builtin_amdgcn_perm(0x01010100u - g[l].x, g[l].x, s[l].x);
+                g[l].y = __builtin_amdgcn_perm(0x01010100u - g[l].y, g[l].y, s[l].y);
+            }
         }
 #pragma unroll
-        for (int t = 0; t < NV; t++)
-            if (t < nv) r[t] += (db * x[t].D) * (float)dot8(q, x[t].q);
+        for (int t = 0; t < NV; t++) {
+            if (NV == 1 || t < nv) {
+                int acc = 0;
+#pragma unroll
+                for (int l = 0; l < 4; l++) {
+                    const uint32_t q0 = XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l], x[t].q[2 * l], s[l].x) : x[t].q[2 * l];
+                    const uint32_t q1 =
+                        XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l + 1], x[t].q[2 * l + 1], s[l].y) : x[t].q[2 * l + 1];
+                    acc = __builtin_amdgcn_sdot4((int)g[l].x, (int)q0, acc, false);
+                    acc = __builtin_amdgcn_sdot4((int)g[l].y, (int)q1, acc, false);
+                }
+                r[t] += (db * x[t].D) * (float)acc;
+            }
+        }
     }
 };
 
 // Generic path for the remaining types: exact f32 decode of the unit straight from global
 // memory, f32 dot with the dequantized activations (D * q). Slower; used for the non-hot formats.
 template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float *)>
-struct FGeneric : UnitGeom<QK_, BB_> {
+struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
     static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0, RAW = 2;
     struct Raw { const uint8_t *p; };
-    __device__ static void init(uint8_t *, int) {}
     __device__ static __forceinline__ void load(const uint8_t *b, int, Raw &w) { w.p = b; }
-    template <int NV>
+    template <int NV, bool XNEG = false>
     __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {
         float v[32];

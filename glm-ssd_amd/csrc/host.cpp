@@ -145,7 +145,7 @@ bool geometry(int ty, int &qk, int &bb) {
 int ggml_block_elems(int ty) {  // elements per ggml block (1 for plain types)
     return ty == GS_F32 || ty == GS_F16 || ty == GS_BF16 ? 1 : (ty == GS_Q8_0 ? 32 : 256);
 }
-int table_bytes(int ty) { return ty == GS_IQ2_XXS ? 2048 + 1024 : 0; }
+int table_bytes(int) { return 0; }  // lookup tables are static LDS arrays of their kernels
 
 // Plan and launch one streaming kernel (kind 0 GEMV, 1 MoE gate/up, 2 MoE down).
 hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 1) {
@@ -188,6 +188,10 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     const int tab = (table_bytes(ty) + 15) & ~15;
     const size_t lds = (size_t)tab + (size_t)(kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
     if (lds > std::min<size_t>(c->max_lds, 160 * 1024)) return hipErrorInvalidValue;
+    {
+        static const int dbg = getenv("GLMSSD_STREAM_DBG") ? atoi(getenv("GLMSSD_STREAM_DBG")) : 0;
+        a.dbg = dbg;
+    }
     const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" +
                              std::to_string(NVt) + "_" + std::to_string(best_um);
     hipFunction_t f;
@@ -208,7 +212,15 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     }
     const int G = GS_WG / a.lpr;
     const int nrow = kind == 1 ? a.nseg * a.rows : a.rows;
-    const int grid = std::max(1, std::min((nrow + G - 1) / G, c->cu_count * per_cu));
+    // one workgroup per CU by default: each workgroup pays the activation prologue once, and the
+    // row pipeline inside it supplies the memory parallelism
+    static const int gmult = getenv("GLMSSD_GRID_MULT") ? std::max(1, atoi(getenv("GLMSSD_GRID_MULT"))) : 1;
+    int grid = std::max(1, std::min((nrow + G - 1) / G, c->cu_count * std::min(gmult, per_cu)));
+    if (kind == 1) {   // waves are pinned to experts: at least one per expert, a whole number each
+        const int wpw = GS_WG / 64;
+        const int waves = std::max(grid * wpw, a.nseg) / a.nseg * a.nseg;
+        grid = (waves + wpw - 1) / wpw;
+    }
     return launch(name, dim3(grid, n_batch, 1), dim3(GS_WG, 1, 1), lds, s, a);
 }
 

@@ -92,30 +92,41 @@ __device__ __forceinline__ float swiglu(float g, float u, float lim) { // ops.cu
 //   kind 1 GATEUP:  units of gate_e[r] then up_e[r] (two sums, SwiGLU epilogue)
 //   kind 2 DOWN:    units of down_e[r] for every expert e of the batch (one weighted sum)
 // =============================================================================================
+// Rows in flight per lane group: as many as ~64 VGPRs of raw weight bytes hold (at most 8), so a
+// group's whole share of a decode-sized matrix is requested before the first row is decoded.
+#ifndef GS_PF_REGS
+#define GS_PF_REGS 64
+#endif
 template <class F, int UMAX>
 __device__ __forceinline__ constexpr int pf_depth() {
-    return F::RAW * UMAX <= 16 ? 4 : (F::RAW * UMAX <= 36 ? 2 : 1);
+    constexpr int n = GS_PF_REGS / (F::RAW * UMAX);
+    return n < 1 ? 1 : (n > 8 ? 8 : n);
 }
 
-// Load activation unit (vector v, unit up) from the LDS q8_1 staging area.
+// Load activation unit (vector v, unit up) from the LDS q8_1 staging area; `scale` multiplies D
+// (routing weight and the format's constant factor); a zero scale or padding unit yields zeros.
+template <class F, bool XNEG>
 __device__ __forceinline__ XU load_xu(const uint8_t *xq, const uint32_t *xm, int K, int nu, int v, int up, float scale,
                                       bool valid) {
     XU z;
-    if (valid && scale != 0.f) {
-        const uint4 *src = (const uint4 *)(xq + (size_t)v * K + 32 * up);
-        const uint4 lo = src[0], hi = src[1];
-        z.q[0] = lo.x; z.q[1] = lo.y; z.q[2] = lo.z; z.q[3] = lo.w;
-        z.q[4] = hi.x; z.q[5] = hi.y; z.q[6] = hi.z; z.q[7] = hi.w;
-        const int mi = v * nu + up;
-        z.D = __builtin_bit_cast(float, xm[2 * mi]) * scale;
-        const uint32_t ss = xm[2 * mi + 1];
-        z.slo = (int)(int16_t)(ss & 0xffff);
-        z.shi = (int)(int16_t)(ss >> 16);
-    } else {   // padding unit or routing weight 0: contributes nothing
+    const bool live = valid && scale != 0.f;
+    const int mi = v * nu + up;
+    const uint4 *src = (const uint4 *)(xq + (size_t)v * K + 32 * (live ? up : 0));
+    const uint4 lo = src[0], hi = src[1];
+    const uint32_t dbits = xm[live ? 2 * mi : 0], ss = xm[live ? 2 * mi + 1 : 1];
+    z.q[0] = live ? lo.x : 0u; z.q[1] = live ? lo.y : 0u; z.q[2] = live ? lo.z : 0u; z.q[3] = live ? lo.w : 0u;
+    z.q[4] = live ? hi.x : 0u; z.q[5] = live ? hi.y : 0u; z.q[6] = live ? hi.z : 0u; z.q[7] = live ? hi.w : 0u;
+    z.D = live ? __builtin_bit_cast(float, dbits) * scale * XScale<F>::value : 0.f;
+    z.slo = live ? (int)(int16_t)(ss & 0xffff) : 0;
+    z.shi = live ? (int)(int16_t)(ss >> 16) : 0;
+    if (XNEG) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) z.q[i] = 0;
-        z.D = 0.f;
-        z.slo = z.shi = 0;
+        for (int i = 0; i < 8; i++) {   // bytewise -q (|q| <= 127, no overflow)
+            uint32_t n = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) n |= ((uint32_t)(-(int)(int8_t)(z.q[i] >> (8 * b))) & 0xffu) << (8 * b);
+            z.nq[i] = n;
+        }
     }
     return z;
 }
@@ -127,6 +138,7 @@ template <class F, int KIND, int NV, int UMAX>
 __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     constexpr int PF = pf_depth<F, UMAX>();
     constexpr int UX = KIND == 1 ? UMAX / 2 : UMAX;       // activation units per lane
+    constexpr bool XNEG = NegX<F>::value && UX * NV <= 4;  // -q in registers only while it is cheap
     static_assert(KIND != 1 || UMAX % 2 == 0, "gate/up needs an even unit count");
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x;
@@ -142,12 +154,28 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
         y += (int64_t)blockIdx.y * a.y_bs;
     }
     const int K = a.K, nu = a.nu, nv = a.nvec, rows = a.rows;
-    const int lpr = a.lpr, lane = tid & (lpr - 1), grp = tid / lpr, G = GS_WG / lpr;
+    const int lpr = a.lpr, lane = tid & (lpr - 1), G = GS_WG / lpr;
     const int tot = KIND == 2 ? a.nseg * nu : nu;          // units along the (concatenated) row
-    const int nrow = KIND == 1 ? a.nseg * rows : rows;     // output rows of this launch
-    const int ngroups = gridDim.x * G;
-    const int gid = blockIdx.x * G + grp;
+    // Lane groups: GATEUP pins each wave to one expert (its pointers become scalar loads) and the
+    // wave's groups stride over that expert's rows; other kinds stride over all rows.
+    const int gpw = 64 / lpr;                                   // groups per wave
+    const int wave_all = blockIdx.x * (GS_WG / 64) + (tid >> 6);
+    const int nwaves_all = gridDim.x * (GS_WG / 64);
+    const int gin = (tid & 63) / lpr;                           // group within the wave
+    int ge = 0, ngroups, gid, nrow;
+    if (KIND == 1) {
+        ge = __builtin_amdgcn_readfirstlane(wave_all % a.nseg);
+        const int wpe = nwaves_all / a.nseg;                    // waves per expert
+        ngroups = wpe * gpw;
+        gid = (wave_all / a.nseg) * gpw + gin;
+        nrow = wave_all >= wpe * a.nseg ? 0 : rows;             // leftover waves idle
+    } else {
+        ngroups = nwaves_all * gpw;
+        gid = wave_all * gpw + gin;
+        nrow = rows;
+    }
     const int64_t rs = a.row_stride;
+    const uint8_t *wg = KIND == 1 ? a.w0[ge] : nullptr, *wu = KIND == 1 ? a.w1[ge] : nullptr;
 
     // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
     int uspan[UX], usub[UX];
@@ -167,63 +195,77 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     }
     const uint8_t *ubase[UX];
 #pragma unroll
-    for (int j = 0; j < UX; j++) ubase[j] = (KIND == 2 ? a.w0[uspan[j]] : wb) + uoff[j];
+    for (int j = 0; j < UX; j++) ubase[j] = wb + uoff[j];
+    if (KIND == 2) {   // expert pointers through scalar loads, selected per unit
+        for (int s = 0; s < a.nseg; s++) {
+            const uint8_t *ps = a.w0[s];
+#pragma unroll
+            for (int j = 0; j < UX; j++)
+                if (uspan[j] == s) ubase[j] = ps + uoff[j];
+        }
+    }
 
-    // pipeline slots: output row (GATEUP: expert and row) advance by PF*ngroups rows
+    // ---- prologue loads first: activation units and lookup tables are requested before the
+    // weight prefetch so waiting for them (vmcnt counts in issue order) never waits on weights
+    constexpr int XQ = 2;                                       // activation units per thread in flight
+    const int nxv = KIND == 2 ? a.nseg * nv : nv;
+    const int nxu = (a.dbg & 1) ? 0 : nxv * nu;
+    float xf[XQ][32];
+#pragma unroll
+    for (int k = 0; k < XQ; k++) {
+        const int i = tid + GS_WG * k;
+        if (i < nxu) {
+            const int v = i / nu, u = i - v * nu;
+            const float *src = (KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u;
+            load32(src, a.x_aligned != 0, xf[k]);
+        }
+    }
+    typename F::TabReg treg;
+    F::tab_load(tid, treg);
+
+    // pipeline slots: output row advances by PF*ngroups rows
     const int step = PF * ngroups;
-    int srow[PF], se[PF], sr[PF];
+    int srow[PF];
     typename F::Raw R[PF][UMAX];
     auto load_slot = [&](int p) {
+        const int64_t roff = (int64_t)srow[p] * rs;
         if (KIND == 1) {
-            const int64_t roff = (int64_t)sr[p] * rs;
-            const uint8_t *g = a.w0[se[p]] + roff, *u = a.w1[se[p]] + roff;
 #pragma unroll
             for (int j = 0; j < UX; j++) {
-                F::load(g + uoff[j], usub[j], R[p][j]);
-                F::load(u + uoff[j], usub[j], R[p][UX + j]);
+                F::load(wg + roff + uoff[j], usub[j], R[p][j]);
+                F::load(wu + roff + uoff[j], usub[j], R[p][UX + j]);
             }
         } else {
-            const int64_t roff = (int64_t)srow[p] * rs;
 #pragma unroll
             for (int j = 0; j < UX; j++) F::load(ubase[j] + roff, usub[j], R[p][j]);
         }
     };
-    auto advance = [&](int p) {
-        srow[p] += step;
-        if (KIND == 1) {
-            sr[p] += step;
-            while (sr[p] >= rows) {
-                sr[p] -= rows;
-                se[p]++;
-            }
-        }
-    };
-    // the first PF rows' weight loads go out before the activation prologue
 #pragma unroll
     for (int p = 0; p < PF; p++) {
         srow[p] = gid + p * ngroups;
-        if (KIND == 1) {
-            se[p] = srow[p] / rows;
-            sr[p] = srow[p] - se[p] * rows;
-        }
         if (srow[p] < nrow) load_slot(p);
     }
 
-    // ---- prologue: tables + q8_1 quantization of every activation vector into LDS ----------
-    F::init(tab, tid);
-    const int nxv = KIND == 2 ? a.nseg * nv : nv;
+    // ---- prologue compute: tables + q8_1 quantization of every activation vector into LDS ----
+    F::tab_store(tid, treg);
     uint32_t *xm = (uint32_t *)(xq + (size_t)nxv * K);
-    for (int i = tid; i < nxv * nu; i += GS_WG) {
+    auto quant_store = [&](int i, const float (&f)[32]) {
         const int v = i / nu, u = i - v * nu;
-        const float *src = (KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u;
-        float f[32];
-        load32(src, a.x_aligned != 0, f);
         const Q81 q = quant_unit(f);
         uint4 *dst = (uint4 *)(xq + (size_t)v * K + 32 * u);
         dst[0] = make_uint4(q.q[0], q.q[1], q.q[2], q.q[3]);
         dst[1] = make_uint4(q.q[4], q.q[5], q.q[6], q.q[7]);
         xm[2 * i] = __builtin_bit_cast(uint32_t, h2f(f2h(q.d)));
         xm[2 * i + 1] = ((uint32_t)q.slo & 0xffffu) | ((uint32_t)q.shi << 16);
+    };
+#pragma unroll
+    for (int k = 0; k < XQ; k++)
+        if (tid + GS_WG * k < nxu) quant_store(tid + GS_WG * k, xf[k]);
+    for (int i = tid + GS_WG * XQ; i < nxu; i += GS_WG) {   // large activation sets: the rest
+        const int v = i / nu, u = i - v * nu;
+        float f[32];
+        load32((KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u, a.x_aligned != 0, f);
+        quant_store(i, f);
     }
     __syncthreads();
     XU xr[UX][NV];
@@ -234,7 +276,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
         for (int t = 0; t < NV; t++) {
             const int v = KIND == 2 ? uspan[j] * nv + t : t;
             const float w = KIND == 2 ? a.wt[t][uspan[j]] : 1.f;   // routing weight folded into D
-            xr[j][t] = load_xu(xq, xm, K, nu, v, up, w, uval[j] && t < nv);
+            xr[j][t] = load_xu<F, XNEG>(xq, xm, K, nu, v, up, w, uval[j] && t < nv);
         }
     }
 
@@ -244,16 +286,30 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
         for (int p = 0; p < PF; p++) {
             const int rr = srow[p];
             if (rr < nrow) {
-                const int e = KIND == 1 ? se[p] : 0, r = KIND == 1 ? sr[p] : rr;
                 float acc0[NV], acc1[NV];
 #pragma unroll
                 for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
+                if (a.dbg & 2) {   // experiment: consume the loaded words without decoding
+                    uint32_t h = 0;
+#pragma unroll
+                    for (int j = 0; j < UMAX; j++) {
+                        const uint32_t *w = (const uint32_t *)&R[p][j];
+#pragma unroll
+                        for (int i = 0; i < (int)(sizeof(typename F::Raw) / 4); i++) h ^= w[i];
+                    }
+                    acc0[0] += (float)(h & 1);
+                } else {
 #pragma unroll
                 for (int j = 0; j < UX; j++) {
-                    F::template dot<NV>(R[p][j], usub[j], tab, xr[j], nv, acc0);
-                    if (KIND == 1) F::template dot<NV>(R[p][UX + j], usub[j], tab, xr[j], nv, acc1);
+                    F::template dot<NV, XNEG>(R[p][j], usub[j], tab, xr[j], nv, acc0);
+                    __builtin_amdgcn_sched_barrier(0);   // decode one unit at a time: short live ranges
+                    if (KIND == 1) {
+                        F::template dot<NV, XNEG>(R[p][UX + j], usub[j], tab, xr[j], nv, acc1);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
-                advance(p);
+                }
+                srow[p] += step;
                 if (srow[p] < nrow) load_slot(p);
 #pragma unroll
                 for (int t = 0; t < NV; t++) {
@@ -268,7 +324,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
                                 float *dst = y + (int64_t)t * a.y_stride + rr;
                                 *dst = a.accumulate ? *dst + acc0[t] : acc0[t];
                             } else if (KIND == 1) {
-                                y[((int64_t)e * nv + t) * rows + r] = swiglu(acc0[t], acc1[t], a.lim);
+                                y[((int64_t)ge * nv + t) * rows + rr] = swiglu(acc0[t], acc1[t], a.lim);
                             } else {
                                 y[(int64_t)t * a.y_stride + rr] += acc0[t];
                             }
@@ -280,8 +336,12 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     }
 }
 
+// waves per SIMD the streaming kernels are register-allocated for (HBM latency hiding)
+#ifndef GS_WPE
+#define GS_WPE 1
+#endif
 #define GS_STREAM_KERNEL(F, NAME, KIND, NV, UM)                                                  \
-    extern "C" __global__ void __launch_bounds__(GS_WG)                                         \
+    extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE))) \
         gs_k_stream_##NAME##_##KIND##_##NV##_##UM(StreamArgs a) {                                \
         stream_body<F, KIND, NV, UM>(a);                                                        \
     }
