@@ -226,10 +226,17 @@ __device__ __forceinline__ int dot8(const uint32_t (&w)[8], const uint32_t (&q)[
 // Unaligned loads straight from HBM: every block field is 2-byte aligned and gfx950 serves
 // unaligned global loads (the driver runs the GPU in unaligned-access mode), so a lane reads its
 // unit's bytes with one 8- or 16-byte load whatever the block size.
-__device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *(const uint4 *)p; }
-__device__ __forceinline__ uint2 ldg8(const uint8_t *p) { return *(const uint2 *)p; }
-__device__ __forceinline__ uint32_t ldg4(const uint8_t *p) { return *(const uint32_t *)p; }
-__device__ __forceinline__ uint32_t ldg2(const uint8_t *p) { return *(const uint16_t *)p; }
+// The weights are always in global memory: the address-space cast makes these global_load
+// (not flat_load, which would also count against the LDS wait counter and defeat exact waits).
+#define GS_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ T ldg(const uint8_t *p) { return *(const GS_GLOBAL T *)(const GS_GLOBAL uint8_t *)p; }
+// Wide unaligned loads are written as dword loads that the backend merges into one
+// global_load_dwordx2/x4; a direct 8/16-byte load at 2-byte alignment is lowered to flat_load.
+__device__ __forceinline__ uint32_t ldg4(const uint8_t *p) { return ldg<uint32_t>(p); }
+__device__ __forceinline__ uint2 ldg8(const uint8_t *p) { return make_uint2(ldg4(p), ldg4(p + 4)); }
+__device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return make_uint4(ldg4(p), ldg4(p + 4), ldg4(p + 8), ldg4(p + 12)); }
+__device__ __forceinline__ uint32_t ldg2(const uint8_t *p) { return ldg<uint16_t>(p); }
 
 // Each format: Raw = the registers one unit needs from memory; load() issues the loads for unit
 // `j` of the block at `b`; dot() decodes Raw and accumulates r[t] += W_unit . x_t for t < nv.
@@ -335,6 +342,18 @@ struct FQ6_K : UnitGeom<256, 210>, NoTable {
 __shared__ uint2 gs_iq2xxs_grid_lds[256];
 __shared__ uint2 gs_iq2xxs_sel_lds[128];
 
+// byte L of a, times 8: one SDWA shift (byte select on the source operand) instead of a
+// shift-and-mask pair; it is the byte offset of a 256-entry table of 8-byte rows.
+template <int L>
+__device__ __forceinline__ uint32_t grid_off(uint32_t a) {
+    uint32_t r;
+    if (L == 0) asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(r) : "v"(a));
+    if (L == 1) asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(r) : "v"(a));
+    if (L == 2) asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(r) : "v"(a));
+    if (L == 3) asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(r) : "v"(a));
+    return r;
+}
+
 struct FIQ2_XXS : UnitGeom<256, 66> {
     static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 0, RAW = 3;
     static constexpr bool NEG_X = true;
@@ -369,9 +388,10 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
         // db = d * (0.5 + s) * 0.25 (lib.rs:279); the 0.25 is already in x.D
         const float db = h2f(w.d) * (0.5f + (float)(w.a.y >> 28));
         uint2 g[4], s[4];
+        const uint32_t gofs[4] = {grid_off<0>(w.a.x), grid_off<1>(w.a.x), grid_off<2>(w.a.x), grid_off<3>(w.a.x)};
 #pragma unroll
         for (int l = 0; l < 4; l++) {
-            g[l] = gs_iq2xxs_grid_lds[(w.a.x >> (8 * l)) & 0xff];
+            g[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_grid_lds + gofs[l]);
             s[l] = gs_iq2xxs_sel_lds[(w.a.y >> (7 * l)) & 127];
         }
         if (!XNEG) {   // signed grid: every grid byte is nonzero, so 0x01010100 - g negates bytewise

@@ -188,10 +188,6 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     const int tab = (table_bytes(ty) + 15) & ~15;
     const size_t lds = (size_t)tab + (size_t)(kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
     if (lds > std::min<size_t>(c->max_lds, 160 * 1024)) return hipErrorInvalidValue;
-    {
-        static const int dbg = getenv("GLMSSD_STREAM_DBG") ? atoi(getenv("GLMSSD_STREAM_DBG")) : 0;
-        a.dbg = dbg;
-    }
     const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" +
                              std::to_string(NVt) + "_" + std::to_string(best_um);
     hipFunction_t f;
@@ -501,3 +497,30 @@ GS_EXPORT int gs_scatter_add_rows(float *acc, const int *idx, const float *w, co
     RowsArgs a{y, idx, w, acc, rows, n};
     return launch("gs_k_scatter_add_rows", dim3((n + 255) / 256, rows), dim3(256), 0, (hipStream_t)s, a);
 }
+
+
+#ifdef GS_STREAM_TS
+// profiling build only: copy the per-wave phase timestamps of the last stream launch
+GS_EXPORT int gs_debug_stream_timestamps(void *host, size_t n) {
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    for (hipModule_t m : c->mods) {
+        hipDeviceptr_t p;
+        size_t sz;
+        if (hipModuleGetGlobal(&p, &sz, m, "gs_stream_ts") == hipSuccess) {
+            // every per-format code object has its own copy; the launched one holds nonzero data
+            std::vector<unsigned long long> tmp(sz / 8);
+            if ((e = hipMemcpy(tmp.data(), p, sz, hipMemcpyDeviceToHost)) != hipSuccess) return e;
+            bool any = false;
+            for (auto v : tmp) any |= v != 0;
+            if (any) {
+                memcpy(host, tmp.data(), std::min(n, sz));
+                return hipMemset(p, 0, sz);
+            }
+        }
+    }
+    (void)hipGetLastError();
+    return hipErrorNotFound;
+}
+#endif

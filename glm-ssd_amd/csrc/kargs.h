@@ -10,7 +10,9 @@ enum GsType {
     GS_Q6_K = 14, GS_IQ2_XXS = 16, GS_IQ3_XXS = 18, GS_IQ2_S = 22, GS_IQ4_XS = 23, GS_BF16 = 30,
 };
 
+#ifndef GS_WG
 #define GS_WG 512          // threads per workgroup of the streaming kernels (8 wave64)
+#endif
 #define GS_SEG_MAX 32      // weight matrices (experts) per fused-MoE launch
 #define GS_NT_MAX 8        // activation vectors (tokens) per launch
 
@@ -40,7 +42,6 @@ struct StreamArgs {
     int lpr;                         // lanes per row group (16, 32 or 64)
     int upl;                         // units per lane = ceil(segments*nu/lpr)
     int x_aligned;                   // x and x_stride allow 16-byte loads
-    int dbg;                         // experiment switches (GLMSSD_STREAM_DBG), 0 in production
 };
 
 // Whole-tensor dequantization

@@ -40,9 +40,10 @@ __device__ __forceinline__ Q81 quant_unit(const float (&v)[32]) {
     return r;
 }
 
-__device__ __forceinline__ void load32(const float *src, bool aligned, float (&v)[32]) {
+__device__ __forceinline__ void load32(const float *src_, bool aligned, float (&v)[32]) {
+    const GS_GLOBAL float *src = (const GS_GLOBAL float *)src_;
     if (aligned) {
-        const float4 *p = (const float4 *)src;
+        const GS_GLOBAL float4 *p = (const GS_GLOBAL float4 *)src;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const float4 f = p[i];
@@ -95,7 +96,7 @@ __device__ __forceinline__ float swiglu(float g, float u, float lim) { // ops.cu
 // Rows in flight per lane group: as many as ~64 VGPRs of raw weight bytes hold (at most 8), so a
 // group's whole share of a decode-sized matrix is requested before the first row is decoded.
 #ifndef GS_PF_REGS
-#define GS_PF_REGS 64
+#define GS_PF_REGS 48
 #endif
 template <class F, int UMAX>
 __device__ __forceinline__ constexpr int pf_depth() {
@@ -134,6 +135,22 @@ __device__ __forceinline__ XU load_xu(const uint8_t *xq, const uint32_t *xm, int
 // UMAX = weight units per lane per row. GEMV / DOWN: units j of the (concatenated) row.
 // GATEUP: j < UMAX/2 are units of the gate row, j >= UMAX/2 the same units of the up row, so
 // the lane holds UMAX/2 activation units.
+//
+// Rows are processed in batches of PF rows per lane group: every load of a batch is issued
+// unconditionally (rows past the end are clamped to a valid row and their results dropped), so
+// the waits before each row are exact in-order counts and decoding row 0 overlaps the arrival of
+// rows 1..PF-1. Results are stored after the batch.
+#ifdef GS_STREAM_TS
+// profiling build only: per-wave phase timestamps (100 MHz s_memrealtime)
+__device__ unsigned long long gs_stream_ts[1 << 16];
+#define GS_TS(i, extra)                                                                          \
+    if ((threadIdx.x & 63) == 0)                                                                \
+        gs_stream_ts[((size_t)blockIdx.x * (GS_WG / 64) + (threadIdx.x >> 6)) * 8 + (i)] =       \
+            __builtin_amdgcn_s_memrealtime() + (extra);
+#else
+#define GS_TS(i, extra)
+#endif
+
 template <class F, int KIND, int NV, int UMAX>
 __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     constexpr int PF = pf_depth<F, UMAX>();
@@ -142,6 +159,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     static_assert(KIND != 1 || UMAX % 2 == 0, "gate/up needs an even unit count");
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x;
+    GS_TS(0, 0)
     uint8_t *tab = smem;
     uint8_t *xq = smem + ((F::TAB + 15) & ~15);
 
@@ -154,9 +172,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
         y += (int64_t)blockIdx.y * a.y_bs;
     }
     const int K = a.K, nu = a.nu, nv = a.nvec, rows = a.rows;
-    const int lpr = a.lpr, lane = tid & (lpr - 1), G = GS_WG / lpr;
+    const int lpr = a.lpr, lane = tid & (lpr - 1);
     const int tot = KIND == 2 ? a.nseg * nu : nu;          // units along the (concatenated) row
-    // Lane groups: GATEUP pins each wave to one expert (its pointers become scalar loads) and the
+    // Lane groups: GATEUP pins each wave to one expert (its pointers are wave-uniform) and the
     // wave's groups stride over that expert's rows; other kinds stride over all rows.
     const int gpw = 64 / lpr;                                   // groups per wave
     const int wave_all = blockIdx.x * (GS_WG / 64) + (tid >> 6);
@@ -175,7 +193,23 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
         nrow = rows;
     }
     const int64_t rs = a.row_stride;
-    const uint8_t *wg = KIND == 1 ? a.w0[ge] : nullptr, *wu = KIND == 1 ? a.w1[ge] : nullptr;
+    // expert pointer tables: one vector load (lane i <- entry i), then readlane / bpermute, so no
+    // weight address waits on a second, dependent kernel-argument fetch
+    const int L64 = tid & 63;
+    const uint64_t tw0 = KIND != 0 && L64 < GS_SEG_MAX ? (uint64_t)a.w0[L64] : 0;
+    const uint64_t tw1 = KIND == 1 && L64 < GS_SEG_MAX ? (uint64_t)a.w1[L64] : 0;
+    auto lane_u64 = [](uint64_t v, int src) -> uint64_t {   // v of lane `src` (per-lane src)
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)(v >> 32));
+        return (uint64_t)lo | ((uint64_t)hi << 32);
+    };
+    const uint8_t *wg = nullptr, *wu = nullptr;
+    if (KIND == 1) {
+        wg = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw0 >> 32), ge) << 32) |
+                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw0, ge));
+        wu = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw1 >> 32), ge) << 32) |
+                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw1, ge));
+    }
 
     // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
     int uspan[UX], usub[UX];
@@ -195,56 +229,48 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     }
     const uint8_t *ubase[UX];
 #pragma unroll
-    for (int j = 0; j < UX; j++) ubase[j] = wb + uoff[j];
-    if (KIND == 2) {   // expert pointers through scalar loads, selected per unit
-        for (int s = 0; s < a.nseg; s++) {
-            const uint8_t *ps = a.w0[s];
-#pragma unroll
-            for (int j = 0; j < UX; j++)
-                if (uspan[j] == s) ubase[j] = ps + uoff[j];
-        }
-    }
+    for (int j = 0; j < UX; j++)
+        ubase[j] = (KIND == 2 ? (const uint8_t *)lane_u64(tw0, uspan[j]) : (KIND == 1 ? nullptr : wb)) + uoff[j];
 
     // ---- prologue loads first: activation units and lookup tables are requested before the
-    // weight prefetch so waiting for them (vmcnt counts in issue order) never waits on weights
+    // weight loads, so waiting for them (vmcnt counts in issue order) never waits on weights
     constexpr int XQ = 2;                                       // activation units per thread in flight
     const int nxv = KIND == 2 ? a.nseg * nv : nv;
-    const int nxu = (a.dbg & 1) ? 0 : nxv * nu;
+    const int nxu = nxv * nu;
     float xf[XQ][32];
 #pragma unroll
     for (int k = 0; k < XQ; k++) {
-        const int i = tid + GS_WG * k;
-        if (i < nxu) {
-            const int v = i / nu, u = i - v * nu;
-            const float *src = (KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u;
-            load32(src, a.x_aligned != 0, xf[k]);
-        }
+        const int i = min(tid + GS_WG * k, nxu - 1);            // clamped: the loads are unconditional
+        const int v = i / nu, u = i - v * nu;
+        const float *src = (KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u;
+        load32(src, a.x_aligned != 0, xf[k]);
     }
     typename F::TabReg treg;
     F::tab_load(tid, treg);
 
-    // pipeline slots: output row advances by PF*ngroups rows
-    const int step = PF * ngroups;
-    int srow[PF];
+    // ---- weight batches ------------------------------------------------------------------------
     typename F::Raw R[PF][UMAX];
-    auto load_slot = [&](int p) {
-        const int64_t roff = (int64_t)srow[p] * rs;
-        if (KIND == 1) {
+    const int last = nrow > 0 ? nrow - 1 : 0;
+    auto load_batch = [&](int base) {
 #pragma unroll
-            for (int j = 0; j < UX; j++) {
-                F::load(wg + roff + uoff[j], usub[j], R[p][j]);
-                F::load(wu + roff + uoff[j], usub[j], R[p][UX + j]);
+        for (int p = 0; p < PF; p++) {
+            const int r = min(base + p * ngroups, last);
+            const int64_t roff = (int64_t)r * rs;
+            if (KIND == 1) {
+#pragma unroll
+                for (int j = 0; j < UX; j++) {
+                    F::load(wg + roff + uoff[j], usub[j], R[p][j]);
+                    F::load(wu + roff + uoff[j], usub[j], R[p][UX + j]);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < UX; j++) F::load(ubase[j] + roff, usub[j], R[p][j]);
             }
-        } else {
-#pragma unroll
-            for (int j = 0; j < UX; j++) F::load(ubase[j] + roff, usub[j], R[p][j]);
         }
     };
-#pragma unroll
-    for (int p = 0; p < PF; p++) {
-        srow[p] = gid + p * ngroups;
-        if (srow[p] < nrow) load_slot(p);
-    }
+    GS_TS(1, 0)
+    load_batch(gid);
+    GS_TS(2, 0)
 
     // ---- prologue compute: tables + q8_1 quantization of every activation vector into LDS ----
     F::tab_store(tid, treg);
@@ -268,6 +294,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
         quant_store(i, f);
     }
     __syncthreads();
+    GS_TS(3, 0)
     XU xr[UX][NV];
 #pragma unroll
     for (int j = 0; j < UX; j++) {
@@ -280,53 +307,51 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
         }
     }
 
-    // ---- row loop, PF rows in flight ---------------------------------------------------------
-    while (srow[0] < nrow) {
+    // ---- batches of PF rows per group ----------------------------------------------------------
+    for (int base = gid; base < nrow; base += PF * ngroups) {
+        if (base != gid) load_batch(base);
+        float res0[PF][NV], res1[PF][NV];
 #pragma unroll
         for (int p = 0; p < PF; p++) {
-            const int rr = srow[p];
-            if (rr < nrow) {
-                float acc0[NV], acc1[NV];
+            float acc0[NV], acc1[NV];
 #pragma unroll
-                for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
-                if (a.dbg & 2) {   // experiment: consume the loaded words without decoding
-                    uint32_t h = 0;
+            for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
+#ifdef GS_STREAM_TS
+            if (base == gid && p == 0) {
+                uint32_t h = 0;
 #pragma unroll
-                    for (int j = 0; j < UMAX; j++) {
-                        const uint32_t *w = (const uint32_t *)&R[p][j];
-#pragma unroll
-                        for (int i = 0; i < (int)(sizeof(typename F::Raw) / 4); i++) h ^= w[i];
-                    }
-                    acc0[0] += (float)(h & 1);
-                } else {
+                for (int j = 0; j < UMAX; j++) h ^= ((const uint32_t *)&R[0][j])[0];
+                GS_TS(4, h == 0x9e3779b9u)
+            }
+#endif
+            if (base + p * ngroups < nrow) {   // no loads inside: the waits stay exact
 #pragma unroll
                 for (int j = 0; j < UX; j++) {
                     F::template dot<NV, XNEG>(R[p][j], usub[j], tab, xr[j], nv, acc0);
-                    __builtin_amdgcn_sched_barrier(0);   // decode one unit at a time: short live ranges
-                    if (KIND == 1) {
-                        F::template dot<NV, XNEG>(R[p][UX + j], usub[j], tab, xr[j], nv, acc1);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
+                    if (KIND == 1) F::template dot<NV, XNEG>(R[p][UX + j], usub[j], tab, xr[j], nv, acc1);
                 }
-                }
-                srow[p] += step;
-                if (srow[p] < nrow) load_slot(p);
+            }
 #pragma unroll
-                for (int t = 0; t < NV; t++) {
-                    acc0[t] = group_sum(acc0[t], lpr);
-                    if (KIND == 1) acc1[t] = group_sum(acc1[t], lpr);
-                }
-                if (lane == lpr - 1) {
+            for (int t = 0; t < NV; t++) {
+                res0[p][t] = group_sum(acc0[t], lpr);
+                if (KIND == 1) res1[p][t] = group_sum(acc1[t], lpr);
+            }
+        }
+        if (lane == lpr - 1) {
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                const int rr = base + p * ngroups;
+                if (rr < nrow) {
 #pragma unroll
                     for (int t = 0; t < NV; t++) {
                         if (t < nv) {
                             if (KIND == 0) {
                                 float *dst = y + (int64_t)t * a.y_stride + rr;
-                                *dst = a.accumulate ? *dst + acc0[t] : acc0[t];
+                                *dst = a.accumulate ? *dst + res0[p][t] : res0[p][t];
                             } else if (KIND == 1) {
-                                y[((int64_t)ge * nv + t) * rows + rr] = swiglu(acc0[t], acc1[t], a.lim);
+                                y[((int64_t)ge * nv + t) * rows + rr] = swiglu(res0[p][t], res1[p][t], a.lim);
                             } else {
-                                y[(int64_t)t * a.y_stride + rr] += acc0[t];
+                                y[(int64_t)t * a.y_stride + rr] += res0[p][t];
                             }
                         }
                     }
@@ -334,6 +359,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
             }
         }
     }
+    GS_TS(5, 0)
 }
 
 // waves per SIMD the streaming kernels are register-allocated for (HBM latency hiding)
