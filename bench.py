@@ -28,6 +28,18 @@ METRIC = "quant-GEMV weight GB/s (% HBM peak); MoE grouped-GEMM TFLOP/s at 512 t
 HBM_PEAK_GBPS = 8000.0
 
 
+GATEUP_KERNEL = "gs_k_stream_16_1_1_4"   # the kernel gs_moe_gateup launches for config 2
+
+
+def traffic_bytes(kernel):
+    """HBM bytes per launch from the committed rocprofv3 counter summary, if it covers `kernel`."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "stream_kernels_traffic.json")) as f:
+            return json.load(f)["kernels"][kernel]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
