@@ -10,6 +10,7 @@ gs_blob_##NAME##_end:                    \
     .byte 0;
 
 BLOB(common, "build/common.hsaco")
+BLOB(grouped, "build/grouped.hsaco")
 BLOB(t0, "build/t0.hsaco")
 BLOB(t1, "build/t1.hsaco")
 BLOB(t8, "build/t8.hsaco")

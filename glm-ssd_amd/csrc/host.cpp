@@ -25,7 +25,7 @@
 #define GS_BLOB(NAME)                                 \
     extern "C" const unsigned char gs_blob_##NAME##_start[]; \
     extern "C" const unsigned char gs_blob_##NAME##_end[];
-#define GS_BLOB_LIST(X) X(common) X(t0) X(t1) X(t8) X(t10) X(t11) X(t12) X(t13) X(t14) X(t16) X(t18) X(t22) X(t23) X(t30)
+#define GS_BLOB_LIST(X) X(common) X(grouped) X(t0) X(t1) X(t8) X(t10) X(t11) X(t12) X(t13) X(t14) X(t16) X(t18) X(t22) X(t23) X(t30)
 GS_BLOB_LIST(GS_BLOB)
 
 namespace {
@@ -496,6 +496,122 @@ GS_EXPORT int gs_scatter_add_rows(float *acc, const int *idx, const float *w, co
     if (n <= 0) return hipErrorInvalidValue;
     RowsArgs a{y, idx, w, acc, rows, n};
     return launch("gs_k_scatter_add_rows", dim3((n + 255) / 256, rows), dim3(256), 0, (hipStream_t)s, a);
+}
+
+
+// =============================================================================================
+// grouped routed-expert FFN (no single reference kernel: it fuses what forward.rs:1399-1413
+// run_expert_rows does per expert -- gather, gate/up GEMM, SwiGLU, down GEMM, weighted
+// scatter-add -- for every expert of a layer at once)
+// =============================================================================================
+namespace {
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+struct GroupedWork {
+    size_t x16, x16lo, xs, h, h16, hs, total;
+};
+GroupedWork grouped_layout(int n_tok, int n_pairs, int K, int n_ff) {
+    GroupedWork w;
+    size_t o = 0;
+    w.x16 = o; o += align256((size_t)n_tok * K * 2);
+    w.x16lo = o; o += align256((size_t)n_tok * K * 2);
+    w.xs = o;  o += align256((size_t)n_tok * 4);
+    w.h = o;   o += align256((size_t)n_pairs * n_ff * 4);
+    w.h16 = o; o += align256((size_t)n_pairs * n_ff * 2);
+    w.hs = o;  o += align256((size_t)n_pairs * 4);
+    w.total = o;
+    return w;
+}
+
+int occupancy(DeviceCtx *c, const std::string &name, int threads, hipFunction_t f) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto key = std::make_pair(name, 0);
+    auto it = c->occ.find(key);
+    if (it != c->occ.end()) return it->second;
+    int nb = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, threads, 0) != hipSuccess || nb < 1) nb = 1;
+    c->occ[key] = nb;
+    return nb;
+}
+
+hipError_t rows_q8f16(const float *x, int64_t x_stride, int K, int nrows, uint16_t *out, uint16_t *out_lo, float *scale,
+                      hipStream_t s) {
+    if (nrows <= 0) return hipSuccess;
+    RowsQArgs a{x, x_stride, out, out_lo, scale, K, nrows};
+    return launch("gs_k_rows_q8f16", dim3((nrows + 3) / 4), dim3(256), 0, s, a);
+}
+
+// kind 1 (gate/up) or 2 (down) over every tile of the layer; the grid is persistent
+hipError_t grouped_launch(int kind, GroupedArgs &a, int n_pairs, hipStream_t s) {
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    static const int nt_env = getenv("GLMSSD_GRP_NT") ? atoi(getenv("GLMSSD_GRP_NT")) : 0;
+    const int nt = nt_env == 1 || nt_env == 2 || nt_env == 4 ? nt_env : (n_pairs <= 64 ? 1 : 2);
+    const int nr = kind == 1 ? 1 : 2;
+    const std::string name = "gs_k_grouped_16_" + std::to_string(kind) + "_" + std::to_string(nt) + "_" +
+                             std::to_string(nr);
+    hipFunction_t f;
+    if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
+    const int threads = 64 * GS_GRP_WAVES;
+    const int per_cu = occupancy(c, name, threads, f);
+    const int rb = GS_GRP_WAVES * 16 * nr, mt = 16 * nt;
+    const int64_t nrb = (a.rows + rb - 1) / rb;
+    const int64_t bound = nrb * (std::min<int64_t>(a.n_exp, n_pairs) + (n_pairs + mt - 1) / mt);
+    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, (int64_t)c->cu_count * per_cu));
+    return launch(name, dim3(grid), dim3(threads), 0, s, a);
+}
+}  // namespace
+
+GS_EXPORT int gs_moe_grouped_workspace(int n_tok, int n_pairs, int K, int n_ff, size_t *bytes) {
+    if (!bytes || n_tok < 0 || n_pairs < 0 || K <= 0 || n_ff <= 0) return hipErrorInvalidValue;
+    *bytes = grouped_layout(n_tok, n_pairs, K, n_ff).total;
+    return 0;
+}
+
+GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs,
+                             const int *idx, const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K,
+                             int n_ff, int64_t down_row_stride, const float *x, float *y, float lim, void *work,
+                             size_t work_bytes, void *s) {
+    if (ty_gu != GS_IQ2_XXS || ty_down != GS_IQ2_XXS) return hipErrorInvalidValue;
+    if (n_exp < 1 || n_exp > GS_GRP_EXP_MAX || n_pairs < 0 || n_tok < 1) return hipErrorInvalidValue;
+    if (K <= 0 || n_ff <= 0 || K % 256 != 0 || n_ff % 256 != 0) return hipErrorInvalidValue;
+    if (!experts || !offs || !x || !y || (gu_row_stride & 1) || (down_row_stride & 1)) return hipErrorInvalidValue;
+    if (gu_row_stride < (int64_t)K / 256 * 66 || down_row_stride < (int64_t)n_ff / 256 * 66) return hipErrorInvalidValue;
+    if (n_pairs == 0) return 0;
+    if (!idx || !w || !aligned16(x) || ((uintptr_t)work & 255)) return hipErrorInvalidValue;
+    const GroupedWork L = grouped_layout(n_tok, n_pairs, K, n_ff);
+    if (!work || work_bytes < L.total) return hipErrorInvalidValue;
+    uint8_t *wb = (uint8_t *)work;
+    uint16_t *x16 = (uint16_t *)(wb + L.x16), *x16lo = (uint16_t *)(wb + L.x16lo), *h16 = (uint16_t *)(wb + L.h16);
+    float *xs = (float *)(wb + L.xs), *h = (float *)(wb + L.h), *hs = (float *)(wb + L.hs);
+    hipStream_t st = (hipStream_t)s;
+    hipError_t e = rows_q8f16(x, K, K, n_tok, x16, x16lo, xs, st);
+    if (e != hipSuccess) return e;
+    GroupedArgs a;
+    memset(&a, 0, sizeof(a));
+    a.experts = (const uint8_t *const *)experts;
+    a.offs = offs;
+    a.idx = idx;
+    a.w = w;
+    a.act = x16;
+    a.act_lo = x16lo;
+    a.ascale = xs;
+    a.out = h;
+    a.row_stride = gu_row_stride;
+    a.K = K;
+    a.rows = n_ff;
+    a.n_exp = n_exp;
+    a.lim = lim;
+    if ((e = grouped_launch(1, a, n_pairs, st)) != hipSuccess) return e;
+    if ((e = rows_q8f16(h, n_ff, n_ff, n_pairs, h16, nullptr, hs, st)) != hipSuccess) return e;
+    a.act = h16;
+    a.act_lo = nullptr;
+    a.ascale = hs;
+    a.out = y;
+    a.row_stride = down_row_stride;
+    a.K = n_ff;
+    a.rows = K;
+    return grouped_launch(2, a, n_pairs, st);
 }
 
 

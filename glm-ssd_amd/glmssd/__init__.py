@@ -34,6 +34,12 @@ class MoeBatch(C.Structure):
                 ("w", (C.c_float * MOE_MAX) * MOE_NT), ("n", C.c_int)]
 
 
+class ExpertPtrs(C.Structure):
+    """Device pointers of one routed expert's gate / up / down matrices (GsExpertPtrs; the
+    engine's ExpertPtrs, crates/engine/src/experts.rs:133-137)."""
+    _fields_ = [("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p)]
+
+
 class DeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 256), ("cc_major", C.c_int), ("cc_minor", C.c_int), ("sm_count", C.c_int),
                 ("total_mem", C.c_uint64), ("free_mem", C.c_uint64), ("pci_bus", C.c_int), ("pci_device", C.c_int),
@@ -81,6 +87,9 @@ SIGNATURES = {
     "gs_scatter_add_rows": [_P, _P, _P, _P, C.c_int, C.c_int, _P],
     "gs_f32_to_f16": [_P, _P, _I64, _P],
     "gs_quant_q8_1": [_P, _P, _I64, _P],
+    "gs_moe_grouped_workspace": [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_size_t)],
+    "gs_moe_grouped": [C.c_int, C.c_int, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int, _I64, C.c_int, C.c_int, _I64,
+                       _P, _P, C.c_float, _P, C.c_size_t, _P],
 }
 
 
@@ -265,6 +274,19 @@ class ops:
              y_bs=0, s=None):
         check(lib().gs_gemm(ty, _p(w), row_stride, k, rows, _p(x), x_stride, _p(y), y_stride, n,
                             1 if accumulate else 0, n_batch, w_bs, x_bs, y_bs, _raw(s)))
+
+    @staticmethod
+    def moe_grouped_workspace(n_tok, n_pairs, k, n_ff):
+        n = C.c_size_t()
+        check(lib().gs_moe_grouped_workspace(n_tok, n_pairs, k, n_ff, C.byref(n)))
+        return n.value
+
+    @staticmethod
+    def moe_grouped(ty_gu, ty_down, experts, n_exp, offs, idx, w, n_pairs, n_tok, gu_row_stride, k, n_ff,
+                    down_row_stride, x, y, lim, work, work_bytes, s=None):
+        check(lib().gs_moe_grouped(ty_gu, ty_down, _p(experts), n_exp, _p(offs), _p(idx), _p(w), n_pairs, n_tok,
+                                   gu_row_stride, k, n_ff, down_row_stride, _p(x), _p(y), lim, _p(work), work_bytes,
+                                   _raw(s)))
 
     @staticmethod
     def swiglu(g, u, y, n, lim=0.0, s=None):

@@ -129,6 +129,28 @@ int gs_f32_to_f16(const float *x, void *y, int64_t n, void *s);
  * for bit-exact testing. */
 int gs_quant_q8_1(const float *x, void *q, int64_t n, void *s);
 
+/* Grouped routed-expert FFN over every expert of one MoE layer in one call (prefill, MTP verify;
+ * the multi-token path crates/engine/src/forward.rs:1335-1368 + run_expert_rows :1399-1413 runs
+ * as gs_gather_rows, gs_gemm x3, gs_swiglu, gs_scatter_add_rows per expert). The pairs are the
+ * engine's grouping (forward.rs:1017-1036): pair p = (token idx[p], weight w[p]), sorted by
+ * expert, expert e owning pairs offs[e] .. offs[e+1]-1 (offs has n_exp+1 entries; empty experts
+ * allowed). experts[e] holds the device pointers of expert e's gate/up ([K] x n_ff rows,
+ * gu_row_stride bytes apart) and down ([n_ff] x K rows, down_row_stride apart).
+ *   y[idx[p]][:] += w[p] * down_e . swiglu(gate_e . x[idx[p]], up_e . x[idx[p]])   (always adds)
+ * x [n_tok][K], y [n_tok][K] f32; activations are q8_1-quantized as in the other matmul calls.
+ * Supported: ty_gu == ty_down == IQ2_XXS, K and n_ff multiples of 256, n_exp <= 1024, x 16-byte
+ * aligned. `work` (256-byte aligned, >= gs_moe_grouped_workspace bytes) is caller-owned scratch.
+ * All of offs/idx/w/experts are device arrays; the call launches without a host sync. */
+typedef struct GsExpertPtrs {
+    const uint8_t *gate;
+    const uint8_t *up;
+    const uint8_t *down;
+} GsExpertPtrs;
+int gs_moe_grouped_workspace(int n_tok, int n_pairs, int K, int n_ff, size_t *bytes);
+int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs, const int *idx,
+                   const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K, int n_ff,
+                   int64_t down_row_stride, const float *x, float *y, float lim, void *work, size_t work_bytes, void *s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,3 +66,27 @@ def test_kernels_embedded_for_gfx950():
     for name in [b"gs_k_stream_16_1_1", b"gs_k_stream_8_0_1", b"gs_k_dequant_f32_16", b"gs_k_quant_q8_1"]:
         assert name in data, name
     assert b"gfx950" in data
+
+
+def test_expert_ptrs_layout():
+    import glmssd
+    assert ctypes.sizeof(glmssd.ExpertPtrs) == 24
+    assert glmssd.ExpertPtrs.down.offset == 16
+
+
+def test_group_pairs_matches_engine_grouping():
+    from glmssd.moe import group_pairs
+    import numpy as np
+    rng = np.random.default_rng(0)
+    routes = [[(int(e), float(rng.random())) for e in rng.choice(10, 3, replace=False)] for _ in range(7)]
+    offs, idx, w, pe = group_pairs(routes, 10)
+    assert offs[0] == 0 and offs[-1] == 21 and np.all(np.diff(offs) >= 0)
+    # brute force: pairs of expert e are exactly the tokens routed to e, in token order
+    for e in range(10):
+        want = [(t, wt) for t, r in enumerate(routes) for (ee, wt) in r if ee == e]
+        got = list(zip(idx[offs[e]:offs[e + 1]].tolist(), w[offs[e]:offs[e + 1]].tolist()))
+        assert [g[0] for g in got] == [t for t, _ in want]
+        assert np.allclose([g[1] for g in got], [wt for _, wt in want])
+        assert np.all(pe[offs[e]:offs[e + 1]] == e)
+    with pytest.raises(ValueError):
+        group_pairs([[(10, 1.0)]], 10)
