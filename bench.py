@@ -26,6 +26,7 @@ sys.path.insert(0, os.path.join(ROOT, "glm-ssd_amd"))
 
 METRIC = "quant-GEMV weight GB/s (% HBM peak); MoE grouped-GEMM TFLOP/s at 512 tok"
 HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0   # dense f16 MFMA (the grouped GEMM's operand type)
 
 
 GATEUP_KERNEL = "gs_k_stream_16_1_1_4"   # the kernel gs_moe_gateup launches for config 2
@@ -54,6 +55,8 @@ def bench_lib():
     L.bn_gemv.argtypes = [C.c_int, P, C.c_int, I64, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P,
                           C.POINTER(C.c_float)]
     L.bn_copy.argtypes = [P, P, C.c_size_t, C.c_int, P, C.POINTER(C.c_float)]
+    L.bn_moe_grouped.argtypes = [C.c_int, P, C.c_int, C.c_int, P, P, P, P, C.c_int, I64, C.c_int, C.c_int, I64, P, P,
+                                 P, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     return L
 
 
@@ -99,8 +102,57 @@ def run_moe_decode(L, s, steps, warmup, n_expert=288, n_embd=4096, n_ff=1536, se
     step_bytes = 8 * 3 * mat
     gu_bytes = 8 * 2 * mat
     keep = (gate, up, down, dx, dh, dy, batches)
+    layer = dict(gate=gate, up=up, down=down, mat=mat, n_expert=n_expert, n_embd=n_embd, n_ff=n_ff, rbg=rbg, rbd=rbd)
     return dict(ms_step=ms.value, ms_gateup=msg.value, step_bytes=step_bytes, gateup_bytes=gu_bytes,
-                flops=8 * 3 * 2 * n_ff * n_embd), keep
+                flops=8 * 3 * 2 * n_ff * n_embd), keep, layer
+
+
+def run_moe_grouped(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
+    """Configs 4 and 5: n_tok tokens through one MoE layer of the 288 resident experts, top-k per token
+    drawn Zipf(1.1) over a seeded permutation (a fresh permutation per routing, n_rout routings
+    rotated), one gs_moe_grouped call per step."""
+    import glmssd as G
+    from glmssd import synth
+    from glmssd.moe import group_pairs
+    ty = G.GgmlType.IQ2_XXS
+    n_exp, mat = layer["n_expert"], layer["mat"]
+    tab = (G.ExpertPtrs * n_exp)()
+    for e in range(n_exp):
+        tab[e].gate = layer["gate"].p.value + e * mat
+        tab[e].up = layer["up"].p.value + e * mat
+        tab[e].down = layer["down"].p.value + e * mat
+    dtab = G.DeviceBuffer.from_array(np.frombuffer(bytes(tab), dtype=np.uint8), s)
+    rng = np.random.default_rng(seed)
+    keep, offs_p, idx_p, w_p, npairs, uniq, maxg = [dtab], [], [], [], [], [], []
+    for _ in range(n_rout):
+        routes = [list(zip(e, w)) for e, w in synth.zipf_topk(rng, n_tok, n_exp, k)]
+        offs, idx, w, _pe = group_pairs(routes, n_exp)
+        bufs = [G.DeviceBuffer.from_array(a, s) for a in (offs, idx, w)]
+        keep += bufs
+        offs_p.append(bufs[0].p.value); idx_p.append(bufs[1].p.value); w_p.append(bufs[2].p.value)
+        npairs.append(int(idx.size))
+        uniq.append(int(np.count_nonzero(np.diff(offs))))
+        maxg.append(int(np.diff(offs).max()))
+    n_embd, n_ff = layer["n_embd"], layer["n_ff"]
+    x = G.DeviceBuffer.from_array(rng.standard_normal((n_tok, n_embd)).astype(np.float32), s)
+    y = G.DeviceBuffer(n_tok * n_embd * 4)
+    y.zero(s)
+    wb = max(G.ops.moe_grouped_workspace(n_tok, n, n_embd, n_ff) for n in npairs)
+    work = G.DeviceBuffer(wb)
+    A = lambda v, t: (t * len(v))(*v)
+    ms = C.c_float()
+    G.check(L.bn_moe_grouped(ty, dtab.p, n_exp, n_rout, C.cast(A(offs_p, C.c_void_p), C.c_void_p),
+                             C.cast(A(idx_p, C.c_void_p), C.c_void_p), C.cast(A(w_p, C.c_void_p), C.c_void_p),
+                             C.cast(A(npairs, C.c_int), C.c_void_p), n_tok, layer["rbg"], n_embd, n_ff, layer["rbd"],
+                             x.p, y.p, work.p, wb, steps, warmup, s.raw(), C.byref(ms)))
+    u = float(np.mean(uniq))
+    wbytes = u * 3 * mat
+    flops = float(np.mean(npairs)) * 3 * 2 * n_ff * n_embd
+    t = ms.value * 1e-3
+    return dict(us_per_step=round(ms.value * 1e3, 2), unique_experts=round(u, 1), max_group=max(maxg),
+                pairs=int(np.mean(npairs)), weight_bytes=int(wbytes), GBps=round(wbytes / t / 1e9, 1),
+                frac_hbm_peak=round(wbytes / t / 1e9 / HBM_PEAK_GBPS, 4), TFLOPs=round(flops / t / 1e12, 2),
+                frac_mfma_f16_peak=round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4), routings_rotated=n_rout)
 
 
 def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 20):
@@ -169,14 +221,20 @@ def main():
     info = G.device_info(0)
     log(f"device: {info.name.decode()} CUs={info.sm_count}")
 
-    res, keep = run_moe_decode(L, s, args.steps, args.warmup)
+    res, keep, layer = run_moe_decode(L, s, args.steps, args.warmup)
     value = res["step_bytes"] / (res["ms_step"] * 1e-3) / 1e9
     gu_gbps = res["gateup_bytes"] / (res["ms_gateup"] * 1e-3) / 1e9
     log(f"config 2: {res['ms_step'] * 1e3:.2f} us/step, {value:.1f} GB/s; gate/up kernel {res['ms_gateup'] * 1e3:.2f} us "
         f"= {gu_gbps:.1f} GB/s")
-    del keep
 
     secondary = {}
+    if not args.no_secondary:
+        gsteps, gwarm = max(10, args.steps // 10), max(3, args.warmup // 10)
+        for name, n_tok, seed in [("config4_mtp_verify_4tok_grouped", 4, 4), ("config5_prefill_512tok_grouped", 512, 5)]:
+            r = run_moe_grouped(L, s, layer, n_tok, gsteps, gwarm, seed)
+            secondary[name] = r
+            log(f"{name}: {r}")
+    del keep, layer
     if not args.no_secondary:
         from glmssd import synth
         r1 = run_gemv(L, s, G.GgmlType.Q8_0, 4096, 4096, synth.q8_0_matrix, args.steps, args.warmup, 1)

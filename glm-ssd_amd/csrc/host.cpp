@@ -80,9 +80,22 @@ DeviceCtx *ctx(hipError_t *err) {
         }
     }
     if (e == hipSuccess) {
+        // profiling builds only: GLMSSD_GROUPED_HSACO names a code object that replaces the
+        // embedded grouped-GEMM one (kernel variants are timed without relinking the library)
+        std::vector<char> grouped_override;
+        if (const char *path = getenv("GLMSSD_GROUPED_HSACO")) {
+            if (FILE *f = fopen(path, "rb")) {
+                char buf[1 << 16];
+                size_t n;
+                while ((n = fread(buf, 1, sizeof buf, f)) > 0) grouped_override.insert(grouped_override.end(), buf, buf + n);
+                fclose(f);
+            }
+            if (grouped_override.empty()) fprintf(stderr, "glmssd: cannot read %s\n", path);
+        }
         for (const Blob &b : blobs()) {
             hipModule_t m;
-            e = hipModuleLoadData(&m, b.p);
+            const bool swap = !grouped_override.empty() && b.p == gs_blob_grouped_start;
+            e = hipModuleLoadData(&m, swap ? (const void *)grouped_override.data() : (const void *)b.p);
             if (e != hipSuccess) break;
             c->mods.push_back(m);
         }
@@ -522,17 +535,6 @@ GroupedWork grouped_layout(int n_tok, int n_pairs, int K, int n_ff) {
     return w;
 }
 
-int occupancy(DeviceCtx *c, const std::string &name, int threads, hipFunction_t f) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    auto key = std::make_pair(name, 0);
-    auto it = c->occ.find(key);
-    if (it != c->occ.end()) return it->second;
-    int nb = 0;
-    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, threads, 0) != hipSuccess || nb < 1) nb = 1;
-    c->occ[key] = nb;
-    return nb;
-}
-
 hipError_t rows_q8f16(const float *x, int64_t x_stride, int K, int nrows, uint16_t *out, uint16_t *out_lo, float *scale,
                       hipStream_t s) {
     if (nrows <= 0) return hipSuccess;
@@ -540,25 +542,57 @@ hipError_t rows_q8f16(const float *x, int64_t x_stride, int K, int nrows, uint16
     return launch("gs_k_rows_q8f16", dim3((nrows + 3) / 4), dim3(256), 0, s, a);
 }
 
-// kind 1 (gate/up) or 2 (down) over every tile of the layer; the grid is persistent
+// kind 1 (gate/up) or 2 (down) over every tile of the layer; the grid is persistent.
+// Tile shape: NT token sub-tiles of 16 (the chunk of one expert's pairs a workgroup takes) and NR
+// row sub-tiles of 16 per wave. Larger tiles stage fewer activation bytes per weight byte, but the
+// tile count must still fill the chip: take the largest NR whose (upper-bound) tile count is at
+// least two per CU. Instantiated shapes: grouped.hip GS_GRP_KERNEL.
 hipError_t grouped_launch(int kind, GroupedArgs &a, int n_pairs, hipStream_t s) {
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
-    static const int nt_env = getenv("GLMSSD_GRP_NT") ? atoi(getenv("GLMSSD_GRP_NT")) : 0;
-    const int nt = nt_env == 1 || nt_env == 2 || nt_env == 4 ? nt_env : (n_pairs <= 64 ? 1 : 2);
-    const int nr = kind == 1 ? 1 : 2;
+    auto env = [](const char *n) { return getenv(n) ? atoi(getenv(n)) : 0; };
+    static const int nt1 = env("GLMSSD_GRP_NT1"), nr1 = env("GLMSSD_GRP_NR1");
+    static const int nt2 = env("GLMSSD_GRP_NT2"), nr2 = env("GLMSSD_GRP_NR2");
+    const std::vector<std::pair<int, int>> shapes =
+        kind == 1 ? std::vector<std::pair<int, int>>{{1, 1}, {1, 2}, {2, 1}, {2, 2}, {2, 4}}
+                  : std::vector<std::pair<int, int>>{{1, 1}, {1, 2}, {2, 2}, {2, 4}, {4, 4}};
+    int nt = n_pairs <= 64 ? 1 : 2;
+    if ((kind == 1 ? nt1 : nt2) > 0) nt = kind == 1 ? nt1 : nt2;
+    const int groups = std::min(a.n_exp, n_pairs);
+    int nr = 0;
+    for (const auto &sh : shapes) {
+        if (sh.first != nt) continue;
+        const int64_t rbk = GS_GRP_WAVES * 16 * sh.second;
+        const int64_t tiles = (a.rows + rbk - 1) / rbk * (groups + (n_pairs + 16 * nt - 1) / (16 * nt));
+        if (nr == 0 || tiles >= 2 * (int64_t)c->cu_count) nr = std::max(nr, sh.second);
+    }
+    if ((kind == 1 ? nr1 : nr2) > 0) nr = kind == 1 ? nr1 : nr2;
+    if (std::find(shapes.begin(), shapes.end(), std::make_pair(nt, nr)) == shapes.end()) return hipErrorInvalidValue;
     const std::string name = "gs_k_grouped_16_" + std::to_string(kind) + "_" + std::to_string(nt) + "_" +
                              std::to_string(nr);
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
     const int threads = 64 * GS_GRP_WAVES;
-    const int per_cu = occupancy(c, name, threads, f);
+    const size_t lds = 2 * (size_t)(kind == 1 ? 2 : 1) * 16 * nt * 512;   // two staged super-blocks
+    int per_cu = 1;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto key = std::make_pair(name, (int)lds);
+        auto it = c->occ.find(key);
+        if (it != c->occ.end()) {
+            per_cu = it->second;
+        } else {
+            int nb = 0;
+            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, threads, lds) != hipSuccess || nb < 1) nb = 1;
+            c->occ[key] = per_cu = nb;
+        }
+    }
     const int rb = GS_GRP_WAVES * 16 * nr, mt = 16 * nt;
     const int64_t nrb = (a.rows + rb - 1) / rb;
-    const int64_t bound = nrb * (std::min<int64_t>(a.n_exp, n_pairs) + (n_pairs + mt - 1) / mt);
+    const int64_t bound = nrb * (groups + (n_pairs + mt - 1) / mt);
     const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, (int64_t)c->cu_count * per_cu));
-    return launch(name, dim3(grid), dim3(threads), 0, s, a);
+    return launch(name, dim3(grid), dim3(threads), lds, s, a);
 }
 }  // namespace
 
@@ -574,7 +608,8 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
                              size_t work_bytes, void *s) {
     if (ty_gu != GS_IQ2_XXS || ty_down != GS_IQ2_XXS) return hipErrorInvalidValue;
     if (n_exp < 1 || n_exp > GS_GRP_EXP_MAX || n_pairs < 0 || n_tok < 1) return hipErrorInvalidValue;
-    if (K <= 0 || n_ff <= 0 || K % 256 != 0 || n_ff % 256 != 0) return hipErrorInvalidValue;
+    // whole super-blocks, at least two per row (the kernel's load pipeline runs two ahead)
+    if (K < 512 || n_ff < 512 || K % 256 != 0 || n_ff % 256 != 0) return hipErrorInvalidValue;
     if (!experts || !offs || !x || !y || (gu_row_stride & 1) || (down_row_stride & 1)) return hipErrorInvalidValue;
     if (gu_row_stride < (int64_t)K / 256 * 66 || down_row_stride < (int64_t)n_ff / 256 * 66) return hipErrorInvalidValue;
     if (n_pairs == 0) return 0;

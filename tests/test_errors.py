@@ -54,3 +54,28 @@ def test_zero_sized_row_ops_are_noops():
     assert L.gs_scatter_add_rows(NULL, NULL, NULL, NULL, 0, 16, NULL) == 0
     assert L.gs_swiglu(NULL, NULL, NULL, 0, 0.0, NULL) == 0
     assert L.gs_axpy(NULL, NULL, 1.0, 0, NULL) == 0
+
+
+def test_moe_grouped_rejects_bad_arguments():
+    L = G.lib()
+    P = C.c_void_p
+    x, y, tab, offs, idx, w, work = (P(256 * i) for i in range(1, 8))
+
+    def call(ty=16, n_exp=288, n_pairs=64, n_tok=8, K=4096, n_ff=1536, rs_gu=1056, rs_dn=396, xx=x, wk=work,
+             wb=1 << 30):
+        return L.gs_moe_grouped(ty, ty, tab, n_exp, offs, idx, w, n_pairs, n_tok, rs_gu, K, n_ff, rs_dn, xx, y, 0.0,
+                                wk, wb, NULL)
+    assert call(ty=12) == INVALID                    # only IQ2_XXS
+    assert call(n_exp=0) == INVALID
+    assert call(n_exp=1025) == INVALID
+    assert call(K=4000) == INVALID                   # not whole super-blocks
+    assert call(n_ff=256, rs_dn=66) == INVALID       # fewer than two super-blocks per row
+    assert call(rs_gu=1055) == INVALID               # odd row stride
+    assert call(rs_gu=66) == INVALID                 # row stride shorter than a row
+    assert call(xx=P(258)) == INVALID                # x not 16-byte aligned
+    assert call(wk=P(300)) == INVALID                # workspace not 256-byte aligned
+    assert call(wb=1024) == INVALID                  # workspace too small
+    assert call(n_pairs=0) == 0                      # nothing to do, nothing launched
+    n = C.c_size_t()
+    assert L.gs_moe_grouped_workspace(512, 4096, 4096, 1536, C.byref(n)) == 0
+    assert n.value >= 512 * 4096 * 4 + 4096 * 1536 * 6

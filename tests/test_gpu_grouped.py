@@ -68,10 +68,10 @@ def test_grouped_hot_expert_chunks_and_clamp():
     n_tok = 150
     rng = np.random.default_rng(9)
     routes = [[(3, 0.6), (int(rng.choice([0, 2, 4, 6, 7])), 0.4)] for _ in range(n_tok)]
-    run_case(n_exp=8, n_tok=n_tok, k=2, n_embd=768, n_ff=256, seed=6, lim=7.0, routes=routes, zero_w=True)
+    run_case(n_exp=8, n_tok=n_tok, k=2, n_embd=768, n_ff=512, seed=6, lim=7.0, routes=routes, zero_w=True)
 
 
 def test_grouped_repeat_is_stable():
     # two calls into fresh outputs agree to f32 atomic-order noise
-    layer, a = run_case(n_exp=16, n_tok=20, k=4, n_embd=512, n_ff=256, seed=11)
+    layer, a = run_case(n_exp=16, n_tok=20, k=4, n_embd=512, n_ff=768, seed=11)
     assert np.all(np.isfinite(a))
