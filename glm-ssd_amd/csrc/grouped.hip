@@ -9,12 +9,11 @@
 //   * IQ2_XXS super-block (256 weights of one row) -> f16 B fragments that hold the exact integers
 //     grid * sign * (2s+1) (|v| <= 43*31 = 1333, exact in f16); the remaining factor d/8 of the
 //     super-block is applied to the f32 accumulator once per super-block. A lane owns one row
-//     (the D column it accumulates), so that factor is one scalar per lane.
-//   * activations (A operand) are the q8_1 values D*q of each row after a power-of-two row scale
-//     (restored in the epilogue). D*q has up to 19 significant bits, so for gate/up it is carried
-//     exactly as two f16 halves (hi + lo, two MFMAs per fragment): a rounded x would perturb
-//     gate/up by ~1e-4 relative, enough to flip q8_1 rounding decisions when h is re-quantized
-//     (rel-L2 ~2e-3 at the output). h enters the down projection as one rounded f16 (~2e-4).
+//     (the D column it accumulates), so that factor is one scalar per lane. Weights are therefore
+//     exact, where the reference's GEMM rounds dequantized weights to half (gemm.cu:57-66).
+//   * activations (A operand) are f16, as in the reference's multi-token GEMM (gemm.cu:69-78),
+//     after a power-of-two row scale that keeps the row's largest value in the f16 normal range
+//     (restored exactly in the epilogue); h enters the down projection the same way.
 //   * the K order inside a super-block is permuted so that a lane decodes whole 32-element units:
 //     lane quarter Q (lane >> 4) owns units 2Q and 2Q+1, MFMA m (0..7) takes group m&3 of unit
 //     2Q + (m>>2). A and B use the same permutation, so the dot product is unchanged.
@@ -29,55 +28,94 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));   // staging chunk (a native vector, so it stays in VGPRs)
 
-// grid values as f16 (8 per entry) and the f16 sign masks of ksigns(i) (bit 15 per negative lane)
-__shared__ uint4 gs_grp_grid16[256];
-__shared__ uint4 gs_grp_sgn16[128];
+// Decode tables in LDS, built by every workgroup at start:
+//   grid (64 KB): for grid index g and unit scale s (0..15), the 8 grid values times 2s+1 as f16
+//     at byte (g << 8) | (s << 4) -- the address is one v_perm of the unit's index byte and its
+//     scale nibble;
+//   signs (1 KB): for a 7-bit sign index i, 8 bytes, byte e = 0x80 when element e of ksigns(i)
+//     is negative, at byte 65536 + 8 i.
+// A B fragment is one 16-byte and one 8-byte LDS read, 4 v_perm (sign bytes -> f16 sign bits)
+// and 4 XORs. (Measured on gfx950 against one-table alternatives: the 24 bytes of LDS per 8
+// weights, not the VALU work, bound the decode; this layout reads the fewest bytes.)
+#define GS_GRP_TAB_BYTES (65536 + 1024)
 __shared__ int gs_grp_pre[GS_GRP_EXP_MAX + 1];
 
-__device__ __forceinline__ void grp_tables(int tid) {
-    if (tid < 256) {
-        const uint64_t g = iq2xxs_grid[tid];
+template <int NTH>
+__device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
+    for (int e = tid; e < 4096; e += NTH) {
+        const int g = e >> 4, sc = e & 15;
+        const uint64_t grid = iq2xxs_grid[g];
+        const float m = (float)(2 * sc + 1);
         uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t lo = f2h((float)((g >> (16 * i)) & 0xff));
-            const uint32_t hi = f2h((float)((g >> (16 * i + 8)) & 0xff));
-            w[i] = lo | (hi << 16);
-        }
-        gs_grp_grid16[tid] = make_uint4(w[0], w[1], w[2], w[3]);
+        for (int i = 0; i < 4; i++)
+            w[i] = f2h(m * (float)((grid >> (16 * i)) & 0xff)) | (f2h(m * (float)((grid >> (16 * i + 8)) & 0xff)) << 16);
+        *(uint4 *)(tab + (e << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    if (tid < 128) {
-        const uint32_t k = ksigns((uint32_t)tid);
-        uint32_t w[4];
+    for (int i = tid; i < 128; i += NTH) {
+        const uint32_t k = ksigns((uint32_t)i);
+        uint32_t lo = 0, hi = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) w[i] = (((k >> (2 * i)) & 1u) << 15) | (((k >> (2 * i + 1)) & 1u) << 31);
-        gs_grp_sgn16[tid] = make_uint4(w[0], w[1], w[2], w[3]);
+        for (int b = 0; b < 4; b++) {
+            lo |= ((k >> b) & 1u) << (8 * b + 7);
+            hi |= ((k >> (b + 4)) & 1u) << (8 * b + 7);
+        }
+        *(uint2 *)(tab + 65536 + (i << 3)) = make_uint2(lo, hi);
     }
 }
 
-// B fragment: group G (0..3) of the unit with words (a0 = grid indices, a1 = signs | s << 28),
-// times c = 2s+1, as 8 f16 integers
+// B fragment: group G (0..3) of the unit with words (a0 = grid indices, a1 = signs | s << 28):
+// 8 f16 integers grid * sign * (2s+1)
 template <int G>
-__device__ __forceinline__ h8 iq2_frag(uint32_t a0, uint32_t a1, _Float16 c) {
+__device__ __forceinline__ h8 iq2_frag(const uint8_t *tab, uint32_t a0, uint32_t a1) {
 #ifdef GS_GRP_PROBE_NODECODE   // profiling variant: no table lookups
     return __builtin_bit_cast(h8, make_uint4(a0, a1, a0 ^ a1, a0 + a1));
 #endif
-    const uint4 g = gs_grp_grid16[(a0 >> (8 * G)) & 0xff];
-    const uint4 s = gs_grp_sgn16[(a1 >> (7 * G)) & 127];
-    const uint4 v = make_uint4(g.x ^ s.x, g.y ^ s.y, g.z ^ s.z, g.w ^ s.w);
-    return __builtin_bit_cast(h8, v) * c;
+    // [s << 4, index byte G, 0, 0]: byte 3 of (a1 & 0xF0000000) and byte G of a0
+    const uint32_t ga = __builtin_amdgcn_perm(a0, a1 & 0xF0000000u, 0x0c0c0403u + (G << 8));
+    const uint4 g = *(const uint4 *)(tab + ga);
+    const uint2 sb = *(const uint2 *)(tab + 65536 + (((a1 >> (7 * G)) & 127) << 3));
+    // sign byte e -> bit 15 (e even) / bit 31 (e odd) of half pair e/2: bytes [0, s(2i), 0, s(2i+1)]
+    const uint32_t m0 = __builtin_amdgcn_perm(sb.y, sb.x, 0x010c000cu);
+    const uint32_t m1 = __builtin_amdgcn_perm(sb.y, sb.x, 0x030c020cu);
+    const uint32_t m2 = __builtin_amdgcn_perm(sb.y, sb.x, 0x050c040cu);
+    const uint32_t m3 = __builtin_amdgcn_perm(sb.y, sb.x, 0x070c060cu);
+    return __builtin_bit_cast(h8, make_uint4(g.x ^ m0, g.y ^ m1, g.z ^ m2, g.w ^ m3));
 }
 
 // profiling variants replace single components of the contraction
 #ifdef GS_GRP_PROBE_NOLDSA
-#define GS_GRP_AV(p) __builtin_bit_cast(h8, make_uint4(cc, j, hl, tt))
+#define GS_GRP_AV(p) __builtin_bit_cast(h8, make_uint4(cc, j, 0, tt))
 #else
 #define GS_GRP_AV(p) __builtin_bit_cast(h8, *(const uint4 *)(p))
+#endif
+#ifdef GS_GRP_PROBE_NOBAR   // profiling variant: activation fragments from L2, no staging barrier
+#define GS_GRP_AV_LOAD(tt, cc) __builtin_bit_cast(h8, *(const GS_GLOBAL u4 *)(const GS_GLOBAL uint16_t *)(a.act + ((uint32_t)ar_cur[0] * (uint32_t)K + 256u * b + 8u * (cc) + 16u * (tt))))
+#else
+#define GS_GRP_AV_LOAD(tt, cc) GS_GRP_AV(slab + (16 * (tt) + j) * 512 + (((cc) ^ j) << 4))
 #endif
 #ifdef GS_GRP_PROBE_NOMFMA
 #define GS_GRP_MFMA(A, B, C) ((C) + __builtin_bit_cast(f4, (A) + (B)))
 #else
 #define GS_GRP_MFMA(A, B, C) __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, C, 0, 0, 0)
+#endif
+
+// profiling variant: per-wave cycle sums of the loop phases, written over the first rows of the
+// kernel's output at exit (results are then meaningless; timing runs only)
+#ifdef GS_GRP_PROBE_TS
+#define GS_TS_DECL uint64_t ts_acc[6] = {0, 0, 0, 0, 0, 0}; uint64_t ts_prev = __builtin_readcyclecounter(); const uint64_t ts_begin = ts_prev;
+#define GS_TS_MARK(i) { const uint64_t now_ = __builtin_readcyclecounter(); ts_acc[i] += now_ - ts_prev; ts_prev = now_; }
+#define GS_TS_DUMP(out)                                                                           \
+    if ((threadIdx.x & 63) == 0) {                                                                \
+        float *o_ = (out) + ((size_t)blockIdx.x * WV + (threadIdx.x >> 6)) * 8;                     \
+        for (int i_ = 0; i_ < 6; i_++) o_[i_] = (float)ts_acc[i_];                                \
+        o_[6] = (float)(__builtin_readcyclecounter() - ts_begin);                                 \
+        o_[7] = 1.f;                                                                              \
+    }
+#else
+#define GS_TS_DECL
+#define GS_TS_MARK(i)
+#define GS_TS_DUMP(out)
 #endif
 
 __device__ __forceinline__ float grp_swiglu(float g, float u, float lim) {   // ops.cu:101-115
@@ -115,7 +153,7 @@ __device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb
 }
 
 // KIND 1: gate/up + SwiGLU -> h[pair][rows] (f32).  KIND 2: down, y[token][rows] += w * result.
-// NT token sub-tiles of 16, NR row sub-tiles of 16 per wave, 4 waves per workgroup.
+// NT token sub-tiles of 16, NR row sub-tiles of 16 per wave, WV waves per workgroup.
 //
 // Software pipeline over the workgroup's flat sequence of (tile, super-block) positions, across
 // tile boundaries: weight words are loaded two positions ahead, the activations one position
@@ -125,36 +163,37 @@ __device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb
 // scales, combine weights) during the tile, so no load is waited on right after it is issued.
 // A token row of one super-block is 512 B in LDS (32 chunks of 16 B); chunk c of slot i sits at
 // chunk position c ^ (i & 15), so the 16 lanes that read one chunk column hit 16 bank groups.
-template <int KIND, int NT, int NR>
+template <int KIND, int NT, int NR, int WV>
 __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     constexpr int MATS = KIND == 1 ? 2 : 1;
-    constexpr int HL = KIND == 1 ? 2 : 1;            // activation halves (hi, lo)
     constexpr int MT = 16 * NT;
-    constexpr int RB = GS_GRP_WAVES * 16 * NR;
-    constexpr int NTH = 64 * GS_GRP_WAVES;
-    constexpr int SLAB = HL * MT * 512;              // bytes of one staged super-block
-    constexpr int NLD = SLAB / 16 / NTH;             // 16-byte chunks per thread per super-block
-    static_assert(SLAB % (16 * NTH) == 0, "staging split");
+    constexpr int RB = WV * 16 * NR;
+    constexpr int NTH = 64 * WV;
+    constexpr int SLAB = MT * 512;                   // bytes of one staged super-block
+    constexpr int NCH = SLAB / 16;                   // 16-byte chunks per staged super-block
+    constexpr int NLD = (NCH + NTH - 1) / NTH;       // per thread (the last one may be partial)
     extern __shared__ __align__(16) uint8_t gs_grp_dyn[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4;
     const int K = a.K, rows = a.rows, nsb = K / 256;
     const int nrb = (rows + RB - 1) / RB;
     const uint32_t rs = (uint32_t)a.row_stride;
-    grp_tables(tid);
+    uint8_t *const tab = gs_grp_dyn;
+    uint8_t *const stage = gs_grp_dyn + GS_GRP_TAB_BYTES;
+    grp_tables<NTH>(tab, tid);
     grp_prefix(a, MT, nrb);
     __syncthreads();
     const int total = gs_grp_pre[a.n_exp];
     int t = blockIdx.x;
     if (t >= total) return;
 
-    // staging chunks of this thread: chunk z = tid + NTH*k -> half, slot, chunk column
+    // staging chunks of this thread: chunk z = tid + NTH*k -> slot z >> 5, chunk column z & 31
     int dst[NLD];
 #pragma unroll
     for (int k = 0; k < NLD; k++) {
         const int z = tid + NTH * k;
-        const int i = (z >> 5) % MT, c = z & 31;
-        dst[k] = (z >> 5) / MT * MT * 512 + i * 512 + ((c ^ (i & 15)) << 4);
+        const int i = min(z >> 5, MT - 1), c = z & 31;
+        dst[k] = i * 512 + ((c ^ (i & 15)) << 4);
     }
 
     // ---- tile descriptors ---------------------------------------------------------------------
@@ -187,7 +226,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     auto arows_raw = [&](const Desc &d, int (&ar)[NLD]) {
 #pragma unroll
         for (int k = 0; k < NLD; k++) {
-            const int i = ((tid + NTH * k) >> 5) % MT;
+            const int i = min((tid + NTH * k) >> 5, MT - 1);
             const int p = d.p_beg + min(i, d.n_here - 1);
             ar[k] = KIND == 1 ? a.idx[p] : p;
         }
@@ -205,7 +244,11 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     arows_raw(cur, ar_cur);
     if (has_nxt) arows_raw(nxt, ar_nxt);
 
-    auto load_w = [&](const Desc &d, const uint32_t (&wo)[NR], int b, uint4 (&wq)[NR][MATS], uint32_t (&wd)[NR][MATS]) {
+    struct WRegs {   // one position's raw weight words: 16 bytes (units 2q, 2q+1) + f16 d per row
+        uint4 q[NR][MATS];
+        uint32_t d[NR][MATS];
+    };
+    auto load_w = [&](const Desc &d, const uint32_t (&wo)[NR], int b, WRegs &w) {
 #pragma unroll
         for (int n = 0; n < NR; n++)
 #pragma unroll
@@ -215,34 +258,35 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 #else
                 const uint8_t *p = d.wb[mt] + (wo[n] + 66u * b);
 #endif
-                wq[n][mt] = ldg16(p);
-                wd[n][mt] = ldg2(p - 2 - 16 * q);
+                w.q[n][mt] = ldg16(p);
+                w.d[n][mt] = ldg2(p - 2 - 16 * q);
             }
     };
     auto load_a = [&](const int (&ar)[NLD], int b, u4 (&stg)[NLD]) {
 #pragma unroll
         for (int k = 0; k < NLD; k++) {
             const int z = tid + NTH * k;
-            const uint16_t *base = (z >> 5) / MT ? a.act_lo : a.act;
+            if (NCH % NTH != 0 && z >= NCH) continue;
 #ifdef GS_GRP_PROBE_NOSTG   // profiling variant: no activation staging loads
             stg[k] = u4{(uint32_t)ar[k], (uint32_t)b, (uint32_t)z, 0u};
-            (void)base;
 #else
-            stg[k] = *(const GS_GLOBAL u4 *)(const GS_GLOBAL uint16_t *)(base + ((uint32_t)ar[k] * (uint32_t)K + 256u * b + 8u * (z & 31)));
+            stg[k] = *(const GS_GLOBAL u4 *)(const GS_GLOBAL uint16_t *)(a.act + ((uint32_t)ar[k] * (uint32_t)K + 256u * b + 8u * (z & 31)));
 #endif
         }
     };
 
-    // prologue: weights of positions 0 and 1, activations of position 0
-    uint4 w0q[NR][MATS], w1q[NR][MATS];
-    uint32_t w0d[NR][MATS], w1d[NR][MATS];
+    // prologue: weights of positions 0 and 1, activations of position 0. Three weight register
+    // sets rotate by role (the loop body is instantiated three times), so a set loaded for position
+    // p + 2 is not touched until position p + 2: no register copies, no early waits.
+    WRegs W0, W1, W2;
     {
         u4 stg0[NLD];
         load_a(ar_cur, 0, stg0);
-        load_w(cur, wo_cur, 0, w0q, w0d);
-        load_w(cur, wo_cur, 1, w1q, w1d);
+        load_w(cur, wo_cur, 0, W0);
+        load_w(cur, wo_cur, 1, W1);
 #pragma unroll
-        for (int k = 0; k < NLD; k++) *(u4 *)(gs_grp_dyn + dst[k]) = stg0[k];
+        for (int k = 0; k < NLD; k++)
+            if (NCH % NTH == 0 || tid + NTH * k < NCH) *(u4 *)(stage + dst[k]) = stg0[k];
     }
     __syncthreads();
 
@@ -271,7 +315,8 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             for (int mt = 0; mt < MATS; mt++) acc[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
 
     int b = 0, buf = 0;
-    for (;;) {
+    GS_TS_DECL
+    auto step = [&](WRegs &wu, WRegs &wl) __attribute__((always_inline)) -> bool {
         // ---- issue: activations of position +1, weights of position +2 -------------------
         const bool last_sb = b == nsb - 1;
         const bool have1 = !last_sb || has_nxt;
@@ -282,8 +327,6 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             for (int k = 0; k < NLD; k++) ar[k] = last_sb ? ar_nxt[k] : ar_cur[k];
             load_a(ar, last_sb ? 0 : b + 1, stg);
         }
-        uint4 w2q[NR][MATS];
-        uint32_t w2d[NR][MATS];
         {
             const bool in_cur = b + 2 < nsb;
             if (in_cur || has_nxt) {
@@ -293,7 +336,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 for (int mt = 0; mt < MATS; mt++) d.wb[mt] = in_cur ? cur.wb[mt] : nxt.wb[mt];
 #pragma unroll
                 for (int n = 0; n < NR; n++) wo[n] = in_cur ? wo_cur[n] : wo_nxt[n];
-                load_w(d, wo, in_cur ? b + 2 : b + 2 - nsb, w2q, w2d);
+                load_w(d, wo, in_cur ? b + 2 : b + 2 - nsb, wl);
             }
         }
         if (KIND == 1 && b == nsb / 2) {   // gate/up row scales by token id
@@ -303,9 +346,10 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 for (int i = 0; i < 4; i++) ep_sc[tt][i] = a.ascale[ep_tok[tt][i]];
         }
 
+        GS_TS_MARK(0)
         // ---- contract position (cur, b) ------------------------------------------------------
         {
-            const uint8_t *slab = gs_grp_dyn + buf * SLAB;
+            const uint8_t *slab = stage + buf * SLAB;
             const int n_here = cur.n_here;
             f4 sb[NT][NR][MATS];
 #pragma unroll
@@ -316,29 +360,19 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                     for (int mt = 0; mt < MATS; mt++) sb[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int hu = 0; hu < 2; hu++) {    // unit 2q + hu
-                _Float16 c[NR][MATS];
-#pragma unroll
-                for (int n = 0; n < NR; n++)
-#pragma unroll
-                    for (int mt = 0; mt < MATS; mt++) {
-                        const uint32_t a1 = hu ? w0q[n][mt].w : w0q[n][mt].y;
-                        c[n][mt] = (_Float16)(int)(2 * (a1 >> 28) + 1);
-                    }
 #define GS_GRP_STEP(G)                                                                             \
     {                                                                                              \
         h8 bf[NR][MATS];                                                                           \
         _Pragma("unroll") for (int n = 0; n < NR; n++)                                             \
         _Pragma("unroll") for (int mt = 0; mt < MATS; mt++)                                        \
-            bf[n][mt] = iq2_frag<G>(hu ? w0q[n][mt].z : w0q[n][mt].x, hu ? w0q[n][mt].w : w0q[n][mt].y, c[n][mt]); \
+            bf[n][mt] = iq2_frag<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y); \
         const int cc = 8 * q + 4 * hu + G;                                                         \
         _Pragma("unroll") for (int tt = 0; tt < NT; tt++)                                          \
             if (tt == 0 || 16 * tt < n_here) {                                                     \
-                _Pragma("unroll") for (int hl = 0; hl < HL; hl++) {                                \
-                    const h8 av = GS_GRP_AV(slab + (hl * MT + 16 * tt + j) * 512 + ((cc ^ j) << 4)); \
-                    _Pragma("unroll") for (int n = 0; n < NR; n++)                                 \
-                    _Pragma("unroll") for (int mt = 0; mt < MATS; mt++)                            \
-                        sb[tt][n][mt] = GS_GRP_MFMA(av, bf[n][mt], sb[tt][n][mt]);                 \
-                }                                                                                  \
+                const h8 av = GS_GRP_AV_LOAD(tt, cc);                                              \
+                _Pragma("unroll") for (int n = 0; n < NR; n++)                                     \
+                _Pragma("unroll") for (int mt = 0; mt < MATS; mt++)                                \
+                    sb[tt][n][mt] = GS_GRP_MFMA(av, bf[n][mt], sb[tt][n][mt]);                     \
             }                                                                                      \
     }
                 GS_GRP_STEP(0) GS_GRP_STEP(1) GS_GRP_STEP(2) GS_GRP_STEP(3)
@@ -348,12 +382,13 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             for (int n = 0; n < NR; n++)
 #pragma unroll
                 for (int mt = 0; mt < MATS; mt++) {
-                    const float cd = h2f(w0d[n][mt]) * 0.125f;
+                    const float cd = h2f(wu.d[n][mt]) * 0.125f;
 #pragma unroll
                     for (int tt = 0; tt < NT; tt++) acc[tt][n][mt] += cd * sb[tt][n][mt];
                 }
         }
 
+        GS_TS_MARK(1)
         // ---- tile epilogue: lane holds tokens 16t + 4q + i (i < 4) of row row0 + 16n + j ----
         if (last_sb) {
 #pragma unroll
@@ -384,19 +419,15 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 #pragma unroll
                     for (int mt = 0; mt < MATS; mt++) acc[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
         }
-        if (!have1) break;
+        GS_TS_MARK(2)
+        if (!have1) return false;
 
         // ---- advance: stage position +1, rotate the weight registers -------------------------
 #pragma unroll
-        for (int k = 0; k < NLD; k++) *(u4 *)(gs_grp_dyn + (buf ^ 1) * SLAB + dst[k]) = stg[k];
-#pragma unroll
-        for (int n = 0; n < NR; n++)
-#pragma unroll
-            for (int mt = 0; mt < MATS; mt++) {
-                w0q[n][mt] = w1q[n][mt]; w0d[n][mt] = w1d[n][mt];
-                w1q[n][mt] = w2q[n][mt]; w1d[n][mt] = w2d[n][mt];
-            }
+        for (int k = 0; k < NLD; k++)
+            if (NCH % NTH == 0 || tid + NTH * k < NCH) *(u4 *)(stage + (buf ^ 1) * SLAB + dst[k]) = stg[k];
         buf ^= 1;
+        GS_TS_MARK(3)
         if (last_sb) {   // enter the next tile; fetch the one after it
             b = 0;
             t += tstep;
@@ -415,32 +446,50 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         } else {
             b++;
         }
+        GS_TS_MARK(4)
+#ifndef GS_GRP_PROBE_NOBAR
         __syncthreads();
+#endif
+        GS_TS_MARK(5)
+        return true;
+    };
+    for (;;) {
+        if (!step(W0, W2)) break;
+        if (!step(W1, W0)) break;
+        if (!step(W2, W1)) break;
     }
+    GS_TS_DUMP(a.out)
 }
 
-#define GS_GRP_KERNEL(KIND, NT, NR)                                                              \
-    extern "C" __global__ void __launch_bounds__(64 * GS_GRP_WAVES)                             \
-        gs_k_grouped_16_##KIND##_##NT##_##NR(GroupedArgs a) {                                   \
-        grouped_body<KIND, NT, NR>(a);                                                          \
+#define GS_GRP_KERNEL(KIND, NT, NR, WV)                                                          \
+    extern "C" __global__ void __launch_bounds__(64 * WV)                                       \
+        gs_k_grouped_16_##KIND##_##NT##_##NR##_##WV(GroupedArgs a) {                            \
+        grouped_body<KIND, NT, NR, WV>(a);                                                      \
     }
-GS_GRP_KERNEL(1, 1, 1)
-GS_GRP_KERNEL(1, 1, 2)
-GS_GRP_KERNEL(1, 2, 1)
-GS_GRP_KERNEL(1, 2, 2)
-GS_GRP_KERNEL(1, 2, 4)
-GS_GRP_KERNEL(2, 1, 1)
-GS_GRP_KERNEL(2, 1, 2)
-GS_GRP_KERNEL(2, 2, 2)
-GS_GRP_KERNEL(2, 2, 4)
-GS_GRP_KERNEL(2, 4, 4)
+// instantiated (kind, NT, NR, waves) tile shapes; host.cpp grouped_launch keeps the same list
+GS_GRP_KERNEL(1, 1, 1, 8)
+GS_GRP_KERNEL(1, 1, 2, 8)
+GS_GRP_KERNEL(1, 2, 1, 8)
+GS_GRP_KERNEL(1, 2, 2, 8)
+GS_GRP_KERNEL(1, 4, 1, 8)
+GS_GRP_KERNEL(1, 1, 1, 16)
+GS_GRP_KERNEL(2, 1, 1, 8)
+GS_GRP_KERNEL(2, 1, 2, 8)
+GS_GRP_KERNEL(2, 1, 4, 8)
+GS_GRP_KERNEL(2, 2, 1, 8)
+GS_GRP_KERNEL(2, 2, 2, 8)
+GS_GRP_KERNEL(2, 2, 4, 8)
+GS_GRP_KERNEL(2, 4, 1, 8)
+GS_GRP_KERNEL(2, 4, 2, 8)
+GS_GRP_KERNEL(2, 1, 1, 16)
+GS_GRP_KERNEL(2, 1, 2, 16)
+GS_GRP_KERNEL(2, 2, 1, 16)
 
 // ---------------------------------------------------------------------------------------------
-// Activation rows -> f16 MFMA operands. Each 32-element unit is q8_1-quantized exactly as the
-// streaming kernels do (d = amax/127, q = round(x/d), D = f16(d)); the f16 operand is
-// D*q*2^-E with 2^E >= 2 * row amax, so no value overflows f16 and the relative rounding error
-// stays below 2^-11. scale[row] = 2^E restores the magnitude in the GEMM epilogue.
-// One wave per row, 4 rows per workgroup.
+// Activation rows -> f16 MFMA operands: out = f16(x * 2^-E), scale[row] = 2^E, with 2^E the
+// power of two that puts the row's largest magnitude in [2^14, 2^15). Where f16(x) is normal this
+// is exactly f16(x) (scaling by a power of two commutes with rounding); rows with values beyond
+// the f16 range stay finite, and small rows keep full precision. One wave per row, 4 per block.
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -448,57 +497,28 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-extern "C" __global__ void __launch_bounds__(256) gs_k_rows_q8f16(RowsQArgs a) {
+extern "C" __global__ void __launch_bounds__(256) gs_k_rows_f16(RowsQArgs a) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.nrows) return;
-    const int nu = a.K / 32;
-    const float *src = a.x + (int64_t)row * a.x_stride;
+    const int n8 = a.K / 8;
+    const float4 *src = (const float4 *)(a.x + (int64_t)row * a.x_stride);
     float amax = 0.f;
-    for (int u = lane; u < nu; u += 64) {
-        const float4 *p = (const float4 *)(src + 32 * u);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 f = p[i];
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
-        }
+    for (int u = lane; u < n8; u += 64) {
+        const float4 f0 = src[2 * u], f1 = src[2 * u + 1];
+        amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(f0.x), fabsf(f0.y)), fmaxf(fabsf(f0.z), fabsf(f0.w))),
+                                 fmaxf(fmaxf(fabsf(f1.x), fabsf(f1.y)), fmaxf(fabsf(f1.z), fabsf(f1.w)))));
     }
     amax = wave_max(amax);
     int E = 0;
-    if (amax > 0.f) (void)frexpf(amax, &E);   // amax < 2^E
-    E -= 14;                                     // values * 2^-E < 2^14 (D rounding stays below 2^15)
+    if (amax > 0.f && amax <= 3.4e38f) (void)frexpf(amax, &E);   // amax < 2^E
+    E -= 15;
     const float down = ldexpf(1.f, -E);
     if (lane == 0) a.scale[row] = ldexpf(1.f, E);
-    uint16_t *dst = a.out + (int64_t)row * a.K;
-    for (int u = lane; u < nu; u += 64) {
-        float v[32];
-        const float4 *p = (const float4 *)(src + 32 * u);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 f = p[i];
-            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-        }
-        float m = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; i++) m = fmaxf(m, fabsf(v[i]));
-        const float d = m / 127.0f;
-        const float id = d != 0.f ? 1.0f / d : 0.f;
-        const float D = h2f(f2h(d)) * down;
-        uint32_t o[16], ol[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float v0 = D * __builtin_roundf(v[2 * i] * id), v1 = D * __builtin_roundf(v[2 * i + 1] * id);
-            const uint32_t h0 = f2h(v0), h1 = f2h(v1);
-            o[i] = h0 | (h1 << 16);
-            ol[i] = f2h(v0 - h2f(h0)) | (f2h(v1 - h2f(h1)) << 16);   // exact remainders
-        }
-        uint4 *d4 = (uint4 *)(dst + 32 * u);
-#pragma unroll
-        for (int i = 0; i < 4; i++) d4[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
-        if (a.out_lo) {
-            uint4 *l4 = (uint4 *)(a.out_lo + (int64_t)row * a.K + 32 * u);
-#pragma unroll
-            for (int i = 0; i < 4; i++) l4[i] = make_uint4(ol[4 * i], ol[4 * i + 1], ol[4 * i + 2], ol[4 * i + 3]);
-        }
+    uint4 *dst = (uint4 *)(a.out + (int64_t)row * a.K);
+    for (int u = lane; u < n8; u += 64) {
+        const float4 f0 = src[2 * u], f1 = src[2 * u + 1];
+        dst[u] = make_uint4(f2h(f0.x * down) | (f2h(f0.y * down) << 16), f2h(f0.z * down) | (f2h(f0.w * down) << 16),
+                            f2h(f1.x * down) | (f2h(f1.y * down) << 16), f2h(f1.z * down) | (f2h(f1.w * down) << 16));
     }
 }

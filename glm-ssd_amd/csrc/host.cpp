@@ -520,13 +520,12 @@ GS_EXPORT int gs_scatter_add_rows(float *acc, const int *idx, const float *w, co
 namespace {
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 struct GroupedWork {
-    size_t x16, x16lo, xs, h, h16, hs, total;
+    size_t x16, xs, h, h16, hs, total;
 };
 GroupedWork grouped_layout(int n_tok, int n_pairs, int K, int n_ff) {
     GroupedWork w;
     size_t o = 0;
     w.x16 = o; o += align256((size_t)n_tok * K * 2);
-    w.x16lo = o; o += align256((size_t)n_tok * K * 2);
     w.xs = o;  o += align256((size_t)n_tok * 4);
     w.h = o;   o += align256((size_t)n_pairs * n_ff * 4);
     w.h16 = o; o += align256((size_t)n_pairs * n_ff * 2);
@@ -535,46 +534,61 @@ GroupedWork grouped_layout(int n_tok, int n_pairs, int K, int n_ff) {
     return w;
 }
 
-hipError_t rows_q8f16(const float *x, int64_t x_stride, int K, int nrows, uint16_t *out, uint16_t *out_lo, float *scale,
-                      hipStream_t s) {
+hipError_t rows_f16(const float *x, int64_t x_stride, int K, int nrows, uint16_t *out, float *scale, hipStream_t s) {
     if (nrows <= 0) return hipSuccess;
-    RowsQArgs a{x, x_stride, out, out_lo, scale, K, nrows};
-    return launch("gs_k_rows_q8f16", dim3((nrows + 3) / 4), dim3(256), 0, s, a);
+    RowsQArgs a{x, x_stride, out, scale, K, nrows};
+    return launch("gs_k_rows_f16", dim3((nrows + 3) / 4), dim3(256), 0, s, a);
 }
 
 // kind 1 (gate/up) or 2 (down) over every tile of the layer; the grid is persistent.
-// Tile shape: NT token sub-tiles of 16 (the chunk of one expert's pairs a workgroup takes) and NR
-// row sub-tiles of 16 per wave. Larger tiles stage fewer activation bytes per weight byte, but the
-// tile count must still fill the chip: take the largest NR whose (upper-bound) tile count is at
-// least two per CU. Instantiated shapes: grouped.hip GS_GRP_KERNEL.
+// Tile shape: NT token sub-tiles of 16 (the chunk of one expert's pairs a workgroup takes), NR row
+// sub-tiles of 16 per wave, WV waves per workgroup (one workgroup per CU shares the 65 KB decode
+// table; WV = 16 doubles the waves available to hide latency where registers allow). Larger
+// tiles stage fewer activation bytes per weight byte, but the tile count must still fill the
+// chip: take the first preferred shape whose (upper-bound) tile count is at least two per CU.
+// Instantiated shapes: grouped.hip GS_GRP_KERNEL.
+struct GrpShape {
+    int nt, nr, wv;
+};
 hipError_t grouped_launch(int kind, GroupedArgs &a, int n_pairs, hipStream_t s) {
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
     auto env = [](const char *n) { return getenv(n) ? atoi(getenv(n)) : 0; };
-    static const int nt1 = env("GLMSSD_GRP_NT1"), nr1 = env("GLMSSD_GRP_NR1");
-    static const int nt2 = env("GLMSSD_GRP_NT2"), nr2 = env("GLMSSD_GRP_NR2");
-    const std::vector<std::pair<int, int>> shapes =
-        kind == 1 ? std::vector<std::pair<int, int>>{{1, 1}, {1, 2}, {2, 1}, {2, 2}, {2, 4}}
-                  : std::vector<std::pair<int, int>>{{1, 1}, {1, 2}, {2, 2}, {2, 4}, {4, 4}};
-    int nt = n_pairs <= 64 ? 1 : 2;
-    if ((kind == 1 ? nt1 : nt2) > 0) nt = kind == 1 ? nt1 : nt2;
+    static const int nt1 = env("GLMSSD_GRP_NT1"), nr1 = env("GLMSSD_GRP_NR1"), wv1 = env("GLMSSD_GRP_WV1");
+    static const int nt2 = env("GLMSSD_GRP_NT2"), nr2 = env("GLMSSD_GRP_NR2"), wv2 = env("GLMSSD_GRP_WV2");
+    static const std::vector<GrpShape> all1 = {{1, 1, 8}, {1, 2, 8}, {2, 1, 8}, {2, 2, 8}, {4, 1, 8}, {1, 1, 16}};
+    static const std::vector<GrpShape> all2 = {{1, 1, 8}, {1, 2, 8}, {1, 4, 8}, {2, 1, 8}, {2, 2, 8}, {2, 4, 8},
+                                               {4, 1, 8}, {4, 2, 8}, {1, 1, 16}, {1, 2, 16}, {2, 1, 16}};
+    // preference order (largest useful tile first), per token-chunk size
+    static const std::vector<GrpShape> pref1 = {{2, 2, 8}, {2, 1, 8}, {1, 2, 8}, {1, 1, 16}, {1, 1, 8}};
+    static const std::vector<GrpShape> pref2 = {{2, 4, 8}, {2, 2, 8}, {1, 4, 8}, {1, 2, 8}, {2, 1, 8}, {1, 1, 8}};
     const int groups = std::min(a.n_exp, n_pairs);
-    int nr = 0;
-    for (const auto &sh : shapes) {
-        if (sh.first != nt) continue;
-        const int64_t rbk = GS_GRP_WAVES * 16 * sh.second;
-        const int64_t tiles = (a.rows + rbk - 1) / rbk * (groups + (n_pairs + 16 * nt - 1) / (16 * nt));
-        if (nr == 0 || tiles >= 2 * (int64_t)c->cu_count) nr = std::max(nr, sh.second);
+    auto tiles = [&](const GrpShape &sh) {
+        const int64_t rbk = (int64_t)sh.wv * 16 * sh.nr;
+        return (a.rows + rbk - 1) / rbk * (groups + (n_pairs + 16 * sh.nt - 1) / (16 * sh.nt));
+    };
+    GrpShape sh{0, 0, 0};
+    for (const GrpShape &p : kind == 1 ? pref1 : pref2) {
+        if ((n_pairs <= 64) != (p.nt == 1)) continue;    // decode-sized batches: one token sub-tile
+        sh = p;
+        if (tiles(p) >= 2 * (int64_t)c->cu_count) break;
     }
-    if ((kind == 1 ? nr1 : nr2) > 0) nr = kind == 1 ? nr1 : nr2;
-    if (std::find(shapes.begin(), shapes.end(), std::make_pair(nt, nr)) == shapes.end()) return hipErrorInvalidValue;
-    const std::string name = "gs_k_grouped_16_" + std::to_string(kind) + "_" + std::to_string(nt) + "_" +
-                             std::to_string(nr);
+    const int ent = kind == 1 ? nt1 : nt2, enr = kind == 1 ? nr1 : nr2, ewv = kind == 1 ? wv1 : wv2;
+    if (ent > 0) sh.nt = ent;
+    if (enr > 0) sh.nr = enr;
+    if (ewv > 0) sh.wv = ewv;
+    const auto &all = kind == 1 ? all1 : all2;
+    if (std::none_of(all.begin(), all.end(),
+                     [&](const GrpShape &p) { return p.nt == sh.nt && p.nr == sh.nr && p.wv == sh.wv; }))
+        return hipErrorInvalidValue;
+    const std::string name = "gs_k_grouped_16_" + std::to_string(kind) + "_" + std::to_string(sh.nt) + "_" +
+                             std::to_string(sh.nr) + "_" + std::to_string(sh.wv);
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
-    const int threads = 64 * GS_GRP_WAVES;
-    const size_t lds = 2 * (size_t)(kind == 1 ? 2 : 1) * 16 * nt * 512;   // two staged super-blocks
+    const int threads = 64 * sh.wv;
+    // decode tables (65 KB) + two staged activation super-blocks
+    const size_t lds = 65536 + 1024 + 2 * (size_t)16 * sh.nt * 512;
     int per_cu = 1;
     {
         std::lock_guard<std::mutex> lk(g_mu);
@@ -588,10 +602,7 @@ hipError_t grouped_launch(int kind, GroupedArgs &a, int n_pairs, hipStream_t s) 
             c->occ[key] = per_cu = nb;
         }
     }
-    const int rb = GS_GRP_WAVES * 16 * nr, mt = 16 * nt;
-    const int64_t nrb = (a.rows + rb - 1) / rb;
-    const int64_t bound = nrb * (groups + (n_pairs + mt - 1) / mt);
-    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, (int64_t)c->cu_count * per_cu));
+    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(tiles(sh), (int64_t)c->cu_count * per_cu));
     return launch(name, dim3(grid), dim3(threads), lds, s, a);
 }
 }  // namespace
@@ -617,10 +628,10 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
     const GroupedWork L = grouped_layout(n_tok, n_pairs, K, n_ff);
     if (!work || work_bytes < L.total) return hipErrorInvalidValue;
     uint8_t *wb = (uint8_t *)work;
-    uint16_t *x16 = (uint16_t *)(wb + L.x16), *x16lo = (uint16_t *)(wb + L.x16lo), *h16 = (uint16_t *)(wb + L.h16);
+    uint16_t *x16 = (uint16_t *)(wb + L.x16), *h16 = (uint16_t *)(wb + L.h16);
     float *xs = (float *)(wb + L.xs), *h = (float *)(wb + L.h), *hs = (float *)(wb + L.hs);
     hipStream_t st = (hipStream_t)s;
-    hipError_t e = rows_q8f16(x, K, K, n_tok, x16, x16lo, xs, st);
+    hipError_t e = rows_f16(x, K, K, n_tok, x16, xs, st);
     if (e != hipSuccess) return e;
     GroupedArgs a;
     memset(&a, 0, sizeof(a));
@@ -629,7 +640,6 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
     a.idx = idx;
     a.w = w;
     a.act = x16;
-    a.act_lo = x16lo;
     a.ascale = xs;
     a.out = h;
     a.row_stride = gu_row_stride;
@@ -638,9 +648,8 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
     a.n_exp = n_exp;
     a.lim = lim;
     if ((e = grouped_launch(1, a, n_pairs, st)) != hipSuccess) return e;
-    if ((e = rows_q8f16(h, n_ff, n_ff, n_pairs, h16, nullptr, hs, st)) != hipSuccess) return e;
+    if ((e = rows_f16(h, n_ff, n_ff, n_pairs, h16, hs, st)) != hipSuccess) return e;
     a.act = h16;
-    a.act_lo = nullptr;
     a.ascale = hs;
     a.out = y;
     a.row_stride = down_row_stride;

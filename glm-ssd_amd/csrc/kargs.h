@@ -77,14 +77,12 @@ struct RowsArgs {
 
 // Grouped MoE GEMM (grouped.hip): pairs sorted by expert, offs = CSR offsets per expert.
 #define GS_GRP_EXP_MAX 1024   // experts per layer the device-side tile list holds
-#define GS_GRP_WAVES 4        // waves per workgroup
 struct GroupedArgs {
     const uint8_t *const *experts;   // [n_exp][3] device pointers: gate, up, down
     const int *offs;                 // [n_exp + 1] pair offsets
     const int *idx;                  // [n_pairs] token of each pair
     const float *w;                  // [n_pairs] combine weights (kind 2)
     const uint16_t *act;             // f16 activation rows (x16 [n_tok][K] or h16 [n_pairs][K])
-    const uint16_t *act_lo;          // kind 1: f16 remainders, act + act_lo == the q8_1 value exactly
     const float *ascale;             // per activation row: power-of-two scale of act
     float *out;                      // kind 1: h [n_pairs][rows]; kind 2: y [n_tok][rows] (+=)
     int64_t row_stride;              // bytes between weight rows
@@ -94,12 +92,11 @@ struct GroupedArgs {
     float lim;                       // SwiGLU clamp (<= 0: none)
 };
 
-// f32 rows -> f16 q8_1 values with a power-of-two row scale (grouped GEMM operands)
+// f32 rows -> f16 with a power-of-two row scale (grouped GEMM operands)
 struct RowsQArgs {
     const float *x;
     int64_t x_stride;   // floats between rows
     uint16_t *out;      // [nrows][K]
-    uint16_t *out_lo;   // optional [nrows][K]: f16(v - f16(v)), so out + out_lo is exact
     float *scale;       // [nrows]
     int K;
     int nrows;

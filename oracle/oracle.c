@@ -438,6 +438,7 @@ typedef struct {
     int64_t row_stride;
     const float *xh; /* [B][K] dequantized activations */
     double *y;
+    int mode;        /* OR_ACT_*: OR_ACT_F16 also rounds the dequantized weights to half */
 } gemv_job;
 
 static void *gemv_worker(void *p) {
@@ -445,6 +446,8 @@ static void *gemv_worker(void *p) {
     float *w = (float *)malloc(sizeof(float) * (size_t)j->K);
     for (int r = j->r0; r < j->r1; r++) {
         or_dequantize(j->ty, j->W + (int64_t)r * j->row_stride, j->K, w);
+        if (j->mode == OR_ACT_F16)
+            for (int k = 0; k < j->K; k++) w[k] = or_f16_to_f32(or_f32_to_f16(w[k]));
         for (int b = 0; b < j->B; b++) {
             const float *xv = j->xh + (int64_t)b * j->K;
             double acc = 0.0;
@@ -456,8 +459,12 @@ static void *gemv_worker(void *p) {
     return NULL;
 }
 
-static void quant_dequant_row(const float *x, int K, float *xh, int quant) {
-    if (!quant) { memcpy(xh, x, sizeof(float) * (size_t)K); return; }
+static void quant_dequant_row(const float *x, int K, float *xh, int mode) {
+    if (mode == OR_ACT_F32) { memcpy(xh, x, sizeof(float) * (size_t)K); return; }
+    if (mode == OR_ACT_F16) {
+        for (int k = 0; k < K; k++) xh[k] = or_f16_to_f32(or_f32_to_f16(x[k]));
+        return;
+    }
     uint8_t *q = (uint8_t *)malloc((size_t)(K / 32) * OR_Q8_1_BYTES);
     or_quantize_q8_1(x, K, q);
     or_dequantize_q8_1(q, K, xh);
@@ -467,7 +474,7 @@ static void quant_dequant_row(const float *x, int K, float *xh, int quant) {
 int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
             int B, int quant_x, double *y, int nthreads) {
     int be, bb;
-    if (or_block(ty, &be, &bb) != 0 || K % be != 0 || K % 32 != 0 || B < 1) return -1;
+    if (or_block(ty, &be, &bb) != 0 || K % be != 0 || K % 32 != 0 || B < 1 || quant_x < 0 || quant_x > 2) return -1;
     float *xh = (float *)malloc(sizeof(float) * (size_t)K * B);
     for (int b = 0; b < B; b++) quant_dequant_row(x + (int64_t)b * x_stride, K, xh + (int64_t)b * K, quant_x);
     if (nthreads < 1) nthreads = 1;
@@ -476,7 +483,7 @@ int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const
     pthread_t *th = (pthread_t *)calloc((size_t)nthreads, sizeof(pthread_t));
     for (int t = 0; t < nthreads; t++) {
         gemv_job j = {ty, K, rows, B, (int)((int64_t)rows * t / nthreads), (int)((int64_t)rows * (t + 1) / nthreads),
-                      W, row_stride, xh, y};
+                      W, row_stride, xh, y, quant_x};
         jobs[t] = j;
         if (nthreads == 1) gemv_worker(&jobs[t]);
         else pthread_create(&th[t], NULL, gemv_worker, &jobs[t]);
@@ -501,7 +508,7 @@ double or_swiglu(double g, double u, double lim) {
 int or_moe_ffn(int ty_gu, int ty_down, const uint8_t *const *gate, const uint8_t *const *up,
                const uint8_t *const *down, int64_t gu_row_stride, int64_t down_row_stride, int n_embd, int n_ff,
                int T, const float *x, int n_pairs, const int *pair_tok, const int *pair_exp, const float *pair_w,
-               float lim, double *y, float *h_out, int nthreads) {
+               float lim, double *y, float *h_out, int nthreads, int act_mode) {
     double *g = (double *)malloc(sizeof(double) * (size_t)n_ff);
     double *u = (double *)malloc(sizeof(double) * (size_t)n_ff);
     double *o = (double *)malloc(sizeof(double) * (size_t)n_embd);
@@ -511,11 +518,11 @@ int or_moe_ffn(int ty_gu, int ty_down, const uint8_t *const *gate, const uint8_t
         int t = pair_tok[p], e = pair_exp[p];
         if (t < 0 || t >= T) { rc = -1; break; }
         const float *xt = x + (int64_t)t * n_embd;
-        rc |= or_gemv(ty_gu, gate[e], gu_row_stride, n_embd, n_ff, xt, n_embd, 1, 1, g, nthreads);
-        rc |= or_gemv(ty_gu, up[e], gu_row_stride, n_embd, n_ff, xt, n_embd, 1, 1, u, nthreads);
+        rc |= or_gemv(ty_gu, gate[e], gu_row_stride, n_embd, n_ff, xt, n_embd, 1, act_mode, g, nthreads);
+        rc |= or_gemv(ty_gu, up[e], gu_row_stride, n_embd, n_ff, xt, n_embd, 1, act_mode, u, nthreads);
         for (int r = 0; r < n_ff; r++) h[r] = (float)or_swiglu(g[r], u[r], lim);
         if (h_out) memcpy(h_out + (int64_t)p * n_ff, h, sizeof(float) * (size_t)n_ff);
-        rc |= or_gemv(ty_down, down[e], down_row_stride, n_ff, n_embd, h, n_ff, 1, 1, o, nthreads);
+        rc |= or_gemv(ty_down, down[e], down_row_stride, n_ff, n_embd, h, n_ff, 1, act_mode, o, nthreads);
         if (pair_w[p] != 0.0f)
             for (int r = 0; r < n_embd; r++) y[(int64_t)t * n_embd + r] += (double)pair_w[p] * o[r];
     }

@@ -38,8 +38,16 @@ uint64_t or_rng_next(uint64_t *state);
 float or_rng_f32(uint64_t *state);
 int or_random_blocks(int ty, int64_t n_elems, uint64_t *state, uint8_t *out);
 
-/* y[b*rows + r] = sum_k deq(W)[r][k] * xhat[b][k] in f64, xhat = deq(q8_1(x[b])) when
- * quant_x != 0, else x itself. nthreads > 1 splits rows over pthreads. */
+/* y[b*rows + r] = sum_k what[r][k] * xhat[b][k] in f64. Activation modes (quant_x):
+ *   OR_ACT_F32  (0): xhat = x, what = deq(W)
+ *   OR_ACT_Q8_1 (1): xhat = deq(q8_1(x)), what = deq(W)          (this build's GEMV / fused decode)
+ *   OR_ACT_F16  (2): xhat = f16(x), what = f16(deq(W))            (the reference's multi-token GEMM,
+ *                    crates/cuda/kernels/gemm.cu:57-78: weights dequantized then rounded to half,
+ *                    activations converted to half, f32 accumulation)
+ * nthreads > 1 splits rows over pthreads. */
+#define OR_ACT_F32 0
+#define OR_ACT_Q8_1 1
+#define OR_ACT_F16 2
 int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
             int B, int quant_x, double *y, int nthreads);
 
@@ -47,13 +55,15 @@ int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const
 double or_swiglu(double g, double u, double lim);
 
 /* Routed-expert FFN for T tokens over n_pairs (token, expert, weight) pairs:
- *   x̂ = deq(q8_1(x[t])); g = gate_e·x̂; u = up_e·x̂; h = swiglu(g,u,lim) (rounded to f32);
- *   ĥ = deq(q8_1(h)); y[t] += w * down_e·ĥ.   (f64 throughout; y is added to, not cleared)
- * experts: pointer arrays indexed by expert id. h_out (optional) gets h per pair [n_pairs][n_ff]. */
+ *   g = gate_e·x̂; u = up_e·x̂; h = swiglu(g,u,lim) (rounded to f32); y[t] += w * down_e·ĥ,
+ * with x̂, ĥ and the weights as or_gemv's act_mode says (OR_ACT_Q8_1: the fused decode path,
+ * quants.cu:279-363; OR_ACT_F16: the multi-token path, forward.rs:1399-1413 over gemm.cu).
+ * f64 throughout; y is added to, not cleared. experts: pointer arrays indexed by expert id.
+ * h_out (optional) gets h per pair [n_pairs][n_ff]. */
 int or_moe_ffn(int ty_gu, int ty_down, const uint8_t *const *gate, const uint8_t *const *up,
                const uint8_t *const *down, int64_t gu_row_stride, int64_t down_row_stride, int n_embd, int n_ff,
                int T, const float *x, int n_pairs, const int *pair_tok, const int *pair_exp, const float *pair_w,
-               float lim, double *y, float *h_out, int nthreads);
+               float lim, double *y, float *h_out, int nthreads, int act_mode);
 
 #ifdef __cplusplus
 }

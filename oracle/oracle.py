@@ -38,7 +38,7 @@ def lib():
         L.or_swiglu.restype = C.c_double
         L.or_swiglu.argtypes = [C.c_double, C.c_double, C.c_double]
         L.or_moe_ffn.argtypes = [C.c_int, C.c_int, _P, _P, _P, C.c_int64, C.c_int64, C.c_int, C.c_int, C.c_int, _P,
-                                 C.c_int, _P, _P, _P, C.c_float, _P, _P, C.c_int]
+                                 C.c_int, _P, _P, _P, C.c_float, _P, _P, C.c_int, C.c_int]
         for name, ty in [("or_table_ksigns", C.c_uint8), ("or_table_iq2xxs", C.c_uint64), ("or_table_iq2s", C.c_uint64),
                          ("or_table_iq3xxs", C.c_uint32), ("or_table_iq4nl", C.c_int8)]:
             getattr(L, name).restype = C.POINTER(ty)
@@ -111,21 +111,28 @@ class Rng:
         return out
 
 
-def gemv(ty, W, row_stride, K, rows, x, B=1, x_stride=None, quant_x=True, nthreads=1):
-    """f64 y[B][rows] = deq(W) . deq(q8_1(x[b]))."""
+ACT = {"f32": 0, "q8_1": 1, "f16": 2}
+
+
+def gemv(ty, W, row_stride, K, rows, x, B=1, x_stride=None, quant_x=True, nthreads=1, act=None):
+    """f64 y[B][rows] = deq(W) . deq(q8_1(x[b])) (act "q8_1", the default), deq(W) . x (act "f32" or
+    quant_x=False), or f16(deq(W)) . f16(x) (act "f16", the reference's multi-token GEMM)."""
+    mode = ACT[act] if act is not None else (1 if quant_x else 0)
     W = np.ascontiguousarray(W, dtype=np.uint8)
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty((B, rows), dtype=np.float64)
     rc = lib().or_gemv(ty, _ptr(W), row_stride, K, rows, _ptr(x), K if x_stride is None else x_stride, B,
-                       1 if quant_x else 0, _ptr(y), nthreads)
+                       mode, _ptr(y), nthreads)
     if rc != 0:
         raise ValueError("or_gemv failed")
     return y
 
 
 def moe_ffn(ty_gu, ty_down, gate, up, down, gu_row_stride, down_row_stride, n_embd, n_ff, x, pair_tok, pair_exp,
-            pair_w, lim=0.0, nthreads=1, want_h=False):
-    """Routed-expert FFN oracle. gate/up/down: lists of uint8 arrays indexed by expert id."""
+            pair_w, lim=0.0, nthreads=1, want_h=False, act="q8_1"):
+    """Routed-expert FFN oracle. gate/up/down: lists of uint8 arrays indexed by expert id.
+    act: "q8_1" (fused decode path: q8_1 activations) or "f16" (multi-token GEMM path, gemm.cu:
+    half activations and half-rounded dequantized weights)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     T = x.shape[0]
     n_exp = len(gate)
@@ -141,7 +148,7 @@ def moe_ffn(ty_gu, ty_down, gate, up, down, gu_row_stride, down_row_stride, n_em
     rc = lib().or_moe_ffn(ty_gu, ty_down, C.c_void_p(base), C.c_void_p(base + n_exp * ps),
                           C.c_void_p(base + 2 * n_exp * ps), gu_row_stride, down_row_stride, n_embd, n_ff, T, _ptr(x),
                           len(pt), _ptr(pt), _ptr(pe), _ptr(pw), lim, _ptr(y),
-                          _ptr(h) if want_h else None, nthreads)
+                          _ptr(h) if want_h else None, nthreads, ACT[act])
     if rc != 0:
         raise ValueError("or_moe_ffn failed")
     return (y, h) if want_h else y

@@ -78,4 +78,4 @@ def test_moe_grouped_rejects_bad_arguments():
     assert call(n_pairs=0) == 0                      # nothing to do, nothing launched
     n = C.c_size_t()
     assert L.gs_moe_grouped_workspace(512, 4096, 4096, 1536, C.byref(n)) == 0
-    assert n.value >= 512 * 4096 * 4 + 4096 * 1536 * 6
+    assert n.value >= 512 * 4096 * 2 + 4096 * 1536 * 6   # x16, h (f32) and h16

@@ -1,6 +1,8 @@
 """GPU parity of the grouped routed-expert FFN (gs_moe_grouped, the MFMA path for prefill and
-MTP verify) against the CPU oracle's per-pair FFN (oracle/or_moe_ffn: q8_1 activations on x and
-h, f64 accumulation). Output tolerance: rel-L2 <= 1e-3 (north-star bound for FFN outputs)."""
+MTP verify) against the CPU oracle's per-pair FFN in the reference's multi-token GEMM semantics
+(oracle/or_moe_ffn with act="f16": half activations x and h, half-rounded dequantized weights,
+f64 accumulation; crates/cuda/kernels/gemm.cu:57-78 under forward.rs:1399-1413). Output tolerance:
+rel-L2 <= 1e-3 (north-star bound for FFN outputs)."""
 import sys
 
 import numpy as np
@@ -43,7 +45,7 @@ def run_case(n_exp, n_tok, k, n_embd, n_ff, seed, lim=0.0, routes=None, zero_w=F
     layer = M.ResidentMoeLayer(gate, up, down, n_embd, n_ff)
     offs, idx, w, pe = layer.upload_routes(routes)
     want = O.moe_ffn(ty, ty, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, x, idx, pe, w, lim=lim,
-                     nthreads=8)
+                     nthreads=8, act="f16")
     y0 = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
     s = G.Stream()
     dx, dy = G.DeviceBuffer.from_array(x), G.DeviceBuffer.from_array(y0)

@@ -267,3 +267,47 @@ def test_moe_ffn_bruteforce():
         if w != 0:
             want[t] += np.float64(np.float32(w)) * D
     assert np.allclose(y, want, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("ty", [O.IQ2_XXS, O.Q4_K])
+def test_gemv_f16_mode_matches_numpy_half_casts(ty):
+    # OR_ACT_F16 = the reference's multi-token GEMM (gemm.cu:57-78): dequantized weights rounded to
+    # half, activations converted to half, then an exact-ish dot. numpy's float16 cast is an
+    # independent IEEE round-to-nearest-even implementation.
+    K, rows, B = 512, 29, 3
+    rng = O.Rng(777 + ty)
+    W = rng.random_blocks(ty, rows * K)
+    x = (np.random.default_rng(ty).standard_normal((B, K)) * 3).astype(np.float32)
+    x[0, :8] = [65519.0, -65520.0, 6e-8, -3e-8, 1e-5, 2.0 ** -24, 0.0, -0.0]   # overflow / subnormal edges
+    y = O.gemv(ty, W, O.row_bytes(ty, K), K, rows, x, B=B, act="f16")
+    Wd = O.dequantize(ty, W, rows * K).reshape(rows, K).astype(np.float16).astype(np.float64)
+    with np.errstate(over="ignore"):
+        xh = x.astype(np.float16).astype(np.float64)
+    want = xh @ Wd.T
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isfinite(y), fin)
+    assert np.allclose(y[fin], want[fin], rtol=1e-12, atol=1e-9)
+
+
+def test_moe_ffn_f16_mode_bruteforce():
+    n_embd, n_ff, n_exp, T = 256, 512, 3, 2
+    rng = O.Rng(4242)
+    rb, rbd = O.row_bytes(O.IQ2_XXS, n_embd), O.row_bytes(O.IQ2_XXS, n_ff)
+    gate = [rng.random_blocks(O.IQ2_XXS, n_ff * n_embd) for _ in range(n_exp)]
+    up = [rng.random_blocks(O.IQ2_XXS, n_ff * n_embd) for _ in range(n_exp)]
+    down = [rng.random_blocks(O.IQ2_XXS, n_embd * n_ff) for _ in range(n_exp)]
+    x = np.random.default_rng(5).standard_normal((T, n_embd)).astype(np.float32)
+    pt, pe, pw = [0, 1, 1], [2, 2, 0], [0.5, 0.25, 1.0]
+    y, h = O.moe_ffn(O.IQ2_XXS, O.IQ2_XXS, gate, up, down, rb, rbd, n_embd, n_ff, x, pt, pe, pw, lim=3.0,
+                     want_h=True, act="f16")
+    half = lambda a: np.asarray(a).astype(np.float16).astype(np.float64)
+    want = np.zeros((T, n_embd))
+    for p, (t, e, w) in enumerate(zip(pt, pe, pw)):
+        G = half(O.dequantize(O.IQ2_XXS, gate[e], n_ff * n_embd).reshape(n_ff, n_embd)) @ half(x[t])
+        U = half(O.dequantize(O.IQ2_XXS, up[e], n_ff * n_embd).reshape(n_ff, n_embd)) @ half(x[t])
+        Gc, Uc = np.minimum(G, 3.0), np.clip(U, -3.0, 3.0)
+        hh = (Gc / (1 + np.exp(-Gc)) * Uc).astype(np.float32)
+        assert np.allclose(h[p], hh, rtol=1e-6, atol=1e-9)
+        D = half(O.dequantize(O.IQ2_XXS, down[e], n_embd * n_ff).reshape(n_embd, n_ff)) @ half(h[p])
+        want[t] += np.float64(np.float32(w)) * D
+    assert np.allclose(y, want, rtol=1e-10, atol=1e-12)
