@@ -461,7 +461,7 @@ static void *gemv_worker(void *p) {
 
 static void quant_dequant_row(const float *x, int K, float *xh, int mode) {
     if (mode == OR_ACT_F32) { memcpy(xh, x, sizeof(float) * (size_t)K); return; }
-    if (mode == OR_ACT_F16) {
+    if (mode == OR_ACT_F16 || mode == OR_ACT_F16X) {
         for (int k = 0; k < K; k++) xh[k] = or_f16_to_f32(or_f32_to_f16(x[k]));
         return;
     }
@@ -474,7 +474,7 @@ static void quant_dequant_row(const float *x, int K, float *xh, int mode) {
 int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
             int B, int quant_x, double *y, int nthreads) {
     int be, bb;
-    if (or_block(ty, &be, &bb) != 0 || K % be != 0 || K % 32 != 0 || B < 1 || quant_x < 0 || quant_x > 2) return -1;
+    if (or_block(ty, &be, &bb) != 0 || K % be != 0 || K % 32 != 0 || B < 1 || quant_x < 0 || quant_x > 3) return -1;
     float *xh = (float *)malloc(sizeof(float) * (size_t)K * B);
     for (int b = 0; b < B; b++) quant_dequant_row(x + (int64_t)b * x_stride, K, xh + (int64_t)b * K, quant_x);
     if (nthreads < 1) nthreads = 1;

@@ -44,10 +44,13 @@ int or_random_blocks(int ty, int64_t n_elems, uint64_t *state, uint8_t *out);
  *   OR_ACT_F16  (2): xhat = f16(x), what = f16(deq(W))            (the reference's multi-token GEMM,
  *                    crates/cuda/kernels/gemm.cu:57-78: weights dequantized then rounded to half,
  *                    activations converted to half, f32 accumulation)
+ *   OR_ACT_F16X (3): xhat = f16(x), what = deq(W)                 (half activations, exact weights:
+ *                    what this build's grouped MFMA GEMM computes)
  * nthreads > 1 splits rows over pthreads. */
 #define OR_ACT_F32 0
 #define OR_ACT_Q8_1 1
 #define OR_ACT_F16 2
+#define OR_ACT_F16X 3
 int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
             int B, int quant_x, double *y, int nthreads);
 

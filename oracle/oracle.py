@@ -111,7 +111,7 @@ class Rng:
         return out
 
 
-ACT = {"f32": 0, "q8_1": 1, "f16": 2}
+ACT = {"f32": 0, "q8_1": 1, "f16": 2, "f16x": 3}
 
 
 def gemv(ty, W, row_stride, K, rows, x, B=1, x_stride=None, quant_x=True, nthreads=1, act=None):
@@ -131,8 +131,9 @@ def gemv(ty, W, row_stride, K, rows, x, B=1, x_stride=None, quant_x=True, nthrea
 def moe_ffn(ty_gu, ty_down, gate, up, down, gu_row_stride, down_row_stride, n_embd, n_ff, x, pair_tok, pair_exp,
             pair_w, lim=0.0, nthreads=1, want_h=False, act="q8_1"):
     """Routed-expert FFN oracle. gate/up/down: lists of uint8 arrays indexed by expert id.
-    act: "q8_1" (fused decode path: q8_1 activations) or "f16" (multi-token GEMM path, gemm.cu:
-    half activations and half-rounded dequantized weights)."""
+    act: "q8_1" (fused decode path: q8_1 activations), "f16" (multi-token GEMM path, gemm.cu:
+    half activations and half-rounded dequantized weights) or "f16x" (half activations, exact
+    dequantized weights)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     T = x.shape[0]
     n_exp = len(gate)

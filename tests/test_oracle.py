@@ -287,6 +287,10 @@ def test_gemv_f16_mode_matches_numpy_half_casts(ty):
     fin = np.isfinite(want)
     assert np.array_equal(np.isfinite(y), fin)
     assert np.allclose(y[fin], want[fin], rtol=1e-12, atol=1e-9)
+    # f16x: half activations, exact weights
+    yx = O.gemv(ty, W, O.row_bytes(ty, K), K, rows, x, B=B, act="f16x")
+    wantx = xh @ O.dequantize(ty, W, rows * K).reshape(rows, K).astype(np.float64).T
+    assert np.allclose(yx[fin], wantx[fin], rtol=1e-12, atol=1e-9)
 
 
 def test_moe_ffn_f16_mode_bruteforce():
