@@ -264,7 +264,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "iq2_xxs x q8_1 (int8 dot4, f32 accumulate)",
+        "dtype": "int8",
+        "dtype_detail": "IQ2_XXS weights x q8_1 activations: int8 dot4 products, f32 accumulation",
         "data": "synthetic (seeded random IQ2_XXS blocks, d~|N(0,0.02)|; x~N(0,1))",
         "config": {"workload": "config 2: routed-expert FFN, 1 decode token, 8 of 288 resident IQ2_XXS experts "
                                "(hidden 4096, intermediate 1536), gate/up+SwiGLU then down+weighted combine",
@@ -272,7 +273,9 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "gs_moe_gateup (gs_k_stream_16_1_1)",
                      "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(GATEUP_KERNEL),
+                     "traffic_source": "profiles/stream_kernels_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                       "calibrated on a 1 GiB device copy)",
                      "algorithmic_bytes_per_launch": res["gateup_bytes"],
                      "avg_launch_us": round(res["ms_gateup"] * 1e3, 3)},
         "cpu_baseline": cpu,
