@@ -342,6 +342,19 @@ struct FQ6_K : UnitGeom<256, 210>, NoTable {
 __shared__ uint2 gs_iq2xxs_grid_lds[256];
 __shared__ uint2 gs_iq2xxs_sel_lds[128];
 
+// v_perm_b32 selectors for sign index i (two words, elements 0-3 and 4-7): byte e selects q
+// (selector e) or -q (selector e + 4) from the pair {-q, q} by bit e of ksigns(i).
+__device__ __forceinline__ uint2 sign_sel(int i) {
+    const uint32_t k = ksigns((uint32_t)i);
+    uint32_t lo = 0x03020100u, hi = 0x03020100u;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        lo += ((k >> b) & 1u) << (8 * b + 2);
+        hi += ((k >> (b + 4)) & 1u) << (8 * b + 2);
+    }
+    return make_uint2(lo, hi);
+}
+
 // byte L of a, times 8: one SDWA shift (byte select on the source operand) instead of a
 // shift-and-mask pair; it is the byte offset of a 256-entry table of 8-byte rows.
 template <int L>
@@ -364,16 +377,7 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
     __device__ static __forceinline__ void tab_load(int tid, TabReg &r) { r.g = tid < 256 ? iq2xxs_grid[tid] : 0; }
     __device__ static __forceinline__ void tab_store(int tid, const TabReg &r) {
         if (tid < 256) gs_iq2xxs_grid_lds[tid] = make_uint2((uint32_t)r.g, (uint32_t)(r.g >> 32));
-        if (tid < 128) {
-            const uint32_t k = ksigns((uint32_t)tid);
-            uint32_t lo = 0x03020100u, hi = 0x03020100u;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                lo += ((k >> b) & 1u) << (8 * b + 2);
-                hi += ((k >> (b + 4)) & 1u) << (8 * b + 2);
-            }
-            gs_iq2xxs_sel_lds[tid] = make_uint2(lo, hi);
-        }
+        if (tid < 128) gs_iq2xxs_sel_lds[tid] = sign_sel(tid);
     }
     __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
         w.d = ldg2(b);
@@ -395,6 +399,77 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
             s[l] = gs_iq2xxs_sel_lds[(w.a.y >> (7 * l)) & 127];
         }
         if (!XNEG) {   // signed grid: every grid byte is nonzero, so 0x01010100 - g negates bytewise
+#pragma unroll
+            for (int l = 0; l < 4; l++) {
+                g[l].x = __builtin_amdgcn_perm(0x01010100u - g[l].x, g[l].x, s[l].x);
+                g[l].y = __builtin_amdgcn_perm(0x01010100u - g[l].y, g[l].y, s[l].y);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < NV; t++) {
+            if (NV == 1 || t < nv) {
+                int acc = 0;
+#pragma unroll
+                for (int l = 0; l < 4; l++) {
+                    const uint32_t q0 = XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l], x[t].q[2 * l], s[l].x) : x[t].q[2 * l];
+                    const uint32_t q1 =
+                        XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l + 1], x[t].q[2 * l + 1], s[l].y) : x[t].q[2 * l + 1];
+                    acc = __builtin_amdgcn_sdot4((int)g[l].x, (int)q0, acc, false);
+                    acc = __builtin_amdgcn_sdot4((int)g[l].y, (int)q1, acc, false);
+                }
+                r[t] += (db * x[t].D) * (float)acc;
+            }
+        }
+    }
+};
+
+// IQ3_XXS: a unit is 8 grid indices (one byte each, 4 values per entry) and one 32-bit word of
+// four 7-bit sign indices plus the 4-bit scale (lib.rs:312-328). The 256-entry grid (1 KiB) sits
+// in LDS next to the IQ2_XXS sign selectors (shared: both formats use ksigns), and the signs go on
+// the activation side exactly as for IQ2_XXS.
+__shared__ uint32_t gs_iq3xxs_grid_lds[256];
+
+// byte L of a, times 4 (byte offset into a table of 4-byte rows), one SDWA shift.
+template <int L>
+__device__ __forceinline__ uint32_t grid_off4(uint32_t a) {
+    uint32_t r;
+    if (L == 0) asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(r) : "v"(a));
+    if (L == 1) asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(r) : "v"(a));
+    if (L == 2) asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(r) : "v"(a));
+    if (L == 3) asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(r) : "v"(a));
+    return r;
+}
+
+struct FIQ3_XXS : UnitGeom<256, 98> {
+    static constexpr int TYPE = GS_IQ3_XXS, QK = 256, BB = 98, TAB = 0, RAW = 4;
+    static constexpr bool NEG_X = true;
+    static constexpr float XSCALE = 0.5f;   // the format's trailing *0.5, folded into the activation scale
+    struct Raw { uint2 a; uint32_t s; uint32_t d; };
+    struct TabReg { uint32_t g; };
+    __device__ static __forceinline__ void tab_load(int tid, TabReg &r) { r.g = tid < 256 ? iq3xxs_grid[tid] : 0; }
+    __device__ static __forceinline__ void tab_store(int tid, const TabReg &r) {
+        if (tid < 256) gs_iq3xxs_grid_lds[tid] = r.g;
+        if (tid < 128) gs_iq2xxs_sel_lds[tid] = sign_sel(tid);
+    }
+    __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
+        w.d = ldg2(b);
+        w.a = ldg8(b + 2 + 8 * j);
+        w.s = ldg4(b + 66 + 4 * j);
+    }
+    template <int NV, bool XNEG = true>
+    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        // db = d * (0.5 + s) * 0.5 (lib.rs:318); the 0.5 is already in x.D
+        const float db = h2f(w.d) * (0.5f + (float)(w.s >> 28));
+        const uint8_t *gt = (const uint8_t *)gs_iq3xxs_grid_lds;
+        uint2 g[4], s[4];
+        g[0] = make_uint2(*(const uint32_t *)(gt + grid_off4<0>(w.a.x)), *(const uint32_t *)(gt + grid_off4<1>(w.a.x)));
+        g[1] = make_uint2(*(const uint32_t *)(gt + grid_off4<2>(w.a.x)), *(const uint32_t *)(gt + grid_off4<3>(w.a.x)));
+        g[2] = make_uint2(*(const uint32_t *)(gt + grid_off4<0>(w.a.y)), *(const uint32_t *)(gt + grid_off4<1>(w.a.y)));
+        g[3] = make_uint2(*(const uint32_t *)(gt + grid_off4<2>(w.a.y)), *(const uint32_t *)(gt + grid_off4<3>(w.a.y)));
+#pragma unroll
+        for (int l = 0; l < 4; l++) s[l] = gs_iq2xxs_sel_lds[(w.s >> (7 * l)) & 127];
+        if (!XNEG) {   // every grid byte is nonzero, so 0x01010100 - g negates bytewise
 #pragma unroll
             for (int l = 0; l < 4; l++) {
                 g[l].x = __builtin_amdgcn_perm(0x01010100u - g[l].x, g[l].x, s[l].x);
@@ -455,5 +530,4 @@ using FQ2_K = FGeneric<GS_Q2_K, 256, 84, deq8_q2_k>;
 using FQ3_K = FGeneric<GS_Q3_K, 256, 110, deq8_q3_k>;
 using FQ5_K = FGeneric<GS_Q5_K, 256, 176, deq8_q5_k>;
 using FIQ2_S = FGeneric<GS_IQ2_S, 256, 82, deq8_iq2_s>;
-using FIQ3_XXS = FGeneric<GS_IQ3_XXS, 256, 98, deq8_iq3_xxs>;
 using FIQ4_XS = FGeneric<GS_IQ4_XS, 256, 136, deq8_iq4_xs>;
