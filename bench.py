@@ -54,6 +54,8 @@ def bench_lib():
                                 C.c_int, P, C.POINTER(C.c_float), C.POINTER(C.c_float)]
     L.bn_gemv.argtypes = [C.c_int, P, C.c_int, I64, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P,
                           C.POINTER(C.c_float)]
+    L.bn_moe_ffn.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, I64, C.c_int, C.c_int, I64, P, P, P, C.c_int,
+                             C.c_int, P, C.POINTER(C.c_float)]
     L.bn_copy.argtypes = [P, P, C.c_size_t, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_moe_grouped.argtypes = [C.c_int, P, C.c_int, C.c_int, P, P, P, P, C.c_int, I64, C.c_int, C.c_int, I64, P, P,
                                  P, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
@@ -99,11 +101,14 @@ def run_moe_decode(L, s, steps, warmup, n_expert=288, n_embd=4096, n_ff=1536, se
     rc = L.bn_moe_decode(ty, ty, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p, steps,
                          warmup, s.raw(), C.byref(ms), C.byref(msg))
     G.check(rc)
+    msf = C.c_float()
+    G.check(L.bn_moe_ffn(ty, ty, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p, steps,
+                         warmup, s.raw(), C.byref(msf)))
     step_bytes = 8 * 3 * mat
     gu_bytes = 8 * 2 * mat
     keep = (gate, up, down, dx, dh, dy, batches)
     layer = dict(gate=gate, up=up, down=down, mat=mat, n_expert=n_expert, n_embd=n_embd, n_ff=n_ff, rbg=rbg, rbd=rbd)
-    return dict(ms_step=ms.value, ms_gateup=msg.value, step_bytes=step_bytes, gateup_bytes=gu_bytes,
+    return dict(ms_step=ms.value, ms_gateup=msg.value, ms_ffn=msf.value, step_bytes=step_bytes, gateup_bytes=gu_bytes,
                 flops=8 * 3 * 2 * n_ff * n_embd), keep, layer
 
 

@@ -62,6 +62,25 @@ BN_EXPORT int bn_moe_decode(int ty_gu, int ty_dn, const GsMoeBatch *batches, int
     return 0;
 }
 
+// Decode step through gs_moe_ffn (the fused gate/up + down launch) over batch (i % nb); mean ms.
+BN_EXPORT int bn_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *batches, int nb, int nt, int64_t rs_gu, int n_embd,
+                         int n_ff, int64_t rs_dn, const float *x, float *h, float *y, int steps, int warmup, void *s,
+                         float *ms_step) {
+    Timer t;
+    CK(t.init());
+    for (int i = 0; i < warmup; i++)
+        CK(gs_moe_ffn(ty_gu, ty_dn, &batches[i % nb], nt, rs_gu, n_embd, n_ff, rs_dn, x, h, y, 0.0f, s));
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    for (int i = 0; i < steps; i++)
+        CK(gs_moe_ffn(ty_gu, ty_dn, &batches[(warmup + i) % nb], nt, rs_gu, n_embd, n_ff, rs_dn, x, h, y, 0.0f, s));
+    CK(gs_event_record(t.b, s));
+    CK(gs_event_sync(t.b));
+    CK(gs_event_elapsed_ms(ms_step, t.a, t.b));
+    *ms_step /= steps;
+    return 0;
+}
+
 // GEMV over rotating weight copies Ws[i % nw] (defeats the last-level cache); mean ms per call.
 BN_EXPORT int bn_gemv(int ty, const void *const *Ws, int nw, int64_t rs, int K, int rows, const float *x, float *y,
                       int B, int steps, int warmup, void *s, float *ms) {

@@ -367,6 +367,38 @@ __device__ __forceinline__ uint32_t grid_off(uint32_t a) {
     return r;
 }
 
+// r[t] += db * x[t].D * sum over 4 groups of 8: grid bytes g[l] . (signs s[l] applied) q. XNEG: the
+// activation units carry -q and the v_perm_b32 selectors pick q or -q per byte (2 operations per
+// 8 elements); otherwise the signs go on the grid bytes (every grid byte is nonzero, so
+// 0x01010100 - g negates bytewise; one more operation per 4 elements).
+template <int NV, bool XNEG>
+__device__ __forceinline__ void signed_dot8x4(const uint2 (&g_)[4], const uint2 (&s)[4], float db, const XU (&x)[NV],
+                                              int nv, float (&r)[NV]) {
+    uint2 g[4] = {g_[0], g_[1], g_[2], g_[3]};
+    if (!XNEG) {
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            g[l].x = __builtin_amdgcn_perm(0x01010100u - g[l].x, g[l].x, s[l].x);
+            g[l].y = __builtin_amdgcn_perm(0x01010100u - g[l].y, g[l].y, s[l].y);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NV; t++) {
+        if (NV == 1 || t < nv) {
+            int acc = 0;
+#pragma unroll
+            for (int l = 0; l < 4; l++) {
+                const uint32_t q0 = XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l], x[t].q[2 * l], s[l].x) : x[t].q[2 * l];
+                const uint32_t q1 =
+                    XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l + 1], x[t].q[2 * l + 1], s[l].y) : x[t].q[2 * l + 1];
+                acc = __builtin_amdgcn_sdot4((int)g[l].x, (int)q0, acc, false);
+                acc = __builtin_amdgcn_sdot4((int)g[l].y, (int)q1, acc, false);
+            }
+            r[t] += (db * x[t].D) * (float)acc;
+        }
+    }
+}
+
 struct FIQ2_XXS : UnitGeom<256, 66> {
     static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 0, RAW = 3;
     static constexpr bool NEG_X = true;
@@ -380,46 +412,39 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
         if (tid < 128) gs_iq2xxs_sel_lds[tid] = sign_sel(tid);
     }
     __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
+#ifdef GS_STREAM_NOD   // profiling build only: no scale load
+        w.d = 0x3c00u;
+#else
         w.d = ldg2(b);
+#endif
         w.a = ldg8(b + 2 + 8 * j);
     }
     // XNEG: the activation units carry -q (signs applied on the activation side, 2 ops per 8
     // elements); otherwise the signs are applied to the grid bytes (one more op per 4 elements,
     // 8 fewer registers per activation unit).
-    template <int NV, bool XNEG = true>
-    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
-                                               float (&r)[NV]) {
-        // db = d * (0.5 + s) * 0.25 (lib.rs:279); the 0.25 is already in x.D
-        const float db = h2f(w.d) * (0.5f + (float)(w.a.y >> 28));
-        uint2 g[4], s[4];
+    // Two phases so the row loop can issue the next unit's table reads before this unit's
+    // arithmetic: fetch() reads the grid rows and sign selectors from LDS, dot2() consumes them.
+    struct Dec { uint2 g[4], s[4]; };
+    __device__ static __forceinline__ void fetch(const Raw &w, Dec &e) {
         const uint32_t gofs[4] = {grid_off<0>(w.a.x), grid_off<1>(w.a.x), grid_off<2>(w.a.x), grid_off<3>(w.a.x)};
 #pragma unroll
         for (int l = 0; l < 4; l++) {
-            g[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_grid_lds + gofs[l]);
-            s[l] = gs_iq2xxs_sel_lds[(w.a.y >> (7 * l)) & 127];
+            e.g[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_grid_lds + gofs[l]);
+            e.s[l] = gs_iq2xxs_sel_lds[(w.a.y >> (7 * l)) & 127];
         }
-        if (!XNEG) {   // signed grid: every grid byte is nonzero, so 0x01010100 - g negates bytewise
-#pragma unroll
-            for (int l = 0; l < 4; l++) {
-                g[l].x = __builtin_amdgcn_perm(0x01010100u - g[l].x, g[l].x, s[l].x);
-                g[l].y = __builtin_amdgcn_perm(0x01010100u - g[l].y, g[l].y, s[l].y);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < NV; t++) {
-            if (NV == 1 || t < nv) {
-                int acc = 0;
-#pragma unroll
-                for (int l = 0; l < 4; l++) {
-                    const uint32_t q0 = XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l], x[t].q[2 * l], s[l].x) : x[t].q[2 * l];
-                    const uint32_t q1 =
-                        XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l + 1], x[t].q[2 * l + 1], s[l].y) : x[t].q[2 * l + 1];
-                    acc = __builtin_amdgcn_sdot4((int)g[l].x, (int)q0, acc, false);
-                    acc = __builtin_amdgcn_sdot4((int)g[l].y, (int)q1, acc, false);
-                }
-                r[t] += (db * x[t].D) * (float)acc;
-            }
-        }
+    }
+    template <int NV, bool XNEG = true>
+    __device__ static __forceinline__ void dot2(const Raw &w, const Dec &e, const XU (&x)[NV], int nv, float (&r)[NV]) {
+        // db = d * (0.5 + s) * 0.25 (lib.rs:279); the 0.25 is already in x.D
+        const float db = h2f(w.d) * (0.5f + (float)(w.a.y >> 28));
+        signed_dot8x4<NV, XNEG>(e.g, e.s, db, x, nv, r);
+    }
+    template <int NV, bool XNEG = true>
+    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        Dec e;
+        fetch(w, e);
+        dot2<NV, XNEG>(w, e, x, nv, r);
     }
 };
 
@@ -456,41 +481,28 @@ struct FIQ3_XXS : UnitGeom<256, 98> {
         w.a = ldg8(b + 2 + 8 * j);
         w.s = ldg4(b + 66 + 4 * j);
     }
+    struct Dec { uint2 g[4], s[4]; };
+    __device__ static __forceinline__ void fetch(const Raw &w, Dec &e) {
+        const uint8_t *gt = (const uint8_t *)gs_iq3xxs_grid_lds;
+        e.g[0] = make_uint2(*(const uint32_t *)(gt + grid_off4<0>(w.a.x)), *(const uint32_t *)(gt + grid_off4<1>(w.a.x)));
+        e.g[1] = make_uint2(*(const uint32_t *)(gt + grid_off4<2>(w.a.x)), *(const uint32_t *)(gt + grid_off4<3>(w.a.x)));
+        e.g[2] = make_uint2(*(const uint32_t *)(gt + grid_off4<0>(w.a.y)), *(const uint32_t *)(gt + grid_off4<1>(w.a.y)));
+        e.g[3] = make_uint2(*(const uint32_t *)(gt + grid_off4<2>(w.a.y)), *(const uint32_t *)(gt + grid_off4<3>(w.a.y)));
+#pragma unroll
+        for (int l = 0; l < 4; l++) e.s[l] = gs_iq2xxs_sel_lds[(w.s >> (7 * l)) & 127];
+    }
+    template <int NV, bool XNEG = true>
+    __device__ static __forceinline__ void dot2(const Raw &w, const Dec &e, const XU (&x)[NV], int nv, float (&r)[NV]) {
+        // db = d * (0.5 + s) * 0.5 (lib.rs:318); the 0.5 is already in x.D
+        const float db = h2f(w.d) * (0.5f + (float)(w.s >> 28));
+        signed_dot8x4<NV, XNEG>(e.g, e.s, db, x, nv, r);
+    }
     template <int NV, bool XNEG = true>
     __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {
-        // db = d * (0.5 + s) * 0.5 (lib.rs:318); the 0.5 is already in x.D
-        const float db = h2f(w.d) * (0.5f + (float)(w.s >> 28));
-        const uint8_t *gt = (const uint8_t *)gs_iq3xxs_grid_lds;
-        uint2 g[4], s[4];
-        g[0] = make_uint2(*(const uint32_t *)(gt + grid_off4<0>(w.a.x)), *(const uint32_t *)(gt + grid_off4<1>(w.a.x)));
-        g[1] = make_uint2(*(const uint32_t *)(gt + grid_off4<2>(w.a.x)), *(const uint32_t *)(gt + grid_off4<3>(w.a.x)));
-        g[2] = make_uint2(*(const uint32_t *)(gt + grid_off4<0>(w.a.y)), *(const uint32_t *)(gt + grid_off4<1>(w.a.y)));
-        g[3] = make_uint2(*(const uint32_t *)(gt + grid_off4<2>(w.a.y)), *(const uint32_t *)(gt + grid_off4<3>(w.a.y)));
-#pragma unroll
-        for (int l = 0; l < 4; l++) s[l] = gs_iq2xxs_sel_lds[(w.s >> (7 * l)) & 127];
-        if (!XNEG) {   // every grid byte is nonzero, so 0x01010100 - g negates bytewise
-#pragma unroll
-            for (int l = 0; l < 4; l++) {
-                g[l].x = __builtin_amdgcn_perm(0x01010100u - g[l].x, g[l].x, s[l].x);
-                g[l].y = __builtin_amdgcn_perm(0x01010100u - g[l].y, g[l].y, s[l].y);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < NV; t++) {
-            if (NV == 1 || t < nv) {
-                int acc = 0;
-#pragma unroll
-                for (int l = 0; l < 4; l++) {
-                    const uint32_t q0 = XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l], x[t].q[2 * l], s[l].x) : x[t].q[2 * l];
-                    const uint32_t q1 =
-                        XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l + 1], x[t].q[2 * l + 1], s[l].y) : x[t].q[2 * l + 1];
-                    acc = __builtin_amdgcn_sdot4((int)g[l].x, (int)q0, acc, false);
-                    acc = __builtin_amdgcn_sdot4((int)g[l].y, (int)q1, acc, false);
-                }
-                r[t] += (db * x[t].D) * (float)acc;
-            }
-        }
+        Dec e;
+        fetch(w, e);
+        dot2<NV, XNEG>(w, e, x, nv, r);
     }
 };
 

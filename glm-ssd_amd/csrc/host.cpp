@@ -160,13 +160,15 @@ int ggml_block_elems(int ty) {  // elements per ggml block (1 for plain types)
 }
 int table_bytes(int) { return 0; }  // lookup tables are static LDS arrays of their kernels
 
-// Plan and launch one streaming kernel (kind 0 GEMV, 1 MoE gate/up, 2 MoE down).
-hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 1) {
+// Plan of one streaming pass: lanes per row group and unit budget (into `a`), the kernel's
+// weight-unit budget and its dynamic LDS bytes.
+struct StreamPlan {
+    int um = 0;
+    size_t lds = 0;
+};
+hipError_t plan_stream(DeviceCtx *c, int kind, int ty, StreamArgs &a, StreamPlan &P) {
     int qk, bb;
     if (!geometry(ty, qk, bb)) return hipErrorInvalidValue;
-    hipError_t e;
-    DeviceCtx *c = ctx(&e);
-    if (!c) return e;
     const int NVt = a.nvec <= 1 ? 1 : a.nvec <= 2 ? 2 : a.nvec <= 4 ? 4 : 8;
     a.row_bytes = (int)((int64_t)a.K / qk * bb);
     a.nu = a.K / 32;
@@ -199,26 +201,38 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     a.lpr = best_lpr;
     a.upl = (tot + best_lpr - 1) / best_lpr;
     const int tab = (table_bytes(ty) + 15) & ~15;
-    const size_t lds = (size_t)tab + (size_t)(kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
-    if (lds > std::min<size_t>(c->max_lds, 160 * 1024)) return hipErrorInvalidValue;
+    P.lds = (size_t)tab + (size_t)(kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
+    if (P.lds > std::min<size_t>(c->max_lds, 160 * 1024)) return hipErrorInvalidValue;
+    P.um = best_um;
+    return hipSuccess;
+}
+
+// workgroups of `f` that fit one CU with `lds` bytes of dynamic LDS (cached)
+int blocks_per_cu(DeviceCtx *c, const std::string &name, hipFunction_t f, size_t lds) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto key = std::make_pair(name, (int)lds);
+    auto it = c->occ.find(key);
+    if (it != c->occ.end()) return it->second;
+    int nb = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, GS_WG, lds) != hipSuccess || nb < 1) nb = 0;
+    (void)hipGetLastError();
+    c->occ[key] = nb;
+    return nb;
+}
+
+// Plan and launch one streaming kernel (kind 0 GEMV, 1 MoE gate/up, 2 MoE down).
+hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 1) {
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    StreamPlan P;
+    if ((e = plan_stream(c, kind, ty, a, P)) != hipSuccess) return e;
+    const int NVt = a.nvec <= 1 ? 1 : a.nvec <= 2 ? 2 : a.nvec <= 4 ? 4 : 8;
     const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" +
-                             std::to_string(NVt) + "_" + std::to_string(best_um);
+                             std::to_string(NVt) + "_" + std::to_string(P.um);
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
-    int per_cu = 1;
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        auto key = std::make_pair(name, (int)lds);
-        auto it = c->occ.find(key);
-        if (it != c->occ.end()) {
-            per_cu = it->second;
-        } else {
-            int nb = 0;
-            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, GS_WG, lds) != hipSuccess || nb < 1) nb = 1;
-            c->occ[key] = nb;
-            per_cu = nb;
-        }
-    }
+    const int per_cu = std::max(1, blocks_per_cu(c, name, f, P.lds));
     const int G = GS_WG / a.lpr;
     const int nrow = kind == 1 ? a.nseg * a.rows : a.rows;
     // one workgroup per CU by default: each workgroup pays the activation prologue once, and the
@@ -230,7 +244,7 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
         const int waves = std::max(grid * wpw, a.nseg) / a.nseg * a.nseg;
         grid = (waves + wpw - 1) / wpw;
     }
-    return launch(name, dim3(grid, n_batch, 1), dim3(GS_WG, 1, 1), lds, s, a);
+    return launch(name, dim3(grid, n_batch, 1), dim3(GS_WG, 1, 1), P.lds, s, a);
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -405,11 +419,8 @@ static int moe_check(int ty, const GsMoeBatch *b, int nt, int K, int rows, int64
     return 0;
 }
 
-GS_EXPORT int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *x,
-                            float *h, float lim, void *s) {
-    int rc = moe_check(ty, b, nt, K, rows, row_stride);
-    if (rc) return rc;
-    StreamArgs a;
+static int gateup_args(StreamArgs &a, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows,
+                       const float *x, float *h, float lim) {
     memset(&a, 0, sizeof(a));
     for (int e = 0; e < b->n; e++) {
         if (((uintptr_t)b->gate[e] | (uintptr_t)b->up[e]) & 1) return hipErrorInvalidValue;
@@ -426,6 +437,42 @@ GS_EXPORT int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_str
     a.nseg = b->n;
     a.lim = lim;
     a.x_aligned = aligned16(x) && K % 4 == 0;
+    return 0;
+}
+
+// experts e0 .. e0+n-1 of the batch
+static int down_args(StreamArgs &a, const GsMoeBatch *b, int e0, int n, int nt, int64_t row_stride, int K, int rows,
+                     const float *h, float *y) {
+    memset(&a, 0, sizeof(a));
+    for (int e = 0; e < n; e++) {
+        if ((uintptr_t)b->down[e0 + e] & 1) return hipErrorInvalidValue;
+        a.w0[e] = b->down[e0 + e];
+        for (int t = 0; t < nt; t++) a.wt[t][e] = b->w[t][e0 + e];
+    }
+    a.x = h + (int64_t)e0 * nt * K;
+    a.y = y;
+    a.row_stride = row_stride;
+    a.y_stride = rows;
+    a.K = K;
+    a.rows = rows;
+    a.nvec = nt;
+    a.nseg = n;
+    a.x_aligned = aligned16(a.x) && K % 4 == 0;
+    return 0;
+}
+
+// experts one down launch covers: as many as fit one lane's register budget (64 lanes x 8/NV units)
+static int down_per_launch(int nt, int K) {
+    const int NVt = nt <= 1 ? 1 : 2;
+    return std::max(1, 64 * (8 / NVt) / (K / 32));
+}
+
+GS_EXPORT int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *x,
+                            float *h, float lim, void *s) {
+    int rc = moe_check(ty, b, nt, K, rows, row_stride);
+    if (rc) return rc;
+    StreamArgs a;
+    if ((rc = gateup_args(a, b, nt, row_stride, K, rows, x, h, lim))) return rc;
     return stream(1, ty, a, (hipStream_t)s);
 }
 
@@ -433,31 +480,56 @@ GS_EXPORT int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_strid
                           float *y, void *s) {
     int rc = moe_check(ty, b, nt, K, rows, row_stride);
     if (rc) return rc;
-    // one launch covers as many experts as fit one lane's register budget (64 lanes x 8/NV units)
-    const int NVt = nt <= 1 ? 1 : 2;
-    const int per = std::max(1, 64 * (8 / NVt) / (K / 32));
+    const int per = down_per_launch(nt, K);
     for (int e0 = 0; e0 < b->n; e0 += per) {
         const int n = std::min(per, b->n - e0);
         StreamArgs a;
-        memset(&a, 0, sizeof(a));
-        for (int e = 0; e < n; e++) {
-            if ((uintptr_t)b->down[e0 + e] & 1) return hipErrorInvalidValue;
-            a.w0[e] = b->down[e0 + e];
-            for (int t = 0; t < nt; t++) a.wt[t][e] = b->w[t][e0 + e];
-        }
-        a.x = h + (int64_t)e0 * nt * K;
-        a.y = y;
-        a.row_stride = row_stride;
-        a.y_stride = rows;
-        a.K = K;
-        a.rows = rows;
-        a.nvec = nt;
-        a.nseg = n;
-        a.x_aligned = aligned16(a.x) && K % 4 == 0;
+        if ((rc = down_args(a, b, e0, n, nt, row_stride, K, rows, h, y))) return rc;
         hipError_t e = stream(2, ty, a, (hipStream_t)s);
         if (e != hipSuccess) return e;
     }
     return 0;
+}
+
+// fused FFN kernels exist for these (gate/up, down) format pairs (kernels.hip GS_FFN_ALL)
+static bool ffn_pair(int ty_gu, int ty_dn) {
+    if (ty_gu == GS_IQ2_XXS && ty_dn == GS_IQ3_XXS) return true;
+    return ty_gu == ty_dn && (ty_gu == GS_Q8_0 || ty_gu == GS_Q4_K || ty_gu == GS_Q6_K || ty_gu == GS_IQ2_XXS ||
+                              ty_gu == GS_IQ3_XXS);
+}
+
+// Routed-expert FFN of one layer: exactly gs_moe_gateup followed by gs_moe_down (h is written
+// too). For one token whose down pass fits one launch this is a single fused launch (gate/up,
+// grid barrier, down); otherwise, or with GLMSSD_NO_FFN_FUSION set, the two launches.
+GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int64_t rs_gu, int n_embd, int n_ff,
+                         int64_t rs_dn, const float *x, float *h, float *y, float lim, void *s) {
+    int rc = moe_check(ty_gu, b, nt, n_embd, n_ff, rs_gu);
+    if (rc) return rc;
+    if ((rc = moe_check(ty_dn, b, nt, n_ff, n_embd, rs_dn))) return rc;
+    static const bool no_fusion = getenv("GLMSSD_NO_FFN_FUSION") != nullptr;
+    bool fuse = !no_fusion && nt == 1 && ffn_pair(ty_gu, ty_dn) && b->n <= down_per_launch(nt, n_ff);
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    FfnArgs fa;
+    StreamPlan P1, P2;
+    if (fuse) {
+        if ((rc = gateup_args(fa.gu, b, nt, rs_gu, n_embd, n_ff, x, h, lim))) return rc;
+        if ((rc = down_args(fa.dn, b, 0, b->n, nt, rs_dn, n_ff, n_embd, h, y))) return rc;
+        fuse = plan_stream(c, 1, ty_gu, fa.gu, P1) == hipSuccess && plan_stream(c, 2, ty_dn, fa.dn, P2) == hipSuccess;
+    }
+    if (fuse) {
+        const std::string name = "gs_k_ffn_" + std::to_string(ty_gu) + "_" + std::to_string(ty_dn) + "_" +
+                                 std::to_string(P1.um) + "_" + std::to_string(P2.um);
+        const size_t lds = std::max(P1.lds, P2.lds);
+        hipFunction_t f;
+        if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
+        // the barrier needs every workgroup resident at once: one per CU, within the occupancy limit
+        const int per_cu = blocks_per_cu(c, name, f, lds);
+        if (per_cu >= 1) return launch(name, dim3(c->cu_count, 1, 1), dim3(GS_WG, 1, 1), lds, (hipStream_t)s, fa);
+    }
+    if ((rc = gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, lim, s))) return rc;
+    return gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y, s);
 }
 
 // =============================================================================================

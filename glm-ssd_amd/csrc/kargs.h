@@ -44,6 +44,12 @@ struct StreamArgs {
     int x_aligned;                   // x and x_stride allow 16-byte loads
 };
 
+// Fused MoE FFN (gate/up + SwiGLU, grid barrier, down + combine) for one token
+struct FfnArgs {
+    StreamArgs gu;   // kind 1: gate/up -> h
+    StreamArgs dn;   // kind 2: h -> y (accumulated)
+};
+
 // Whole-tensor dequantization
 struct DequantArgs {
     const uint8_t *src;

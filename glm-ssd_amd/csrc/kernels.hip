@@ -55,6 +55,24 @@ __device__ __forceinline__ void load32(const float *src_, bool aligned, float (&
     }
 }
 
+__device__ __forceinline__ void load8(const float *src_, bool aligned, float (&v)[8]) {
+    const GS_GLOBAL float *src = (const GS_GLOBAL float *)src_;
+    if (aligned) {
+        const GS_GLOBAL float4 *p = (const GS_GLOBAL float4 *)src;
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = src[i];
+    }
+}
+
+// value of another lane of the same quad (DPP quad_perm CTRL)
+template <int CTRL>
+__device__ __forceinline__ float quad_swap(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
 // =============================================================================================
 // Cross-lane sum over groups of 16/32/64 lanes with DPP; the group's last lane ends with the total.
 // =============================================================================================
@@ -122,11 +140,12 @@ __device__ __forceinline__ XU load_xu(const uint8_t *xq, const uint32_t *xm, int
     z.shi = live ? (int)(int16_t)(ss >> 16) : 0;
     if (XNEG) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {   // bytewise -q (|q| <= 127, no overflow)
-            uint32_t n = 0;
-#pragma unroll
-            for (int b = 0; b < 4; b++) n |= ((uint32_t)(-(int)(int8_t)(z.q[i] >> (8 * b))) & 0xffu) << (8 * b);
-            z.nq[i] = n;
+        for (int i = 0; i < 8; i++) {
+            // bytewise -q in four operations: per byte, 0x80 - (q & 0x7f) is ~q's low seven bits
+            // plus one (no borrow leaves the byte), and the sign bit is then flipped unless q's
+            // was set. |q| <= 127, so -q never overflows.
+            const uint32_t q = z.q[i];
+            z.nq[i] = (0x80808080u - (q & 0x7f7f7f7fu)) ^ (q & 0x80808080u) ^ 0x80808080u;
         }
     }
     return z;
@@ -151,107 +170,165 @@ __device__ unsigned long long gs_stream_ts[1 << 16];
 #define GS_TS(i, extra)
 #endif
 
+// Unit decode in two phases where the format has them (LDS table reads, then arithmetic), so
+// the row loop can issue unit i+1's reads before unit i's arithmetic; one phase otherwise.
+template <class F, class = void>
+struct TwoPhase {
+    struct Dec {};
+    __device__ static __forceinline__ void fetch(const typename F::Raw &, Dec &) {}
+    template <int NV, bool XNEG>
+    __device__ static __forceinline__ void dot(const typename F::Raw &w, const Dec &, int j, const uint8_t *tab,
+                                               const XU (&x)[NV], int nv, float (&r)[NV]) {
+        F::template dot<NV, XNEG>(w, j, tab, x, nv, r);
+    }
+};
+template <class F>
+struct TwoPhase<F, decltype((void)sizeof(typename F::Dec), void())> {
+    using Dec = typename F::Dec;
+    __device__ static __forceinline__ void fetch(const typename F::Raw &w, Dec &e) { F::fetch(w, e); }
+    template <int NV, bool XNEG>
+    __device__ static __forceinline__ void dot(const typename F::Raw &w, const Dec &e, int, const uint8_t *,
+                                               const XU (&x)[NV], int nv, float (&r)[NV]) {
+        F::template dot2<NV, XNEG>(w, e, x, nv, r);
+    }
+};
+
+// h (gate/up output) stores at device scope: written through to memory on completion, so the
+// fused FFN's down pass on another XCD reads them after its barrier without any cache flush.
+__device__ __forceinline__ void store_h(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Exact u / d for 0 <= u < 2^21 through the rounded reciprocal rd = 1/d (two VALU operations
+// instead of a ~20-instruction integer division): (u + 0.5) / d lies at least 0.5/d from an
+// integer, and the two roundings move it by at most 3 * 2^-24 * (u + 0.5) / d, less than that.
+__device__ __forceinline__ int udiv_small(int u, float rd) { return (int)(((float)u + 0.5f) * rd); }
+
 template <class F, int KIND, int NV, int UMAX>
-__device__ __forceinline__ void stream_body(const StreamArgs &a) {
-    constexpr int PF = pf_depth<F, UMAX>();
-    constexpr int UX = KIND == 1 ? UMAX / 2 : UMAX;       // activation units per lane
-    constexpr bool XNEG = NegX<F>::value && UX * NV <= 4;  // -q in registers only while it is cheap
+struct StreamPass {
+    static constexpr int PF = pf_depth<F, UMAX>();
+    static constexpr int UX = KIND == 1 ? UMAX / 2 : UMAX;       // activation units per lane
+    static constexpr bool XNEG = NegX<F>::value && UX * NV <= 4;  // -q in registers only while it is cheap
+    // activation prologue: 4 threads per 32-element unit (8 floats each), XP passes of GS_WG/4
+    // units in flight before the weight loads (a decode-sized x is one pass: 2 loads per thread)
+    static constexpr int XT = 4, XPU = GS_WG / XT;
+    static constexpr int XP = KIND == 2 ? 4 : (NV < 4 ? NV : 4);
     static_assert(KIND != 1 || UMAX % 2 == 0, "gate/up needs an even unit count");
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x;
-    GS_TS(0, 0)
-    uint8_t *tab = smem;
-    uint8_t *xq = smem + ((F::TAB + 15) & ~15);
 
-    const uint8_t *wb = a.w0[0];
-    const float *x = a.x;
-    float *y = a.y;
-    if (KIND == 0) {
-        wb += (int64_t)blockIdx.y * a.w_bs;
-        x += (int64_t)blockIdx.y * a.x_bs;
-        y += (int64_t)blockIdx.y * a.y_bs;
-    }
-    const int K = a.K, nu = a.nu, nv = a.nvec, rows = a.rows;
-    const int lpr = a.lpr, lane = tid & (lpr - 1);
-    const int tot = KIND == 2 ? a.nseg * nu : nu;          // units along the (concatenated) row
-    // Lane groups: GATEUP pins each wave to one expert (its pointers are wave-uniform) and the
-    // wave's groups stride over that expert's rows; other kinds stride over all rows.
-    const int gpw = 64 / lpr;                                   // groups per wave
-    const int wave_all = blockIdx.x * (GS_WG / 64) + (tid >> 6);
-    const int nwaves_all = gridDim.x * (GS_WG / 64);
-    const int gin = (tid & 63) / lpr;                           // group within the wave
-    int ge = 0, ngroups, gid, nrow;
-    if (KIND == 1) {
-        ge = __builtin_amdgcn_readfirstlane(wave_all % a.nseg);
-        const int wpe = nwaves_all / a.nseg;                    // waves per expert
-        ngroups = wpe * gpw;
-        gid = (wave_all / a.nseg) * gpw + gin;
-        nrow = wave_all >= wpe * a.nseg ? 0 : rows;             // leftover waves idle
-    } else {
-        ngroups = nwaves_all * gpw;
-        gid = wave_all * gpw + gin;
-        nrow = rows;
-    }
-    const int64_t rs = a.row_stride;
-    // expert pointer tables: one vector load (lane i <- entry i), then readlane / bpermute, so no
-    // weight address waits on a second, dependent kernel-argument fetch
-    const int L64 = tid & 63;
-    const uint64_t tw0 = KIND != 0 && L64 < GS_SEG_MAX ? (uint64_t)a.w0[L64] : 0;
-    const uint64_t tw1 = KIND == 1 && L64 < GS_SEG_MAX ? (uint64_t)a.w1[L64] : 0;
-    auto lane_u64 = [](uint64_t v, int src) -> uint64_t {   // v of lane `src` (per-lane src)
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)(v >> 32));
-        return (uint64_t)lo | ((uint64_t)hi << 32);
-    };
-    const uint8_t *wg = nullptr, *wu = nullptr;
-    if (KIND == 1) {
-        wg = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw0 >> 32), ge) << 32) |
-                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw0, ge));
-        wu = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw1 >> 32), ge) << 32) |
-                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw1, ge));
-    }
-
-    // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
+    const StreamArgs &a;
+    int tid;
+    uint8_t *tab, *xq;
+    const float *x;
+    float *y;
+    int K, nu, nv, rows, lpr, lane, tot, ngroups, gid, nrow, ge, nxv, nxu;
+    float rnu;   // 1/nu
+    int64_t rs;
+    const uint8_t *wg, *wu;
     int uspan[UX], usub[UX];
     uint32_t uoff[UX];
     bool uval[UX];
-#pragma unroll
-    for (int j = 0; j < UX; j++) {
-        const int u0 = lane + lpr * j;
-        const bool valid = j < a.upl && u0 < tot;
-        const int u = valid ? u0 : (lane < tot ? lane : 0);
-        const int s = KIND == 2 ? u / nu : 0;
-        const int up = u - s * nu;
-        uval[j] = valid;
-        uspan[j] = s;
-        uoff[j] = F::off(up);
-        usub[j] = F::sub(up);
-    }
     const uint8_t *ubase[UX];
-#pragma unroll
-    for (int j = 0; j < UX; j++)
-        ubase[j] = (KIND == 2 ? (const uint8_t *)lane_u64(tw0, uspan[j]) : (KIND == 1 ? nullptr : wb)) + uoff[j];
-
-    // ---- prologue loads first: activation units and lookup tables are requested before the
-    // weight loads, so waiting for them (vmcnt counts in issue order) never waits on weights
-    constexpr int XQ = 2;                                       // activation units per thread in flight
-    const int nxv = KIND == 2 ? a.nseg * nv : nv;
-    const int nxu = nxv * nu;
-    float xf[XQ][32];
-#pragma unroll
-    for (int k = 0; k < XQ; k++) {
-        const int i = min(tid + GS_WG * k, nxu - 1);            // clamped: the loads are unconditional
-        const int v = i / nu, u = i - v * nu;
-        const float *src = (KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u;
-        load32(src, a.x_aligned != 0, xf[k]);
-    }
+    float xf[XP][8];
     typename F::TabReg treg;
-    F::tab_load(tid, treg);
-
-    // ---- weight batches ------------------------------------------------------------------------
     typename F::Raw R[PF][UMAX];
-    const int last = nrow > 0 ? nrow - 1 : 0;
-    auto load_batch = [&](int base) {
+
+    // geometry of this pass; issues no memory access except the pointer-table load (DOWN/GATEUP)
+    __device__ __forceinline__ StreamPass(const StreamArgs &a_, uint8_t *smem) : a(a_) {
+        tid = threadIdx.x;
+        tab = smem;
+        xq = smem + ((F::TAB + 15) & ~15);
+        const uint8_t *wb = a.w0[0];
+        x = a.x;
+        y = a.y;
+        if (KIND == 0) {
+            wb += (int64_t)blockIdx.y * a.w_bs;
+            x += (int64_t)blockIdx.y * a.x_bs;
+            y += (int64_t)blockIdx.y * a.y_bs;
+        }
+        K = a.K, nu = a.nu, nv = a.nvec, rows = a.rows;
+        lpr = a.lpr, lane = tid & (lpr - 1);
+        tot = KIND == 2 ? a.nseg * nu : nu;          // units along the (concatenated) row
+        // Lane groups: GATEUP pins each wave to one expert (its pointers are wave-uniform) and the
+        // wave's groups stride over that expert's rows; other kinds stride over all rows.
+        const int lsh = __builtin_ctz(lpr);                         // lpr is a power of two
+        const int gpw = 64 >> lsh;                                  // groups per wave
+        // wave-uniform (SGPR) wave index: the expert/row split below stays on the scalar unit
+        const int wave_all = blockIdx.x * (GS_WG / 64) + __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int nwaves_all = gridDim.x * (GS_WG / 64);
+        const int gin = (tid & 63) >> lsh;                          // group within the wave
+        rnu = 1.0f / (float)nu;
+        ge = 0;
+        if (KIND == 1) {
+            ge = __builtin_amdgcn_readfirstlane(wave_all % a.nseg);
+            const int wpe = nwaves_all / a.nseg;                    // waves per expert
+            ngroups = wpe * gpw;
+            gid = (wave_all / a.nseg) * gpw + gin;
+            nrow = wave_all >= wpe * a.nseg ? 0 : rows;             // leftover waves idle
+        } else {
+            ngroups = nwaves_all * gpw;
+            gid = wave_all * gpw + gin;
+            nrow = rows;
+        }
+        rs = a.row_stride;
+        // expert pointer tables: one vector load (lane i <- entry i), then readlane / bpermute, so no
+        // weight address waits on a second, dependent kernel-argument fetch
+        const int L64 = tid & 63;
+        const uint64_t tw0 = KIND != 0 && L64 < GS_SEG_MAX ? (uint64_t)a.w0[L64] : 0;
+        const uint64_t tw1 = KIND == 1 && L64 < GS_SEG_MAX ? (uint64_t)a.w1[L64] : 0;
+        auto lane_u64 = [](uint64_t v, int src) -> uint64_t {   // v of lane `src` (per-lane src)
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)(v >> 32));
+            return (uint64_t)lo | ((uint64_t)hi << 32);
+        };
+        wg = wu = nullptr;
+        if (KIND == 1) {
+            wg = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw0 >> 32), ge) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw0, ge));
+            wu = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw1 >> 32), ge) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw1, ge));
+        }
+        // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
+#pragma unroll
+        for (int j = 0; j < UX; j++) {
+            const int u0 = lane + lpr * j;
+            const bool valid = j < a.upl && u0 < tot;
+            const int u = valid ? u0 : (lane < tot ? lane : 0);
+            const int s = KIND == 2 ? udiv_small(u, rnu) : 0;
+            const int up = u - s * nu;
+            uval[j] = valid;
+            uspan[j] = s;
+            uoff[j] = F::off(up);
+            usub[j] = F::sub(up);
+        }
+#pragma unroll
+        for (int j = 0; j < UX; j++)
+            ubase[j] = (KIND == 2 ? (const uint8_t *)lane_u64(tw0, uspan[j]) : (KIND == 1 ? nullptr : wb)) + uoff[j];
+        nxv = KIND == 2 ? a.nseg * nv : nv;
+        nxu = nxv * nu;
+    }
+
+    __device__ __forceinline__ const float *xsrc(int v, int u) const {
+        return (KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u;
+    }
+
+    // activation pieces (8 floats of one unit per thread, first XP passes) and the lookup-table
+    // words: requested before the weight loads, so waiting for them (vmcnt counts in issue
+    // order) never waits on weights
+    __device__ __forceinline__ void issue_x() {
+        const int sub = tid & (XT - 1);
+#pragma unroll
+        for (int k = 0; k < XP; k++) {
+            const int i = min((tid / XT) + XPU * k, nxu - 1);      // clamped: the loads are unconditional
+            const int v = udiv_small(i, rnu), u = i - v * nu;
+            load8(xsrc(v, u) + 8 * sub, a.x_aligned != 0, xf[k]);
+        }
+    }
+    __device__ __forceinline__ void issue_tab() { F::tab_load(tid, treg); }
+
+    // weight batch of PF rows per lane group from row `base` (rows past the end are clamped to a
+    // valid row; their results are dropped)
+    __device__ __forceinline__ void load_batch(int base) {
+        const int last = nrow > 0 ? nrow - 1 : 0;
 #pragma unroll
         for (int p = 0; p < PF; p++) {
             const int r = min(base + p * ngroups, last);
@@ -267,91 +344,169 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
                 for (int j = 0; j < UX; j++) F::load(ubase[j] + roff, usub[j], R[p][j]);
             }
         }
-    };
-    GS_TS(1, 0)
-    load_batch(gid);
-    GS_TS(2, 0)
-
-    // ---- prologue compute: tables + q8_1 quantization of every activation vector into LDS ----
-    F::tab_store(tid, treg);
-    uint32_t *xm = (uint32_t *)(xq + (size_t)nxv * K);
-    auto quant_store = [&](int i, const float (&f)[32]) {
-        const int v = i / nu, u = i - v * nu;
-        const Q81 q = quant_unit(f);
-        uint4 *dst = (uint4 *)(xq + (size_t)v * K + 32 * u);
-        dst[0] = make_uint4(q.q[0], q.q[1], q.q[2], q.q[3]);
-        dst[1] = make_uint4(q.q[4], q.q[5], q.q[6], q.q[7]);
-        xm[2 * i] = __builtin_bit_cast(uint32_t, h2f(f2h(q.d)));
-        xm[2 * i + 1] = ((uint32_t)q.slo & 0xffffu) | ((uint32_t)q.shi << 16);
-    };
-#pragma unroll
-    for (int k = 0; k < XQ; k++)
-        if (tid + GS_WG * k < nxu) quant_store(tid + GS_WG * k, xf[k]);
-    for (int i = tid + GS_WG * XQ; i < nxu; i += GS_WG) {   // large activation sets: the rest
-        const int v = i / nu, u = i - v * nu;
-        float f[32];
-        load32((KIND == 2 ? x + (int64_t)v * K : x + (int64_t)v * a.x_stride) + 32 * u, a.x_aligned != 0, f);
-        quant_store(i, f);
     }
-    __syncthreads();
-    GS_TS(3, 0)
-    XU xr[UX][NV];
+
+    // tables + q8_1 quantization of every activation vector into LDS (the caller then syncs).
+    // The 4 threads of a unit share its amax and its two half sums through quad DPP; the
+    // arithmetic per element is quant_unit's, so the result is the same bit for bit.
+    __device__ __forceinline__ void stage_x() {
+        F::tab_store(tid, treg);
+        uint32_t *xm = (uint32_t *)(xq + (size_t)nxv * K);
+        const int sub = tid & (XT - 1);
+        auto quant_store = [&](int i, const float (&f)[8]) {
+            const int v = udiv_small(i, rnu), u = i - v * nu;
+            float amax = 0.f;
 #pragma unroll
-    for (int j = 0; j < UX; j++) {
-        const int up = lane + lpr * j - uspan[j] * nu;
+            for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(f[e]));
+            amax = fmaxf(amax, quad_swap<0xB1>(amax));   // quad_perm [1,0,3,2]
+            amax = fmaxf(amax, quad_swap<0x4E>(amax));   // quad_perm [2,3,0,1]
+            const float d = amax / 127.0f;
+            const float id = d != 0.f ? 1.0f / d : 0.f;
+            uint32_t w[2];
+            int sum = 0;
 #pragma unroll
-        for (int t = 0; t < NV; t++) {
-            const int v = KIND == 2 ? uspan[j] * nv + t : t;
-            const float w = KIND == 2 ? a.wt[t][uspan[j]] : 1.f;   // routing weight folded into D
-            xr[j][t] = load_xu<F, XNEG>(xq, xm, K, nu, v, up, w, uval[j] && t < nv);
+            for (int h = 0; h < 2; h++) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int q = (int)__builtin_roundf(f[4 * h + b] * id);
+                    word |= ((uint32_t)q & 0xffu) << (8 * b);
+                    sum += q;
+                }
+                w[h] = word;
+            }
+            *(uint2 *)(xq + (size_t)v * K + 32 * u + 8 * sub) = make_uint2(w[0], w[1]);
+            const int half = sum + __builtin_bit_cast(int, quad_swap<0xB1>(__builtin_bit_cast(float, sum)));
+            const int shi = __builtin_bit_cast(int, quad_swap<0x4E>(__builtin_bit_cast(float, half)));
+            if (sub == 0) {   // elements 0..15 sum in this lane, 16..31 in lane 2 of the quad
+                xm[2 * i] = __builtin_bit_cast(uint32_t, h2f(f2h(d)));
+                xm[2 * i + 1] = ((uint32_t)half & 0xffffu) | ((uint32_t)shi << 16);
+            }
+        };
+#pragma unroll
+        for (int k = 0; k < XP; k++)
+            if ((tid / XT) + XPU * k < nxu) quant_store((tid / XT) + XPU * k, xf[k]);
+        for (int i0 = XPU * XP; i0 < nxu; i0 += XPU) {   // large activation sets: the rest
+            const int i = i0 + tid / XT;
+            if (i < nxu) {   // whole quads are in or out together
+                const int v = udiv_small(i, rnu), u = i - v * nu;
+                float f[8];
+                load8(xsrc(v, u) + 8 * sub, a.x_aligned != 0, f);
+                quant_store(i, f);
+            }
         }
     }
 
-    // ---- batches of PF rows per group ----------------------------------------------------------
-    for (int base = gid; base < nrow; base += PF * ngroups) {
-        if (base != gid) load_batch(base);
-        float res0[PF][NV], res1[PF][NV];
+    // activation units from LDS into registers, then every batch of rows (the first batch is
+    // already loaded) with the results stored
+    __device__ __forceinline__ void run_rows() {
+        const uint32_t *xm = (const uint32_t *)(xq + (size_t)nxv * K);
+        XU xr[UX][NV];
 #pragma unroll
-        for (int p = 0; p < PF; p++) {
-            float acc0[NV], acc1[NV];
-#pragma unroll
-            for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
-#ifdef GS_STREAM_TS
-            if (base == gid && p == 0) {
-                uint32_t h = 0;
-#pragma unroll
-                for (int j = 0; j < UMAX; j++) h ^= ((const uint32_t *)&R[0][j])[0];
-                GS_TS(4, h == 0x9e3779b9u)
-            }
-#endif
-            if (base + p * ngroups < nrow) {   // no loads inside: the waits stay exact
-#pragma unroll
-                for (int j = 0; j < UX; j++) {
-                    F::template dot<NV, XNEG>(R[p][j], usub[j], tab, xr[j], nv, acc0);
-                    if (KIND == 1) F::template dot<NV, XNEG>(R[p][UX + j], usub[j], tab, xr[j], nv, acc1);
-                }
-            }
+        for (int j = 0; j < UX; j++) {
+            const int up = lane + lpr * j - uspan[j] * nu;
 #pragma unroll
             for (int t = 0; t < NV; t++) {
-                res0[p][t] = group_sum(acc0[t], lpr);
-                if (KIND == 1) res1[p][t] = group_sum(acc1[t], lpr);
+                const int v = KIND == 2 ? uspan[j] * nv + t : t;
+                const float w = KIND == 2 ? a.wt[t][uspan[j]] : 1.f;   // routing weight folded into D
+                xr[j][t] = load_xu<F, XNEG>(xq, xm, K, nu, v, up, w, uval[j] && t < nv);
             }
         }
-        if (lane == lpr - 1) {
+        // Row results are gathered into lanes (lane p*NV + t of the group holds row p, vector t)
+        // and finished in parallel: one SwiGLU / store sequence per batch instead of one per row.
+        // Groups narrower than PF*NV results keep one store per row from the group's last lane.
+        const bool gather = PF * NV <= lpr;
+        const int bsrc = ((tid & 63) | (lpr - 1)) << 2;    // byte address of the group's last lane
+        using TP = TwoPhase<F>;
+        for (int base = gid; base < nrow; base += PF * ngroups) {
+            if (base != gid) load_batch(base);
+            float res0[PF][NV], res1[PF][NV];
+            float out0 = 0.f, out1 = 0.f;
+            // units of the batch in order (row p, unit j), each one's table reads issued one unit
+            // ahead (reads of rows past the end fetch valid table entries and are unused)
+            typename TP::Dec dec[2];
+            TP::fetch(R[0][0], dec[0]);
 #pragma unroll
             for (int p = 0; p < PF; p++) {
-                const int rr = base + p * ngroups;
-                if (rr < nrow) {
+                float acc0[NV], acc1[NV];
 #pragma unroll
-                    for (int t = 0; t < NV; t++) {
-                        if (t < nv) {
-                            if (KIND == 0) {
-                                float *dst = y + (int64_t)t * a.y_stride + rr;
-                                *dst = a.accumulate ? *dst + res0[p][t] : res0[p][t];
-                            } else if (KIND == 1) {
-                                y[((int64_t)ge * nv + t) * rows + rr] = swiglu(res0[p][t], res1[p][t], a.lim);
-                            } else {
-                                y[(int64_t)t * a.y_stride + rr] += res0[p][t];
+                for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
+#ifdef GS_STREAM_TS
+                if (base == gid && p == 0) {
+                    uint32_t h = 0;
+#pragma unroll
+                    for (int j = 0; j < UMAX; j++) h ^= ((const uint32_t *)&R[0][j])[0];
+                    GS_TS(4, h == 0x9e3779b9u)
+                }
+#endif
+                if (base + p * ngroups < nrow) {   // no loads inside: the waits stay exact
+#ifdef GS_STREAM_NODOT   // profiling build only: consume the weight words, skip the decode
+#pragma unroll
+                    for (int j = 0; j < UMAX; j++)
+#pragma unroll
+                        for (int w = 0; w < (int)(sizeof(typename F::Raw) / 4); w++)
+                            acc0[0] += __builtin_bit_cast(float, ((const uint32_t *)&R[p][j])[w] & 0x3fffffffu);
+                    if (false)
+#endif
+#pragma unroll
+                    for (int j = 0; j < UMAX; j++) {
+                        const int i = p * UMAX + j;
+                        if (i + 1 < PF * UMAX) TP::fetch(R[(i + 1) / UMAX][(i + 1) % UMAX], dec[(i + 1) & 1]);
+                        if (KIND != 1 && j >= UX) continue;
+                        const int jx = j % UX;
+                        if (KIND == 1 && j >= UX)
+                            TP::template dot<NV, XNEG>(R[p][j], dec[i & 1], usub[jx], tab, xr[jx], nv, acc1);
+                        else
+                            TP::template dot<NV, XNEG>(R[p][j], dec[i & 1], usub[jx], tab, xr[jx], nv, acc0);
+                    }
+                } else if (p + 1 < PF) {
+                    TP::fetch(R[p + 1][0], dec[((p + 1) * UMAX) & 1]);
+                }
+#pragma unroll
+                for (int t = 0; t < NV; t++) {
+                    res0[p][t] = group_sum(acc0[t], lpr);
+                    if (KIND == 1) res1[p][t] = group_sum(acc1[t], lpr);
+                    if (gather) {
+                        const float v0 = __builtin_bit_cast(
+                            float, __builtin_amdgcn_ds_bpermute(bsrc, __builtin_bit_cast(int, res0[p][t])));
+                        out0 = lane == p * NV + t ? v0 : out0;
+                        if (KIND == 1) {
+                            const float v1 = __builtin_bit_cast(
+                                float, __builtin_amdgcn_ds_bpermute(bsrc, __builtin_bit_cast(int, res1[p][t])));
+                            out1 = lane == p * NV + t ? v1 : out1;
+                        }
+                    }
+                }
+            }
+            if (gather) {
+                const int p = lane / NV, t = lane % NV;   // NV is a power of two
+                const int rr = base + p * ngroups;
+                if (lane < PF * NV && t < nv && rr < nrow) {
+                    if (KIND == 0) {
+                        float *dst = y + (int64_t)t * a.y_stride + rr;
+                        *dst = a.accumulate ? *dst + out0 : out0;
+                    } else if (KIND == 1) {
+                        store_h(&y[((int64_t)ge * nv + t) * rows + rr], swiglu(out0, out1, a.lim));
+                    } else {
+                        y[(int64_t)t * a.y_stride + rr] += out0;
+                    }
+                }
+            } else if (lane == lpr - 1) {
+#pragma unroll
+                for (int p = 0; p < PF; p++) {
+                    const int rr = base + p * ngroups;
+                    if (rr < nrow) {
+#pragma unroll
+                        for (int t = 0; t < NV; t++) {
+                            if (t < nv) {
+                                if (KIND == 0) {
+                                    float *dst = y + (int64_t)t * a.y_stride + rr;
+                                    *dst = a.accumulate ? *dst + res0[p][t] : res0[p][t];
+                                } else if (KIND == 1) {
+                                    store_h(&y[((int64_t)ge * nv + t) * rows + rr], swiglu(res0[p][t], res1[p][t], a.lim));
+                                } else {
+                                    y[(int64_t)t * a.y_stride + rr] += res0[p][t];
+                                }
                             }
                         }
                     }
@@ -359,6 +514,24 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
             }
         }
     }
+};
+
+template <class F, int KIND, int NV, int UMAX>
+__device__ __forceinline__ void stream_body(const StreamArgs &a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    GS_TS(0, 0)
+    StreamPass<F, KIND, NV, UMAX> P(a, smem);
+    P.issue_x();
+    P.issue_tab();
+    GS_TS(1, 0)
+    P.load_batch(P.gid);
+    GS_TS(2, 0)
+    P.stage_x();
+#ifndef GS_STREAM_NOBAR
+    __syncthreads();
+#endif
+    GS_TS(3, 0)
+    P.run_rows();
     GS_TS(5, 0)
 }
 
@@ -385,10 +558,127 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     GS_STREAM_KERNEL(F, NAME, 1, 4, 4) GS_STREAM_KERNEL(F, NAME, 1, 8, 2)
 #define GS_STREAM_ALL(F, NAME) GS_STREAM_MV(F, NAME, 0) GS_STREAM_GU(F, NAME) GS_STREAM_MV(F, NAME, 2)
 
+// =============================================================================================
+// Fused routed-expert FFN for one decode token: gate/up + SwiGLU for every expert of the batch,
+// a grid-wide barrier, then down + weighted combine, in one launch (the same work as
+// gs_moe_gateup followed by gs_moe_down). The second launch's start-up (dispatch, argument
+// fetch, first-load latency) disappears, and the down weights are requested before the
+// barrier, so they stream in while the slowest workgroups finish gate/up.
+//
+// The grid must be co-resident (the host sizes it to the occupancy limit). Visibility of h
+// across XCDs needs no cache flush: the gate/up pass stores h at device scope (written through),
+// every workgroup waits for its own stores to complete before it arrives, and nothing reads h
+// before the barrier. The barrier counters only grow (see gs_ffn_sync); the wait is bounded in
+// time (GS_BAR_TICKS of the 100 MHz clock): on expiry gs_ffn_timeout is set and the kernel
+// runs to completion with undefined results instead of hanging. Launches of this kernel must
+// not overlap on one device (they share the counters).
+// =============================================================================================
+#ifndef GS_BAR_TICKS
+#define GS_BAR_TICKS 20000000ull   // 0.2 s
+#endif
+// Barrier counters, one 128-byte line each: arrivals of workgroup group g = blockIdx.x % 8
+// (groups arrive on separate lines, so their atomics proceed in parallel), and completed groups.
+// They only ever grow: a launch adds exactly its group sizes and group count, so each launch
+// finds them at multiples of those and derives its own targets (no reset, nothing to clear).
+struct __attribute__((aligned(128))) BarLine {
+    unsigned long long v;
+    unsigned long long pad[15];
+};
+__device__ BarLine gs_ffn_sync[9];
+__device__ unsigned gs_ffn_timeout;   // set when a barrier wait expired (results undefined)
+
+#define GS_BAR_GROUPS 8u
+// completed-group count at kernel start (read before this workgroup can arrive)
+__device__ __forceinline__ unsigned long long barrier_epoch() {
+    return __hip_atomic_load(&gs_ffn_sync[8].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival of this workgroup (thread 0, after a workgroup barrier that waited for every wave's
+// h stores to complete; they were made at device scope, so completion means visibility).
+__device__ __forceinline__ void grid_arrive() {
+    const unsigned nblk = gridDim.x;
+    const unsigned ng = nblk < GS_BAR_GROUPS ? nblk : GS_BAR_GROUPS;
+    const unsigned g = blockIdx.x % ng;
+    const unsigned size_g = (nblk - g + ng - 1) / ng;   // workgroups in group g
+    const unsigned long long old =
+        __hip_atomic_fetch_add(&gs_ffn_sync[g].v, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old + 1) % size_g == 0)   // last of its group in this launch
+        __hip_atomic_fetch_add(&gs_ffn_sync[8].v, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait (thread 0) until every group of this launch has arrived; bounded in time.
+__device__ __forceinline__ void grid_wait(unsigned long long top0) {
+    const unsigned nblk = gridDim.x;
+    const unsigned ng = nblk < GS_BAR_GROUPS ? nblk : GS_BAR_GROUPS;
+    const unsigned long long target = (top0 / ng + 1) * ng;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(&gs_ffn_sync[8].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 > GS_BAR_TICKS) {
+            __hip_atomic_store(&gs_ffn_timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+template <class F1, class F2, int UM1, int UM2>
+__device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    GS_TS(0, 0)
+    const unsigned long long top0 = threadIdx.x == 0 ? barrier_epoch() : 0;
+    {
+        StreamPass<F1, 1, 1, UM1> G(fa.gu, smem);
+        G.issue_x();
+        G.issue_tab();
+        G.load_batch(G.gid);
+        G.stage_x();
+        __syncthreads();
+        G.run_rows();
+    }
+    GS_TS(1, 0)
+    __syncthreads();   // waits for this workgroup's h stores
+    if (threadIdx.x == 0) grid_arrive();
+    StreamPass<F2, 2, 1, UM2> D(fa.dn, smem);
+    D.issue_tab();
+    D.load_batch(D.gid);   // down weights in flight across the barrier
+    GS_TS(2, 0)
+    if (threadIdx.x == 0) grid_wait(top0);
+    __builtin_amdgcn_s_barrier();   // no memory wait: the down weights keep streaming
+    GS_TS(3, 0)
+    D.issue_x();           // h, complete in every expert
+    D.stage_x();
+    __syncthreads();
+    GS_TS(6, 0)
+    D.run_rows();
+    GS_TS(7, 0)
+}
+
+#define GS_FFN_KERNEL(F1, N1, F2, N2, UM1, UM2)                                                  \
+    extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE))) \
+        gs_k_ffn_##N1##_##N2##_##UM1##_##UM2(FfnArgs a) {                                        \
+        ffn_body<F1, F2, UM1, UM2>(a);                                                          \
+    }
+// (gate/up units per lane, down units per lane): the unit budgets the host picks for one token
+#define GS_FFN_ALL(F1, N1, F2, N2)                                                              \
+    GS_FFN_KERNEL(F1, N1, F2, N2, 2, 2) GS_FFN_KERNEL(F1, N1, F2, N2, 2, 4)                     \
+    GS_FFN_KERNEL(F1, N1, F2, N2, 2, 6) GS_FFN_KERNEL(F1, N1, F2, N2, 2, 8)                     \
+    GS_FFN_KERNEL(F1, N1, F2, N2, 4, 2) GS_FFN_KERNEL(F1, N1, F2, N2, 4, 4)                     \
+    GS_FFN_KERNEL(F1, N1, F2, N2, 4, 6) GS_FFN_KERNEL(F1, N1, F2, N2, 4, 8)                     \
+    GS_FFN_KERNEL(F1, N1, F2, N2, 8, 2) GS_FFN_KERNEL(F1, N1, F2, N2, 8, 4)                     \
+    GS_FFN_KERNEL(F1, N1, F2, N2, 8, 6) GS_FFN_KERNEL(F1, N1, F2, N2, 8, 8)
+
 // One code object per format keeps the build parallel: the Makefile compiles this file once
 // per GS_STREAM_TYPE (F-struct, type id) and once with GS_COMMON for the kernels below.
 #if defined(GS_STREAM_F)
 GS_STREAM_ALL(GS_STREAM_F, GS_STREAM_ID)
+// fused FFN for the formats with a fast decode; gate/up and down in the same format, plus the
+// IQ2_XXS gate/up with IQ3_XXS down experts of the target model
+#if GS_STREAM_ID == 8 || GS_STREAM_ID == 12 || GS_STREAM_ID == 14 || GS_STREAM_ID == 16 || GS_STREAM_ID == 18
+GS_FFN_ALL(GS_STREAM_F, GS_STREAM_ID, GS_STREAM_F, GS_STREAM_ID)
+#endif
+#if GS_STREAM_ID == 16
+GS_FFN_ALL(FIQ2_XXS, 16, FIQ3_XXS, 18)
+#endif
 #endif
 
 #if defined(GS_COMMON)

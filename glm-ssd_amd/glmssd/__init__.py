@@ -79,6 +79,8 @@ SIGNATURES = {
     "gs_gemv_batched": [C.c_int, _P, _I64, C.c_int, C.c_int, _P, _P, C.c_int, _I64, _I64, _I64, _P],
     "gs_moe_gateup": [C.c_int, C.POINTER(MoeBatch), C.c_int, _I64, C.c_int, C.c_int, _P, _P, C.c_float, _P],
     "gs_moe_down": [C.c_int, C.POINTER(MoeBatch), C.c_int, _I64, C.c_int, C.c_int, _P, _P, _P],
+    "gs_moe_ffn": [C.c_int, C.c_int, C.POINTER(MoeBatch), C.c_int, _I64, C.c_int, C.c_int, _I64, _P, _P, _P, C.c_float,
+                   _P],
     "gs_swiglu": [_P, _P, _P, _I64, C.c_float, _P],
     "gs_axpy": [_P, _P, C.c_float, _I64, _P],
     "gs_gemm": [C.c_int, _P, _I64, C.c_int, C.c_int, _P, _I64, _P, _I64, C.c_int, C.c_int, C.c_int, _I64, _I64, _I64,
@@ -268,6 +270,12 @@ class ops:
     @staticmethod
     def moe_down(ty, batch, nt, row_stride, k, rows, h, y, s=None):
         check(lib().gs_moe_down(ty, C.byref(batch), nt, row_stride, k, rows, _p(h), _p(y), _raw(s)))
+
+    @staticmethod
+    def moe_ffn(ty_gu, ty_dn, batch, nt, rs_gu, n_embd, n_ff, rs_dn, x, h, y, lim=0.0, s=None):
+        """gs_moe_ffn: moe_gateup then moe_down (one fused launch for one token)."""
+        check(lib().gs_moe_ffn(ty_gu, ty_dn, C.byref(batch), nt, rs_gu, n_embd, n_ff, rs_dn, _p(x), _p(h), _p(y), lim,
+                               _raw(s)))
 
     @staticmethod
     def gemm(ty, w, row_stride, k, rows, x, x_stride, y, y_stride, n, accumulate=False, n_batch=1, w_bs=0, x_bs=0,

@@ -108,6 +108,16 @@ int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K
 int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *h, float *y,
                 void *s);
 
+/* Additive (no counterpart in the reference): the whole routed-expert FFN of one layer, exactly
+ * gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, lim) followed by
+ * gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y); replaces the pair the decode path calls
+ * per expert batch (crates/engine/src/forward.rs:1067-1107). For one token it is one launch
+ * (gate/up, grid-wide barrier, down) when the format pair has a fused kernel (IQ2_XXS, IQ3_XXS,
+ * Q4_K, Q6_K, Q8_0 each with itself; IQ2_XXS gate/up with IQ3_XXS down), else the two launches.
+ * Fused launches must not overlap in time on one device (they share the barrier counters). */
+int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int64_t rs_gu, int n_embd, int n_ff, int64_t rs_dn,
+               const float *x, float *h, float *y, float lim, void *s);
+
 /* ---- GEMM and MoE glue (crates/cuda/src/lib.rs:71-74,115-122; kernels/gemm.cu, ops.cu) ---- */
 /* SwiGLU with clamp: y = silu(min(g,L)) * clamp(u,-L,L); L <= 0: no clamp (lib.rs:76; ops.cu:101-115) */
 int gs_swiglu(const float *g, const float *u, float *y, int64_t n, float lim, void *s);

@@ -1,0 +1,86 @@
+"""GPU parity of gs_moe_ffn (the whole routed-expert FFN in one call; one fused launch with a
+grid-wide barrier for a single token): against the CPU oracle (rel-L2 <= 1e-3, as every matmul
+path), and bit for bit against the two-launch path gs_moe_gateup + gs_moe_down, which computes the
+same sums in the same order. Repeated calls check that the barrier counters are left at zero."""
+import sys
+
+import numpy as np
+import pytest
+
+import glmssd as G
+from glmssd import GgmlType as T
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+REL_L2 = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel_l2(got, want):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def stream():
+    return G.Stream()
+
+
+# (gate/up type, down type, tokens, experts, n_embd, n_ff, clamp); nt = 2 takes the two-launch path
+CASES = [(T.IQ2_XXS, T.IQ2_XXS, 1, 8, 4096, 1536, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 1, 8, 2048, 1536, 0.0),
+         (T.Q4_K, T.Q4_K, 1, 5, 2048, 1024, 7.0), (T.Q8_0, T.Q8_0, 1, 3, 1024, 1024, 0.0),
+         (T.Q6_K, T.Q6_K, 1, 4, 2048, 512, 3.0), (T.IQ3_XXS, T.IQ3_XXS, 1, 1, 2048, 768, 0.0),
+         (T.IQ2_XXS, T.IQ2_XXS, 2, 6, 2048, 1024, 0.0), (T.Q5_K, T.Q5_K, 1, 2, 1024, 512, 0.0)]
+
+
+@pytest.mark.parametrize("ty_gu,ty_dn,nt,n,n_embd,n_ff,lim", CASES)
+def test_moe_ffn(ty_gu, ty_dn, nt, n, n_embd, n_ff, lim, stream):
+    say(f"moe_ffn {G.TYPE_NAMES[ty_gu]}/{G.TYPE_NAMES[ty_dn]} nt={nt} n={n} {n_embd}x{n_ff} lim={lim}")
+    rng = O.Rng(777 + 31 * ty_gu + ty_dn + n)
+    gate = [rng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(n)]
+    up = [rng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(n)]
+    down = [rng.random_blocks(ty_dn, n_embd * n_ff) for _ in range(n)]
+    nrng = np.random.default_rng(n_embd + n)
+    x = nrng.standard_normal((nt, n_embd)).astype(np.float32)
+    w = nrng.random((nt, n)).astype(np.float32)
+    if n > 1:
+        w[0, 1] = 0.0                                   # token 0 not routed to expert 1
+    pt, pe, pw = [], [], []
+    for t in range(nt):
+        for e in range(n):
+            pt.append(t); pe.append(e); pw.append(w[t, e])
+    rbg, rbd = G.row_bytes(ty_gu, n_embd), G.row_bytes(ty_dn, n_ff)
+    want = O.moe_ffn(ty_gu, ty_dn, gate, up, down, rbg, rbd, n_embd, n_ff, x, pt, pe, pw, lim=lim, nthreads=8)
+    bufs = [G.DeviceBuffer.from_array(a) for a in gate + up + down]
+    b = G.MoeBatch()
+    b.n = n
+    for e in range(n):
+        b.gate[e], b.up[e], b.down[e] = bufs[e].p.value, bufs[n + e].p.value, bufs[2 * n + e].p.value
+        for t in range(nt):
+            b.w[t][e] = w[t, e]
+    dx = G.DeviceBuffer.from_array(x)
+    y0 = nrng.standard_normal((nt, n_embd)).astype(np.float32)
+    # reference: the two launches
+    dh2 = G.DeviceBuffer(n * nt * n_ff * 4)
+    dy2 = G.DeviceBuffer.from_array(y0)
+    G.ops.moe_gateup(ty_gu, b, nt, rbg, n_embd, n_ff, dx, dh2, lim, stream)
+    G.ops.moe_down(ty_dn, b, nt, rbd, n_ff, n_embd, dh2, dy2, stream)
+    y2 = dy2.download(np.float32, nt * n_embd, stream)
+    h2 = dh2.download(np.float32, n * nt * n_ff, stream)
+    for rep in range(3):
+        dh = G.DeviceBuffer(n * nt * n_ff * 4)
+        dy = G.DeviceBuffer.from_array(y0)
+        G.ops.moe_ffn(ty_gu, ty_dn, b, nt, rbg, n_embd, n_ff, rbd, dx, dh, dy, lim, stream)
+        y = dy.download(np.float32, nt * n_embd, stream)
+        h = dh.download(np.float32, n * nt * n_ff, stream)
+        got = y.reshape(nt, n_embd).astype(np.float64) - y0
+        e = rel_l2(got, want)
+        say(f"  call {rep}: y rel-L2 vs oracle {e:.2e}; identical to two launches: h {np.array_equal(h, h2)} "
+            f"y {np.array_equal(y, y2)}")
+        assert e <= REL_L2
+        assert np.array_equal(h, h2) and np.array_equal(y, y2)
