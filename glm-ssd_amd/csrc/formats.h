@@ -238,15 +238,46 @@ __device__ __forceinline__ uint2 ldg8(const uint8_t *p) { return make_uint2(ldg4
 __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return make_uint4(ldg4(p), ldg4(p + 4), ldg4(p + 8), ldg4(p + 12)); }
 __device__ __forceinline__ uint32_t ldg2(const uint8_t *p) { return ldg<uint16_t>(p); }
 
+// Weight byte accessors for the formats' load(): GlobalAt reads base + offset with global loads;
+// BufferAt reads through a buffer resource built from a wave-uniform base, so every load is
+// SGPR resource + 32-bit lane offset (no per-load 64-bit address arithmetic). Offsets are bytes,
+// 2-byte aligned; both serve unaligned 4/8/16-byte reads.
+struct GlobalAt {
+    const uint8_t *b;
+    __device__ __forceinline__ uint32_t u16(uint32_t o) const { return ldg2(b + o); }
+    __device__ __forceinline__ uint32_t u32(uint32_t o) const { return ldg4(b + o); }
+    __device__ __forceinline__ uint2 u64(uint32_t o) const { return ldg8(b + o); }
+    __device__ __forceinline__ uint4 u128(uint32_t o) const { return ldg16(b + o); }
+    __device__ __forceinline__ const uint8_t *ptr(uint32_t o) const { return b + o; }
+};
+struct BufferAt {
+    __amdgpu_buffer_rsrc_t r;
+    const uint8_t *b;
+    __device__ __forceinline__ explicit BufferAt(const uint8_t *base)
+        : r(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, -1, 0x00020000)), b(base) {}
+    __device__ __forceinline__ uint32_t u16(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b16(r, o, 0, 0); }
+    __device__ __forceinline__ uint32_t u32(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0); }
+    __device__ __forceinline__ uint2 u64(uint32_t o) const {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0);
+        return make_uint2(v[0], v[1]);
+    }
+    __device__ __forceinline__ uint4 u128(uint32_t o) const {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0);
+        return make_uint4(v[0], v[1], v[2], v[3]);
+    }
+    __device__ __forceinline__ const uint8_t *ptr(uint32_t o) const { return b + o; }
+};
+
 // Each format: Raw = the registers one unit needs from memory; load() issues the loads for unit
-// `j` of the block at `b`; dot() decodes Raw and accumulates r[t] += W_unit . x_t for t < nv.
+// `j` of the block at byte offset o of an accessor (GlobalAt / BufferAt); dot() decodes Raw and accumulates r[t] += W_unit . x_t for t < nv.
 struct FQ8_0 : UnitGeom<32, 34>, NoTable {
     static constexpr int TYPE = GS_Q8_0, QK = 32, BB = 34, TAB = 0, RAW = 9;
     struct Raw { uint4 lo, hi; uint32_t d; };
-    __device__ static __forceinline__ void load(const uint8_t *b, int, Raw &w) {
-        w.d = ldg2(b);
-        w.lo = ldg16(b + 2);
-        w.hi = ldg16(b + 18);
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int, Raw &w) {
+        w.d = m.u16(o);
+        w.lo = m.u128(o + 2);
+        w.hi = m.u128(o + 18);
     }
     template <int NV, bool XNEG = false>
     __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
@@ -262,10 +293,11 @@ struct FQ8_0 : UnitGeom<32, 34>, NoTable {
 struct FQ4_K : UnitGeom<256, 144>, NoTable {
     static constexpr int TYPE = GS_Q4_K, QK = 256, BB = 144, TAB = 0, RAW = 12;
     struct Raw { uint4 hd, lo, hi; };   // bytes 0..15 (d, dmin, scales[12]); 32 quant bytes
-    __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
-        w.hd = ldg16(b);
-        w.lo = ldg16(b + 16 + 32 * (j >> 1));
-        w.hi = ldg16(b + 32 + 32 * (j >> 1));
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int j, Raw &w) {
+        w.hd = m.u128(o);
+        w.lo = m.u128(o + 16 + 32 * (uint32_t)(j >> 1));
+        w.hi = m.u128(o + 32 + 32 * (uint32_t)(j >> 1));
     }
     template <int NV, bool XNEG = false>
     __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
@@ -297,15 +329,16 @@ struct FQ4_K : UnitGeom<256, 144>, NoTable {
 struct FQ6_K : UnitGeom<256, 210>, NoTable {
     static constexpr int TYPE = GS_Q6_K, QK = 256, BB = 210, TAB = 0, RAW = 18;
     struct Raw { uint4 l0, l1, h0, h1; uint32_t sc, d; };
-    __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
-        const int half = j >> 2, quarter = j & 3;
-        const uint8_t *ql = b + 64 * half + 32 * (quarter & 1), *qh = b + 128 + 32 * half;
-        w.l0 = ldg16(ql);
-        w.l1 = ldg16(ql + 16);
-        w.h0 = ldg16(qh);
-        w.h1 = ldg16(qh + 16);
-        w.sc = ldg2(b + 192 + 8 * half + 2 * quarter);
-        w.d = ldg2(b + 208);
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int j, Raw &w) {
+        const uint32_t half = (uint32_t)j >> 2, quarter = (uint32_t)j & 3;
+        const uint32_t ql = o + 64 * half + 32 * (quarter & 1), qh = o + 128 + 32 * half;
+        w.l0 = m.u128(ql);
+        w.l1 = m.u128(ql + 16);
+        w.h0 = m.u128(qh);
+        w.h1 = m.u128(qh + 16);
+        w.sc = m.u16(o + 192 + 8 * half + 2 * quarter);
+        w.d = m.u16(o + 208);
     }
     template <int NV, bool XNEG = false>
     __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
@@ -334,13 +367,13 @@ struct FQ6_K : UnitGeom<256, 210>, NoTable {
     }
 };
 
-// IQ2_XXS: the 256-entry grid (2 KiB) and a 128-entry table of v_perm_b32 selectors (1 KiB)
-// live in LDS at fixed addresses (folded into the ds_read offsets). The signs are applied to the
+// IQ2_XXS: the 256-entry grid (2 KiB) and a table of v_perm_b32 selectors (2 KiB: 128 sign
+// indices, each stored twice so an 8-bit index with a stray top bit needs no mask) live in LDS at fixed addresses (folded into the ds_read offsets). The signs are applied to the
 // activations, not the weights: a selector picks, per byte, q (sel = i) or -q (sel = i+4) from
 // the pair {-q, q}, and -q is computed once per activation unit (XU::nq), so a group of 8
 // elements costs 2 table reads, 2 v_perm_b32 and 2 v_dot4_i32_i8.
 __shared__ uint2 gs_iq2xxs_grid_lds[256];
-__shared__ uint2 gs_iq2xxs_sel_lds[128];
+__shared__ uint2 gs_iq2xxs_sel_lds[256];   // entry i = selectors of sign index i & 127
 
 // v_perm_b32 selectors for sign index i (two words, elements 0-3 and 4-7): byte e selects q
 // (selector e) or -q (selector e + 4) from the pair {-q, q} by bit e of ksigns(i).
@@ -367,13 +400,29 @@ __device__ __forceinline__ uint32_t grid_off(uint32_t a) {
     return r;
 }
 
-// r[t] += db * x[t].D * sum over 4 groups of 8: grid bytes g[l] . (signs s[l] applied) q. XNEG: the
+// Byte offset of the selector row of sign field L (7 bits at bit 7L of a): byte L of a << L holds
+// the field in its low 7 bits (the 8th bit is the next field's, which the doubled table ignores).
+template <int L>
+__device__ __forceinline__ uint32_t sel_off(uint32_t a) {
+    return grid_off<L>(L ? a << L : a);
+}
+
+// sum of 4 int8 products, with a zero accumulator (the VOP3 form: no register to clear first)
+__device__ __forceinline__ int sdot4_0(uint32_t a, uint32_t b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// r[t] += dh * x[t].D * m * sum over 4 groups of 8: grid bytes g[l] . (signs s[l] applied) q. XNEG: the
 // activation units carry -q and the v_perm_b32 selectors pick q or -q per byte (2 operations per
 // 8 elements); otherwise the signs go on the grid bytes (every grid byte is nonzero, so
 // 0x01010100 - g negates bytewise; one more operation per 4 elements).
+// The unit scale is dh * m with m = 2s+1 an odd integer up to 31, applied to the integer sum
+// (|sum| < 2^18, so the 24-bit multiply is exact) before the one float conversion.
 template <int NV, bool XNEG>
-__device__ __forceinline__ void signed_dot8x4(const uint2 (&g_)[4], const uint2 (&s)[4], float db, const XU (&x)[NV],
-                                              int nv, float (&r)[NV]) {
+__device__ __forceinline__ void signed_dot8x4(const uint2 (&g_)[4], const uint2 (&s)[4], float dh, int m,
+                                              const XU (&x)[NV], int nv, float (&r)[NV]) {
     uint2 g[4] = {g_[0], g_[1], g_[2], g_[3]};
     if (!XNEG) {
 #pragma unroll
@@ -391,10 +440,10 @@ __device__ __forceinline__ void signed_dot8x4(const uint2 (&g_)[4], const uint2 
                 const uint32_t q0 = XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l], x[t].q[2 * l], s[l].x) : x[t].q[2 * l];
                 const uint32_t q1 =
                     XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l + 1], x[t].q[2 * l + 1], s[l].y) : x[t].q[2 * l + 1];
-                acc = __builtin_amdgcn_sdot4((int)g[l].x, (int)q0, acc, false);
+                acc = l == 0 ? sdot4_0(g[l].x, q0) : __builtin_amdgcn_sdot4((int)g[l].x, (int)q0, acc, false);
                 acc = __builtin_amdgcn_sdot4((int)g[l].y, (int)q1, acc, false);
             }
-            r[t] += (db * x[t].D) * (float)acc;
+            r[t] += (dh * x[t].D) * (float)__mul24(acc, m);
         }
     }
 }
@@ -402,22 +451,19 @@ __device__ __forceinline__ void signed_dot8x4(const uint2 (&g_)[4], const uint2 
 struct FIQ2_XXS : UnitGeom<256, 66> {
     static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 0, RAW = 3;
     static constexpr bool NEG_X = true;
-    static constexpr float XSCALE = 0.25f;   // the format's /4, folded into the activation scale
+    static constexpr float XSCALE = 0.125f;   // the format's /4 and the 1/2 of (2s+1)/2, in the activation scale
     struct Raw { uint2 a; uint32_t d; };
     // table setup split in two so the global read can be issued before the weight prefetch
     struct TabReg { uint64_t g; };
     __device__ static __forceinline__ void tab_load(int tid, TabReg &r) { r.g = tid < 256 ? iq2xxs_grid[tid] : 0; }
     __device__ static __forceinline__ void tab_store(int tid, const TabReg &r) {
         if (tid < 256) gs_iq2xxs_grid_lds[tid] = make_uint2((uint32_t)r.g, (uint32_t)(r.g >> 32));
-        if (tid < 128) gs_iq2xxs_sel_lds[tid] = sign_sel(tid);
+        if (tid < 256) gs_iq2xxs_sel_lds[tid] = sign_sel(tid & 127);
     }
-    __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
-#ifdef GS_STREAM_NOD   // profiling build only: no scale load
-        w.d = 0x3c00u;
-#else
-        w.d = ldg2(b);
-#endif
-        w.a = ldg8(b + 2 + 8 * j);
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int j, Raw &w) {
+        w.d = m.u16(o);
+        w.a = m.u64(o + 2 + 8 * (uint32_t)j);
     }
     // XNEG: the activation units carry -q (signs applied on the activation side, 2 ops per 8
     // elements); otherwise the signs are applied to the grid bytes (one more op per 4 elements,
@@ -430,14 +476,16 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
 #pragma unroll
         for (int l = 0; l < 4; l++) {
             e.g[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_grid_lds + gofs[l]);
-            e.s[l] = gs_iq2xxs_sel_lds[(w.a.y >> (7 * l)) & 127];
         }
+        const uint32_t sofs[4] = {sel_off<0>(w.a.y), sel_off<1>(w.a.y), sel_off<2>(w.a.y), sel_off<3>(w.a.y)};
+#pragma unroll
+        for (int l = 0; l < 4; l++) e.s[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_sel_lds + sofs[l]);
     }
     template <int NV, bool XNEG = true>
     __device__ static __forceinline__ void dot2(const Raw &w, const Dec &e, const XU (&x)[NV], int nv, float (&r)[NV]) {
-        // db = d * (0.5 + s) * 0.25 (lib.rs:279); the 0.25 is already in x.D
-        const float db = h2f(w.d) * (0.5f + (float)(w.a.y >> 28));
-        signed_dot8x4<NV, XNEG>(e.g, e.s, db, x, nv, r);
+        // db = d * (0.5 + s) * 0.25 = d * (2s+1) * 0.125 (lib.rs:279); the 0.125 is in x.D, and
+        // (a >> 27) | 1 = 2s+1 whatever bit 27 (a sign bit) is
+        signed_dot8x4<NV, XNEG>(e.g, e.s, h2f(w.d), (int)((w.a.y >> 27) | 1u), x, nv, r);
     }
     template <int NV, bool XNEG = true>
     __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
@@ -468,18 +516,19 @@ __device__ __forceinline__ uint32_t grid_off4(uint32_t a) {
 struct FIQ3_XXS : UnitGeom<256, 98> {
     static constexpr int TYPE = GS_IQ3_XXS, QK = 256, BB = 98, TAB = 0, RAW = 4;
     static constexpr bool NEG_X = true;
-    static constexpr float XSCALE = 0.5f;   // the format's trailing *0.5, folded into the activation scale
+    static constexpr float XSCALE = 0.25f;   // the format's *0.5 and the 1/2 of (2s+1)/2, in the activation scale
     struct Raw { uint2 a; uint32_t s; uint32_t d; };
     struct TabReg { uint32_t g; };
     __device__ static __forceinline__ void tab_load(int tid, TabReg &r) { r.g = tid < 256 ? iq3xxs_grid[tid] : 0; }
     __device__ static __forceinline__ void tab_store(int tid, const TabReg &r) {
         if (tid < 256) gs_iq3xxs_grid_lds[tid] = r.g;
-        if (tid < 128) gs_iq2xxs_sel_lds[tid] = sign_sel(tid);
+        if (tid < 256) gs_iq2xxs_sel_lds[tid] = sign_sel(tid & 127);
     }
-    __device__ static __forceinline__ void load(const uint8_t *b, int j, Raw &w) {
-        w.d = ldg2(b);
-        w.a = ldg8(b + 2 + 8 * j);
-        w.s = ldg4(b + 66 + 4 * j);
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int j, Raw &w) {
+        w.d = m.u16(o);
+        w.a = m.u64(o + 2 + 8 * (uint32_t)j);
+        w.s = m.u32(o + 66 + 4 * (uint32_t)j);
     }
     struct Dec { uint2 g[4], s[4]; };
     __device__ static __forceinline__ void fetch(const Raw &w, Dec &e) {
@@ -488,14 +537,14 @@ struct FIQ3_XXS : UnitGeom<256, 98> {
         e.g[1] = make_uint2(*(const uint32_t *)(gt + grid_off4<2>(w.a.x)), *(const uint32_t *)(gt + grid_off4<3>(w.a.x)));
         e.g[2] = make_uint2(*(const uint32_t *)(gt + grid_off4<0>(w.a.y)), *(const uint32_t *)(gt + grid_off4<1>(w.a.y)));
         e.g[3] = make_uint2(*(const uint32_t *)(gt + grid_off4<2>(w.a.y)), *(const uint32_t *)(gt + grid_off4<3>(w.a.y)));
+        const uint32_t sofs[4] = {sel_off<0>(w.s), sel_off<1>(w.s), sel_off<2>(w.s), sel_off<3>(w.s)};
 #pragma unroll
-        for (int l = 0; l < 4; l++) e.s[l] = gs_iq2xxs_sel_lds[(w.s >> (7 * l)) & 127];
+        for (int l = 0; l < 4; l++) e.s[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_sel_lds + sofs[l]);
     }
     template <int NV, bool XNEG = true>
     __device__ static __forceinline__ void dot2(const Raw &w, const Dec &e, const XU (&x)[NV], int nv, float (&r)[NV]) {
-        // db = d * (0.5 + s) * 0.5 (lib.rs:318); the 0.5 is already in x.D
-        const float db = h2f(w.d) * (0.5f + (float)(w.s >> 28));
-        signed_dot8x4<NV, XNEG>(e.g, e.s, db, x, nv, r);
+        // db = d * (0.5 + s) * 0.5 = d * (2s+1) * 0.25 (lib.rs:318); the 0.25 is in x.D
+        signed_dot8x4<NV, XNEG>(e.g, e.s, h2f(w.d), (int)((w.s >> 27) | 1u), x, nv, r);
     }
     template <int NV, bool XNEG = true>
     __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
@@ -512,7 +561,8 @@ template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float *)>
 struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
     static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0, RAW = 2;
     struct Raw { const uint8_t *p; };
-    __device__ static __forceinline__ void load(const uint8_t *b, int, Raw &w) { w.p = b; }
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int, Raw &w) { w.p = m.ptr(o); }
     template <int NV, bool XNEG = false>
     __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {

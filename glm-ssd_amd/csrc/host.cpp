@@ -184,7 +184,12 @@ hipError_t plan_stream(DeviceCtx *c, int kind, int ty, StreamArgs &a, StreamPlan
                 : NVt == 4 ? std::vector<int>{1, 2} : std::vector<int>{1};
     int best_lpr = -1, best_um = 0;
     double best_eff = -1.0;
+    // GLMSSD_LPR_GU / GLMSSD_LPR_DN: tuning override of the lane-group width (16, 32 or 64)
+    static const int lpr_gu = getenv("GLMSSD_LPR_GU") ? atoi(getenv("GLMSSD_LPR_GU")) : 0;
+    static const int lpr_dn = getenv("GLMSSD_LPR_DN") ? atoi(getenv("GLMSSD_LPR_DN")) : 0;
+    const int force = kind == 1 ? lpr_gu : kind == 2 ? lpr_dn : 0;
     for (int lpr : {64, 32, 16}) {
+        if (force && lpr != force) continue;
         const int upl = (tot + lpr - 1) / lpr;
         int um = 0;
         for (int u : umaxes)
@@ -228,8 +233,10 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     StreamPlan P;
     if ((e = plan_stream(c, kind, ty, a, P)) != hipSuccess) return e;
     const int NVt = a.nvec <= 1 ? 1 : a.nvec <= 2 ? 2 : a.nvec <= 4 ? 4 : 8;
+    // one token with 64-lane groups: the variant with the group width fixed at compile time
+    const bool w64 = a.lpr == 64 && NVt == 1 && kind != 2;
     const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" +
-                             std::to_string(NVt) + "_" + std::to_string(P.um);
+                             std::to_string(NVt) + "_" + std::to_string(P.um) + (w64 ? "_w" : "");
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
     const int per_cu = std::max(1, blocks_per_cu(c, name, f, P.lds));
@@ -516,7 +523,8 @@ GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int6
     if (fuse) {
         if ((rc = gateup_args(fa.gu, b, nt, rs_gu, n_embd, n_ff, x, h, lim))) return rc;
         if ((rc = down_args(fa.dn, b, 0, b->n, nt, rs_dn, n_ff, n_embd, h, y))) return rc;
-        fuse = plan_stream(c, 1, ty_gu, fa.gu, P1) == hipSuccess && plan_stream(c, 2, ty_dn, fa.dn, P2) == hipSuccess;
+        fuse = plan_stream(c, 1, ty_gu, fa.gu, P1) == hipSuccess && plan_stream(c, 2, ty_dn, fa.dn, P2) == hipSuccess &&
+               fa.gu.lpr == 64;   // the fused kernels fix 64-lane groups for gate/up
     }
     if (fuse) {
         const std::string name = "gs_k_ffn_" + std::to_string(ty_gu) + "_" + std::to_string(ty_dn) + "_" +

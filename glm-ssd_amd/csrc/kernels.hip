@@ -97,6 +97,15 @@ __device__ __forceinline__ float swiglu(float g, float u, float lim) { // ops.cu
     }
     return g / (1.f + expf(-g)) * u;
 }
+// The same with the hardware exp2 and reciprocal (about 1 ulp each instead of the correctly
+// rounded library sequences): the fused gate/up epilogue, where h then goes through q8_1.
+__device__ __forceinline__ float swiglu_fast(float g, float u, float lim) {
+    if (lim > 0.f) {
+        g = fminf(g, lim);
+        u = fminf(fmaxf(u, -lim), lim);
+    }
+    return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f)) * u;
+}
 
 // =============================================================================================
 // Streaming matrix-vector kernel (GEMV / fused MoE gate-up / fused MoE down).
@@ -204,7 +213,9 @@ __device__ __forceinline__ void store_h(float *p, float v) {
 // integer, and the two roundings move it by at most 3 * 2^-24 * (u + 0.5) / d, less than that.
 __device__ __forceinline__ int udiv_small(int u, float rd) { return (int)(((float)u + 0.5f) * rd); }
 
-template <class F, int KIND, int NV, int UMAX>
+// LP: 0 = lane-group width from the arguments; 64 = fixed 64 (whole rows per wave, so the row
+// index and every row address are wave-uniform scalars)
+template <class F, int KIND, int NV, int UMAX, int LP = 0>
 struct StreamPass {
     static constexpr int PF = pf_depth<F, UMAX>();
     static constexpr int UX = KIND == 1 ? UMAX / 2 : UMAX;       // activation units per lane
@@ -223,7 +234,7 @@ struct StreamPass {
     int K, nu, nv, rows, lpr, lane, tot, ngroups, gid, nrow, ge, nxv, nxu;
     float rnu;   // 1/nu
     int64_t rs;
-    const uint8_t *wg, *wu;
+    const uint8_t *wg, *wu, *wb0;   // GATEUP gate / up, GEMV matrix (wave-uniform)
     int uspan[UX], usub[UX];
     uint32_t uoff[UX];
     bool uval[UX];
@@ -246,7 +257,7 @@ struct StreamPass {
             y += (int64_t)blockIdx.y * a.y_bs;
         }
         K = a.K, nu = a.nu, nv = a.nvec, rows = a.rows;
-        lpr = a.lpr, lane = tid & (lpr - 1);
+        lpr = LP ? LP : a.lpr, lane = tid & (lpr - 1);
         tot = KIND == 2 ? a.nseg * nu : nu;          // units along the (concatenated) row
         // Lane groups: GATEUP pins each wave to one expert (its pointers are wave-uniform) and the
         // wave's groups stride over that expert's rows; other kinds stride over all rows.
@@ -281,6 +292,7 @@ struct StreamPass {
             return (uint64_t)lo | ((uint64_t)hi << 32);
         };
         wg = wu = nullptr;
+        wb0 = wb;
         if (KIND == 1) {
             wg = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw0 >> 32), ge) << 32) |
                                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw0, ge));
@@ -302,7 +314,7 @@ struct StreamPass {
         }
 #pragma unroll
         for (int j = 0; j < UX; j++)
-            ubase[j] = (KIND == 2 ? (const uint8_t *)lane_u64(tw0, uspan[j]) : (KIND == 1 ? nullptr : wb)) + uoff[j];
+            ubase[j] = KIND == 2 ? (const uint8_t *)lane_u64(tw0, uspan[j]) : (KIND == 1 ? nullptr : wb);
         nxv = KIND == 2 ? a.nseg * nv : nv;
         nxu = nxv * nu;
     }
@@ -329,6 +341,24 @@ struct StreamPass {
     // valid row; their results are dropped)
     __device__ __forceinline__ void load_batch(int base) {
         const int last = nrow > 0 ? nrow - 1 : 0;
+        // A 64-lane group covers whole rows, so its row index is wave-uniform: the row address is
+        // then scalar arithmetic and every load goes through a buffer resource on that address
+        // with a 32-bit lane offset (no per-load 64-bit vector adds).
+        if (KIND != 2 && LP == 64) {
+            const uint8_t *bg = KIND == 1 ? wg : wb0;
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                const int r = __builtin_amdgcn_readfirstlane(min(base + p * ngroups, last));
+                const BufferAt mg(bg + (int64_t)r * rs);
+                const BufferAt mu(KIND == 1 ? wu + (int64_t)r * rs : bg);
+#pragma unroll
+                for (int j = 0; j < UX; j++) {
+                    F::load(mg, uoff[j], usub[j], R[p][j]);
+                    if (KIND == 1) F::load(mu, uoff[j], usub[j], R[p][UX + j]);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int p = 0; p < PF; p++) {
             const int r = min(base + p * ngroups, last);
@@ -336,12 +366,12 @@ struct StreamPass {
             if (KIND == 1) {
 #pragma unroll
                 for (int j = 0; j < UX; j++) {
-                    F::load(wg + roff + uoff[j], usub[j], R[p][j]);
-                    F::load(wu + roff + uoff[j], usub[j], R[p][UX + j]);
+                    F::load(GlobalAt{wg + roff}, uoff[j], usub[j], R[p][j]);
+                    F::load(GlobalAt{wu + roff}, uoff[j], usub[j], R[p][UX + j]);
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < UX; j++) F::load(ubase[j] + roff, usub[j], R[p][j]);
+                for (int j = 0; j < UX; j++) F::load(GlobalAt{ubase[j] + roff}, uoff[j], usub[j], R[p][j]);
             }
         }
     }
@@ -453,6 +483,9 @@ struct StreamPass {
                         const int i = p * UMAX + j;
                         if (i + 1 < PF * UMAX) TP::fetch(R[(i + 1) / UMAX][(i + 1) % UMAX], dec[(i + 1) & 1]);
                         if (KIND != 1 && j >= UX) continue;
+#ifdef GS_STREAM_HALFDOT   // profiling build only: decode every other unit
+                        if (j & 1) continue;
+#endif
                         const int jx = j % UX;
                         if (KIND == 1 && j >= UX)
                             TP::template dot<NV, XNEG>(R[p][j], dec[i & 1], usub[jx], tab, xr[jx], nv, acc1);
@@ -464,8 +497,18 @@ struct StreamPass {
                 }
 #pragma unroll
                 for (int t = 0; t < NV; t++) {
+#ifdef GS_PROBE_NORED   // profiling build only: no cross-lane reduction
+                    res0[p][t] = acc0[t];
+                    res1[p][t] = acc1[t];
+                    if (gather) {
+                        out0 = lane == p * NV + t ? res0[p][t] : out0;
+                        out1 = lane == p * NV + t ? res1[p][t] : out1;
+                    }
+                    if (false) {
+#else
                     res0[p][t] = group_sum(acc0[t], lpr);
                     if (KIND == 1) res1[p][t] = group_sum(acc1[t], lpr);
+#endif
                     if (gather) {
                         const float v0 = __builtin_bit_cast(
                             float, __builtin_amdgcn_ds_bpermute(bsrc, __builtin_bit_cast(int, res0[p][t])));
@@ -476,6 +519,9 @@ struct StreamPass {
                             out1 = lane == p * NV + t ? v1 : out1;
                         }
                     }
+#ifdef GS_PROBE_NORED
+                    }
+#endif
                 }
             }
             if (gather) {
@@ -486,7 +532,7 @@ struct StreamPass {
                         float *dst = y + (int64_t)t * a.y_stride + rr;
                         *dst = a.accumulate ? *dst + out0 : out0;
                     } else if (KIND == 1) {
-                        store_h(&y[((int64_t)ge * nv + t) * rows + rr], swiglu(out0, out1, a.lim));
+                        store_h(&y[((int64_t)ge * nv + t) * rows + rr], swiglu_fast(out0, out1, a.lim));
                     } else {
                         y[(int64_t)t * a.y_stride + rr] += out0;
                     }
@@ -503,7 +549,7 @@ struct StreamPass {
                                     float *dst = y + (int64_t)t * a.y_stride + rr;
                                     *dst = a.accumulate ? *dst + res0[p][t] : res0[p][t];
                                 } else if (KIND == 1) {
-                                    store_h(&y[((int64_t)ge * nv + t) * rows + rr], swiglu(res0[p][t], res1[p][t], a.lim));
+                                    store_h(&y[((int64_t)ge * nv + t) * rows + rr], swiglu_fast(res0[p][t], res1[p][t], a.lim));
                                 } else {
                                     y[(int64_t)t * a.y_stride + rr] += res0[p][t];
                                 }
@@ -516,11 +562,11 @@ struct StreamPass {
     }
 };
 
-template <class F, int KIND, int NV, int UMAX>
+template <class F, int KIND, int NV, int UMAX, int LP = 0>
 __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     extern __shared__ __align__(16) uint8_t smem[];
     GS_TS(0, 0)
-    StreamPass<F, KIND, NV, UMAX> P(a, smem);
+    StreamPass<F, KIND, NV, UMAX, LP> P(a, smem);
     P.issue_x();
     P.issue_tab();
     GS_TS(1, 0)
@@ -556,7 +602,17 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     GS_STREAM_KERNEL(F, NAME, 1, 1, 8) GS_STREAM_KERNEL(F, NAME, 1, 2, 2)                       \
     GS_STREAM_KERNEL(F, NAME, 1, 2, 4) GS_STREAM_KERNEL(F, NAME, 1, 4, 2)                       \
     GS_STREAM_KERNEL(F, NAME, 1, 4, 4) GS_STREAM_KERNEL(F, NAME, 1, 8, 2)
-#define GS_STREAM_ALL(F, NAME) GS_STREAM_MV(F, NAME, 0) GS_STREAM_GU(F, NAME) GS_STREAM_MV(F, NAME, 2)
+// one-token GEMV and gate/up with 64-lane groups fixed at compile time (suffix _w)
+#define GS_STREAM_KERNEL_W(F, NAME, KIND, UM)                                                    \
+    extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE))) \
+        gs_k_stream_##NAME##_##KIND##_1_##UM##_w(StreamArgs a) {                                  \
+        stream_body<F, KIND, 1, UM, 64>(a);                                                     \
+    }
+#define GS_STREAM_W(F, NAME)                                                                    \
+    GS_STREAM_KERNEL_W(F, NAME, 0, 2) GS_STREAM_KERNEL_W(F, NAME, 0, 4)                         \
+    GS_STREAM_KERNEL_W(F, NAME, 0, 6) GS_STREAM_KERNEL_W(F, NAME, 0, 8)                         \
+    GS_STREAM_KERNEL_W(F, NAME, 1, 2) GS_STREAM_KERNEL_W(F, NAME, 1, 4) GS_STREAM_KERNEL_W(F, NAME, 1, 8)
+#define GS_STREAM_ALL(F, NAME) GS_STREAM_MV(F, NAME, 0) GS_STREAM_GU(F, NAME) GS_STREAM_MV(F, NAME, 2) GS_STREAM_W(F, NAME)
 
 // =============================================================================================
 // Fused routed-expert FFN for one decode token: gate/up + SwiGLU for every expert of the batch,
@@ -627,7 +683,7 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
     GS_TS(0, 0)
     const unsigned long long top0 = threadIdx.x == 0 ? barrier_epoch() : 0;
     {
-        StreamPass<F1, 1, 1, UM1> G(fa.gu, smem);
+        StreamPass<F1, 1, 1, UM1, 64> G(fa.gu, smem);   // the host fuses only 64-lane gate/up plans
         G.issue_x();
         G.issue_tab();
         G.load_batch(G.gid);
