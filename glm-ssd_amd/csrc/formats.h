@@ -253,19 +253,20 @@ struct GlobalAt {
 struct BufferAt {
     __amdgpu_buffer_rsrc_t r;
     const uint8_t *b;
-    __device__ __forceinline__ explicit BufferAt(const uint8_t *base)
-        : r(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, -1, 0x00020000)), b(base) {}
-    __device__ __forceinline__ uint32_t u16(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b16(r, o, 0, 0); }
-    __device__ __forceinline__ uint32_t u32(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0); }
+    uint32_t so;   // wave-uniform offset added to every access (the scalar offset operand)
+    __device__ __forceinline__ explicit BufferAt(const uint8_t *base, uint32_t soff = 0)
+        : r(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, -1, 0x00020000)), b(base), so(soff) {}
+    __device__ __forceinline__ uint32_t u16(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b16(r, o, so, 0); }
+    __device__ __forceinline__ uint32_t u32(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b32(r, o, so, 0); }
     __device__ __forceinline__ uint2 u64(uint32_t o) const {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, o, so, 0);
         return make_uint2(v[0], v[1]);
     }
     __device__ __forceinline__ uint4 u128(uint32_t o) const {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, o, so, 0);
         return make_uint4(v[0], v[1], v[2], v[3]);
     }
-    __device__ __forceinline__ const uint8_t *ptr(uint32_t o) const { return b + o; }
+    __device__ __forceinline__ const uint8_t *ptr(uint32_t o) const { return b + so + o; }
 };
 
 // Each format: Raw = the registers one unit needs from memory; load() issues the loads for unit

@@ -234,7 +234,7 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     if ((e = plan_stream(c, kind, ty, a, P)) != hipSuccess) return e;
     const int NVt = a.nvec <= 1 ? 1 : a.nvec <= 2 ? 2 : a.nvec <= 4 ? 4 : 8;
     // one token with 64-lane groups: the variant with the group width fixed at compile time
-    const bool w64 = a.lpr == 64 && NVt == 1 && kind != 2;
+    const bool w64 = a.lpr == 64 && NVt == 1 && (kind != 2 || a.wlo != nullptr);
     const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" +
                              std::to_string(NVt) + "_" + std::to_string(P.um) + (w64 ? "_w" : "");
     hipFunction_t f;
@@ -460,6 +460,14 @@ static int down_args(StreamArgs &a, const GsMoeBatch *b, int e0, int n, int nt, 
     a.y = y;
     a.row_stride = row_stride;
     a.y_stride = rows;
+    // 32-bit addressing for the 64-lane kernels when every expert's rows lie within 4 GiB of the
+    // lowest expert pointer (one buffer resource for all of them); wlo stays null otherwise
+    uintptr_t lo = UINTPTR_MAX, hi = 0;
+    for (int e = 0; e < n; e++) {
+        lo = std::min(lo, (uintptr_t)b->down[e0 + e]);
+        hi = std::max(hi, (uintptr_t)b->down[e0 + e] + (uintptr_t)rows * (uintptr_t)row_stride);
+    }
+    if (n > 0 && hi - lo < (uintptr_t)0xffffffffu) a.wlo = (const uint8_t *)lo;
     a.K = K;
     a.rows = rows;
     a.nvec = nt;
@@ -524,7 +532,7 @@ GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int6
         if ((rc = gateup_args(fa.gu, b, nt, rs_gu, n_embd, n_ff, x, h, lim))) return rc;
         if ((rc = down_args(fa.dn, b, 0, b->n, nt, rs_dn, n_ff, n_embd, h, y))) return rc;
         fuse = plan_stream(c, 1, ty_gu, fa.gu, P1) == hipSuccess && plan_stream(c, 2, ty_dn, fa.dn, P2) == hipSuccess &&
-               fa.gu.lpr == 64;   // the fused kernels fix 64-lane groups for gate/up
+               fa.gu.lpr == 64 && fa.dn.lpr == 64 && fa.dn.wlo;   // what the fused kernels fix
     }
     if (fuse) {
         const std::string name = "gs_k_ffn_" + std::to_string(ty_gu) + "_" + std::to_string(ty_dn) + "_" +

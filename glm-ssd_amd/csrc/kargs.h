@@ -42,6 +42,8 @@ struct StreamArgs {
     int lpr;                         // lanes per row group (16, 32 or 64)
     int upl;                         // units per lane = ceil(segments*nu/lpr)
     int x_aligned;                   // x and x_stride allow 16-byte loads
+    const uint8_t *wlo;              // DOWN, 64-lane kernels: lowest expert pointer; every expert's
+                                     // rows lie within 4 GiB above it (32-bit offsets)
 };
 
 // Fused MoE FFN (gate/up + SwiGLU, grid barrier, down + combine) for one token

@@ -313,8 +313,10 @@ struct StreamPass {
             usub[j] = F::sub(up);
         }
 #pragma unroll
-        for (int j = 0; j < UX; j++)
+        for (int j = 0; j < UX; j++) {
             ubase[j] = KIND == 2 ? (const uint8_t *)lane_u64(tw0, uspan[j]) : (KIND == 1 ? nullptr : wb);
+            if (KIND == 2 && LP == 64) uoff[j] += (uint32_t)(ubase[j] - a.wlo);
+        }
         nxv = KIND == 2 ? a.nseg * nv : nv;
         nxu = nxv * nu;
     }
@@ -344,6 +346,16 @@ struct StreamPass {
         // A 64-lane group covers whole rows, so its row index is wave-uniform: the row address is
         // then scalar arithmetic and every load goes through a buffer resource on that address
         // with a 32-bit lane offset (no per-load 64-bit vector adds).
+        if (KIND == 2 && LP == 64) {   // experts within 4 GiB of a.wlo: lane offsets + row offset
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                const int r = __builtin_amdgcn_readfirstlane(min(base + p * ngroups, last));
+                const BufferAt m(a.wlo, (uint32_t)((int64_t)r * rs));
+#pragma unroll
+                for (int j = 0; j < UX; j++) F::load(m, uoff[j], usub[j], R[p][j]);
+            }
+            return;
+        }
         if (KIND != 2 && LP == 64) {
             const uint8_t *bg = KIND == 1 ? wg : wb0;
 #pragma unroll
@@ -602,7 +614,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     GS_STREAM_KERNEL(F, NAME, 1, 1, 8) GS_STREAM_KERNEL(F, NAME, 1, 2, 2)                       \
     GS_STREAM_KERNEL(F, NAME, 1, 2, 4) GS_STREAM_KERNEL(F, NAME, 1, 4, 2)                       \
     GS_STREAM_KERNEL(F, NAME, 1, 4, 4) GS_STREAM_KERNEL(F, NAME, 1, 8, 2)
-// one-token GEMV and gate/up with 64-lane groups fixed at compile time (suffix _w)
+// one-token GEMV, gate/up and down with 64-lane groups fixed at compile time (suffix _w; for down
+// the host also guarantees a.wlo)
 #define GS_STREAM_KERNEL_W(F, NAME, KIND, UM)                                                    \
     extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE))) \
         gs_k_stream_##NAME##_##KIND##_1_##UM##_w(StreamArgs a) {                                  \
@@ -611,7 +624,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
 #define GS_STREAM_W(F, NAME)                                                                    \
     GS_STREAM_KERNEL_W(F, NAME, 0, 2) GS_STREAM_KERNEL_W(F, NAME, 0, 4)                         \
     GS_STREAM_KERNEL_W(F, NAME, 0, 6) GS_STREAM_KERNEL_W(F, NAME, 0, 8)                         \
-    GS_STREAM_KERNEL_W(F, NAME, 1, 2) GS_STREAM_KERNEL_W(F, NAME, 1, 4) GS_STREAM_KERNEL_W(F, NAME, 1, 8)
+    GS_STREAM_KERNEL_W(F, NAME, 1, 2) GS_STREAM_KERNEL_W(F, NAME, 1, 4) GS_STREAM_KERNEL_W(F, NAME, 1, 8) \
+    GS_STREAM_KERNEL_W(F, NAME, 2, 2) GS_STREAM_KERNEL_W(F, NAME, 2, 4)                         \
+    GS_STREAM_KERNEL_W(F, NAME, 2, 6) GS_STREAM_KERNEL_W(F, NAME, 2, 8)
 #define GS_STREAM_ALL(F, NAME) GS_STREAM_MV(F, NAME, 0) GS_STREAM_GU(F, NAME) GS_STREAM_MV(F, NAME, 2) GS_STREAM_W(F, NAME)
 
 // =============================================================================================
@@ -694,7 +709,7 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
     GS_TS(1, 0)
     __syncthreads();   // waits for this workgroup's h stores
     if (threadIdx.x == 0) grid_arrive();
-    StreamPass<F2, 2, 1, UM2> D(fa.dn, smem);
+    StreamPass<F2, 2, 1, UM2, 64> D(fa.dn, smem);   // the host fuses only 64-lane down plans with wlo
     D.issue_tab();
     D.load_batch(D.gid);   // down weights in flight across the barrier
     GS_TS(2, 0)
