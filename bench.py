@@ -29,7 +29,7 @@ HBM_PEAK_GBPS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0   # dense f16 MFMA (the grouped GEMM's operand type)
 
 
-GATEUP_KERNEL = "gs_k_stream_16_1_1_4"   # the kernel gs_moe_gateup launches for config 2
+GATEUP_KERNEL = "gs_k_stream_16_1_1_4_w"   # the kernel gs_moe_gateup launches for config 2
 
 
 def traffic_bytes(kernel):
@@ -276,7 +276,7 @@ def main():
                                "(hidden 4096, intermediate 1536), gate/up+SwiGLU then down+weighted combine",
                    "weight_bytes_per_step": res["step_bytes"], "frac_hbm_peak": round(value / HBM_PEAK_GBPS, 4),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "gs_moe_gateup (gs_k_stream_16_1_1)",
+        "roofline": {"bound": "hbm", "kernel": "gs_moe_gateup (gs_k_stream_16_1_1_4_w)",
                      "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(GATEUP_KERNEL),
                      "traffic_source": "profiles/stream_kernels_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
