@@ -62,28 +62,37 @@ def bench_lib():
     return L
 
 
-def run_moe_decode(L, s, steps, warmup, n_expert=288, n_embd=4096, n_ff=1536, seed=2):
+def run_moe_decode(L, s, steps, warmup, n_expert=288, n_embd=4096, n_ff=1536, seed=2, ty_dn=None, label="config 2"):
+    """Decode-step FFN over 8 of n_expert resident experts, a new 8 each step (rotation defeats the
+    last-level cache). IQ2_XXS gate/up; down IQ2_XXS (config 2) or ty_dn."""
     import glmssd as G
     from glmssd import synth
     ty = G.GgmlType.IQ2_XXS
+    ty_dn = ty if ty_dn is None else ty_dn
     rng = np.random.default_rng(seed)
-    rbg, rbd = G.row_bytes(ty, n_embd), G.row_bytes(ty, n_ff)
-    mat = n_ff * rbg                       # bytes of one gate (= up = down) matrix
+    rbg, rbd = G.row_bytes(ty, n_embd), G.row_bytes(ty_dn, n_ff)
+    mat = n_ff * rbg                       # bytes of one gate (= up) matrix
+    mat_dn = n_embd * rbd                  # bytes of one down matrix
     gate = G.DeviceBuffer(n_expert * mat)
     up = G.DeviceBuffer(n_expert * mat)
-    down = G.DeviceBuffer(n_expert * mat)
-    log(f"config 2: generating {3 * n_expert * mat / 1e9:.2f} GB of IQ2_XXS experts")
+    down = G.DeviceBuffer(n_expert * mat_dn)
+    log(f"{label}: generating {n_expert * (2 * mat + mat_dn) / 1e9:.2f} GB of experts")
     for e in range(n_expert):
-        g, u, d = synth.iq2_xxs_expert(rng, n_embd, n_ff)
+        if ty_dn == ty:
+            g, u, d = synth.iq2_xxs_expert(rng, n_embd, n_ff)
+        else:
+            g = synth.random_blocks(rng, ty, n_ff * n_embd, 0.02, [0])
+            u = synth.random_blocks(rng, ty, n_ff * n_embd, 0.02, [0])
+            d = synth.random_blocks(rng, ty_dn, n_embd * n_ff, 0.02, [0])
         gate.upload(g, s, e * mat)
         up.upload(u, s, e * mat)
-        down.upload(d, s, e * mat)
+        down.upload(d, s, e * mat_dn)
     x = rng.standard_normal(n_embd).astype(np.float32)
     dx = G.DeviceBuffer.from_array(x, s)
     dh = G.DeviceBuffer(8 * n_ff * 4)
     dy = G.DeviceBuffer(n_embd * 4)
     dy.zero(s)
-    # 36 batches = one pass over a permutation of all 288 experts, 8 distinct per step
+    # n_expert/8 batches = one pass over a permutation of all experts, 8 distinct per step
     perm = rng.permutation(n_expert)
     nb = n_expert // 8
     batches = (G.MoeBatch * nb)()
@@ -95,16 +104,16 @@ def run_moe_decode(L, s, steps, warmup, n_expert=288, n_embd=4096, n_ff=1536, se
             e = int(perm[8 * i + j])
             b.gate[j] = gate.p.value + e * mat
             b.up[j] = up.p.value + e * mat
-            b.down[j] = down.p.value + e * mat
+            b.down[j] = down.p.value + e * mat_dn
             b.w[0][j] = w[j]
     ms, msg = C.c_float(), C.c_float()
-    rc = L.bn_moe_decode(ty, ty, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p, steps,
-                         warmup, s.raw(), C.byref(ms), C.byref(msg))
+    rc = L.bn_moe_decode(ty, ty_dn, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p,
+                         steps, warmup, s.raw(), C.byref(ms), C.byref(msg))
     G.check(rc)
     msf = C.c_float()
-    G.check(L.bn_moe_ffn(ty, ty, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p, steps,
-                         warmup, s.raw(), C.byref(msf)))
-    step_bytes = 8 * 3 * mat
+    G.check(L.bn_moe_ffn(ty, ty_dn, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p,
+                         steps, warmup, s.raw(), C.byref(msf)))
+    step_bytes = 8 * (2 * mat + mat_dn)
     gu_bytes = 8 * 2 * mat
     keep = (gate, up, down, dx, dh, dy, batches)
     layer = dict(gate=gate, up=up, down=down, mat=mat, n_expert=n_expert, n_embd=n_embd, n_ff=n_ff, rbg=rbg, rbd=rbd)
@@ -241,6 +250,17 @@ def main():
             log(f"{name}: {r}")
     del keep, layer
     if not args.no_secondary:
+        # the target model's routed experts: IQ2_XXS gate/up, IQ3_XXS down, n_ff_exp = 2048
+        rr, keep2, _ = run_moe_decode(L, s, args.steps, args.warmup, n_expert=96, n_ff=2048, seed=6,
+                                      ty_dn=G.GgmlType.IQ3_XXS, label="target-model decode FFN")
+        secondary["decode_ffn_iq2xxs_gateup_iq3xxs_down_nff2048"] = {
+            "us_per_step": round(rr["ms_step"] * 1e3, 2), "GB/s": round(rr["step_bytes"] / rr["ms_step"] / 1e6, 1),
+            "us_fused_gs_moe_ffn": round(rr["ms_ffn"] * 1e3, 2), "weight_bytes": rr["step_bytes"],
+            "experts_resident": 96}
+        log(f"target-model decode FFN: {secondary['decode_ffn_iq2xxs_gateup_iq3xxs_down_nff2048']}")
+        del keep2
+        secondary["config2_fused_gs_moe_ffn"] = {"us_per_step": round(res["ms_ffn"] * 1e3, 2),
+                                                 "GB/s": round(res["step_bytes"] / res["ms_ffn"] / 1e6, 1)}
         from glmssd import synth
         r1 = run_gemv(L, s, G.GgmlType.Q8_0, 4096, 4096, synth.q8_0_matrix, args.steps, args.warmup, 1)
         r3a = run_gemv(L, s, G.GgmlType.Q4_K, 12288, 4096, synth.q4_k_matrix, args.steps, args.warmup, 3)

@@ -35,7 +35,10 @@ def stream():
 CASES = [(T.IQ2_XXS, T.IQ2_XXS, 1, 8, 4096, 1536, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 1, 8, 2048, 1536, 0.0),
          (T.Q4_K, T.Q4_K, 1, 5, 2048, 1024, 7.0), (T.Q8_0, T.Q8_0, 1, 3, 1024, 1024, 0.0),
          (T.Q6_K, T.Q6_K, 1, 4, 2048, 512, 3.0), (T.IQ3_XXS, T.IQ3_XXS, 1, 1, 2048, 768, 0.0),
-         (T.IQ2_XXS, T.IQ2_XXS, 2, 6, 2048, 1024, 0.0), (T.Q5_K, T.Q5_K, 1, 2, 1024, 512, 0.0)]
+         (T.IQ2_XXS, T.IQ2_XXS, 2, 6, 2048, 1024, 0.0), (T.Q5_K, T.Q5_K, 1, 2, 1024, 512, 0.0),
+         # the target model's routed experts: IQ2_XXS gate/up, IQ3_XXS down, n_ff_exp = 2048
+         # (validate.rs:376-386), one decode token and a 2-token MTP step
+         (T.IQ2_XXS, T.IQ3_XXS, 1, 8, 4096, 2048, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 2, 8, 4096, 2048, 0.0)]
 
 
 @pytest.mark.parametrize("ty_gu,ty_dn,nt,n,n_embd,n_ff,lim", CASES)
