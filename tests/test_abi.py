@@ -9,11 +9,11 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB = os.path.join(ROOT, "glm-ssd_amd", "libglmssd_hip.so")
-HDR = os.path.join(ROOT, "include", "glmssd.h")
+HDRS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include"))) if h.endswith(".h")]
 
 
-def header_symbols():
-    text = open(HDR).read()
+def header_symbols(only=None):
+    text = "".join(open(h).read() for h in HDRS if only is None or h.endswith(only))
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(gs_\w+)\s*\(", text, re.M)))
 
 
@@ -39,7 +39,10 @@ def test_library_exports_every_declared_symbol():
 
 def test_python_binding_covers_header():
     import glmssd
-    missing = [s for s in header_symbols() if s not in glmssd.SIGNATURES and s != "gs_error_string"]
+    from glmssd import gguf
+    missing = [s for s in header_symbols("glmssd.h") if s not in glmssd.SIGNATURES and s != "gs_error_string"]
+    assert not missing, missing
+    missing = [s for s in header_symbols("glmssd_gguf.h") if s not in gguf._SIGS]
     assert not missing, missing
 
 
