@@ -189,12 +189,16 @@ __device__ __forceinline__ void deq8_bf16(const uint8_t *b, int, float *v) {
 struct XU {
     uint32_t q[8];   // int8 x 32
     uint32_t nq[8];  // -q per byte (only formats with NEG_X read it)
-    float D;         // f16-rounded scale (x the routing weight for MoE down, x the format's XSCALE)
+    float D;         // f16-rounded scale (x the routing weight for MoE down, x the format's XSCALE);
+                     // formats with f32 activations: the routing weight alone
     int slo, shi;    // sum of q over elements 0..15 / 16..31
+    const float *xs; // formats with f32 activations: the unit's 32 floats in LDS
 };
 // Traits defaults: formats opt in to negated activations / a folded constant scale.
 template <class F, class = void> struct NegX { static constexpr bool value = false; };
 template <class F> struct NegX<F, decltype((void)F::NEG_X, void())> { static constexpr bool value = F::NEG_X; };
+template <class F, class = void> struct F32Act { static constexpr bool value = false; };
+template <class F> struct F32Act<F, decltype((void)F::F32X, void())> { static constexpr bool value = F::F32X; };
 template <class F, class = void> struct XScale { static constexpr float value = 1.0f; };
 template <class F> struct XScale<F, decltype((void)F::XSCALE, void())> { static constexpr float value = F::XSCALE; };
 
@@ -558,9 +562,13 @@ struct FIQ3_XXS : UnitGeom<256, 98> {
 
 // Generic path for the remaining types: exact f32 decode of the unit straight from global
 // memory, f32 dot with the dequantized activations (D * q). Slower; used for the non-hot formats.
+//
+// The plain float formats (F32, F16, BF16 — the router and other unquantized matrices) take the
+// activations in f32, as the reference's GEMV does for every type (quants.cu:81-96): F32X.
 template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float *)>
 struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
     static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0, RAW = 2;
+    static constexpr bool F32X = T == GS_F32 || T == GS_F16 || T == GS_BF16;
     struct Raw { const uint8_t *p; };
     template <class M>
     __device__ static __forceinline__ void load(const M &m, uint32_t o, int, Raw &w) { w.p = m.ptr(o); }
@@ -579,8 +587,13 @@ struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
         for (int t = 0; t < NV; t++) {
             if (t < nv) {
                 float s = 0.f;
+                if (F32X) {
 #pragma unroll
-                for (int i = 0; i < 32; i++) s += v[i] * (float)(int8_t)((x[t].q[i >> 2] >> (8 * (i & 3))) & 0xff);
+                    for (int i = 0; i < 32; i++) s += v[i] * x[t].xs[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 32; i++) s += v[i] * (float)(int8_t)((x[t].q[i >> 2] >> (8 * (i & 3))) & 0xff);
+                }
                 r[t] += x[t].D * s;
             }
         }

@@ -206,7 +206,10 @@ hipError_t plan_stream(DeviceCtx *c, int kind, int ty, StreamArgs &a, StreamPlan
     a.lpr = best_lpr;
     a.upl = (tot + best_lpr - 1) / best_lpr;
     const int tab = (table_bytes(ty) + 15) & ~15;
-    P.lds = (size_t)tab + (size_t)(kind == 2 ? a.nseg * a.nvec : a.nvec) * (a.K + a.nu * 8);
+    // staged activations per vector: q8_1 bytes + scale/sum words, or the f32 values themselves
+    // for the float formats (F32, F16, BF16 take f32 activations, like the reference)
+    const bool f32x = ty == GS_F32 || ty == GS_F16 || ty == GS_BF16;
+    P.lds = (size_t)tab + (size_t)(kind == 2 ? a.nseg * a.nvec : a.nvec) * (f32x ? (size_t)a.K * 4 : a.K + a.nu * 8);
     if (P.lds > std::min<size_t>(c->max_lds, 160 * 1024)) return hipErrorInvalidValue;
     P.um = best_um;
     return hipSuccess;

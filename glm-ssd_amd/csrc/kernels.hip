@@ -145,6 +145,10 @@ __device__ __forceinline__ XU load_xu(const uint8_t *xq, const uint32_t *xm, int
     z.q[0] = live ? lo.x : 0u; z.q[1] = live ? lo.y : 0u; z.q[2] = live ? lo.z : 0u; z.q[3] = live ? lo.w : 0u;
     z.q[4] = live ? hi.x : 0u; z.q[5] = live ? hi.y : 0u; z.q[6] = live ? hi.z : 0u; z.q[7] = live ? hi.w : 0u;
     z.D = live ? __builtin_bit_cast(float, dbits) * scale * XScale<F>::value : 0.f;
+    if (F32Act<F>::value) {   // f32 activations: staged as floats, read by the unit's dot
+        z.xs = (const float *)xq + (size_t)v * K + 32 * (live ? up : 0);
+        z.D = live ? scale : 0.f;
+    }
     z.slo = live ? (int)(int16_t)(ss & 0xffff) : 0;
     z.shi = live ? (int)(int16_t)(ss >> 16) : 0;
     if (XNEG) {
@@ -395,6 +399,27 @@ struct StreamPass {
         F::tab_store(tid, treg);
         uint32_t *xm = (uint32_t *)(xq + (size_t)nxv * K);
         const int sub = tid & (XT - 1);
+        if (F32Act<F>::value) {   // f32 activations: the floats themselves
+            auto store_f = [&](int i, const float (&f)[8]) {
+                const int v = udiv_small(i, rnu), u = i - v * nu;
+                float4 *dst = (float4 *)((float *)xq + (size_t)v * K + 32 * u + 8 * sub);
+                dst[0] = make_float4(f[0], f[1], f[2], f[3]);
+                dst[1] = make_float4(f[4], f[5], f[6], f[7]);
+            };
+#pragma unroll
+            for (int k = 0; k < XP; k++)
+                if ((tid / XT) + XPU * k < nxu) store_f((tid / XT) + XPU * k, xf[k]);
+            for (int i0 = XPU * XP; i0 < nxu; i0 += XPU) {
+                const int i = i0 + tid / XT;
+                if (i < nxu) {
+                    const int v = udiv_small(i, rnu), u = i - v * nu;
+                    float f[8];
+                    load8(xsrc(v, u) + 8 * sub, a.x_aligned != 0, f);
+                    store_f(i, f);
+                }
+            }
+            return;
+        }
         auto quant_store = [&](int i, const float (&f)[8]) {
             const int v = udiv_small(i, rnu), u = i - v * nu;
             float amax = 0.f;

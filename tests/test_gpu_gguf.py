@@ -78,7 +78,7 @@ def test_gemv_on_file_tensor(model, ty, stream):
     dw, dx, dy = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(x), G.DeviceBuffer(rows * 4)
     G.ops.gemv(ty, dw, t.row_bytes, k, rows, dx, k, dy, rows, 1, s=stream)
     got = dy.download(np.float32, rows, stream)
-    want = O.gemv(ty, raw, t.row_bytes, k, rows, x)[0]
+    want = O.gemv(ty, raw, t.row_bytes, k, rows, x, act="f32" if ty in (T.F32, T.F16) else "q8_1")[0]
     e = rel_l2(got, want)
     say(f"  {t.name}: rel-L2 {e:.2e}")
     assert e <= REL_L2

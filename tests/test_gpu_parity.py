@@ -14,6 +14,8 @@ pytestmark = pytest.mark.gpu
 REL_L2 = 1e-3
 ALL = [T.F32, T.F16, T.BF16, T.Q8_0, T.Q2_K, T.Q3_K, T.Q4_K, T.Q5_K, T.Q6_K, T.IQ2_XXS, T.IQ2_S, T.IQ3_XXS, T.IQ4_XS]
 HOT = [T.Q8_0, T.Q4_K, T.Q6_K, T.IQ2_XXS]
+FLOAT = (T.F32, T.F16, T.BF16)
+REL_L2_F32 = 1e-5   # f32 activations on both sides: only the summation order differs
 
 
 def say(*a):
@@ -89,7 +91,8 @@ def _gemv_case(ty, rows, K, B, stream, seed, x_stride=None, accumulate=False, ro
     x = np.zeros(B * xs, dtype=np.float32)
     for b in range(B):
         x[b * xs:b * xs + K] = rng.standard_normal(K).astype(np.float32)
-    want = O.gemv(ty, wbytes, rs, K, rows, x, B=B, x_stride=xs)
+    # float matrices take f32 activations (quants.cu:81-96), the quantized formats q8_1 ones
+    want = O.gemv(ty, wbytes, rs, K, rows, x, B=B, x_stride=xs, act="f32" if ty in FLOAT else "q8_1")
     y0 = rng.standard_normal(B * rows).astype(np.float32)
     dw = G.DeviceBuffer.from_array(wbytes)
     dx = G.DeviceBuffer.from_array(x)
@@ -108,7 +111,7 @@ def _gemv_case(ty, rows, K, B, stream, seed, x_stride=None, accumulate=False, ro
 @pytest.mark.parametrize("rows,K", [(101, 4096), (3001, 2048), (257, 1536)])
 def test_gemv_matches_oracle(ty, rows, K, stream):
     for B in (1, 3, 8):
-        assert _gemv_case(ty, rows, K, B, stream, seed=1000 * ty + rows + B) <= REL_L2
+        assert _gemv_case(ty, rows, K, B, stream, seed=1000 * ty + rows + B) <= (REL_L2_F32 if ty in FLOAT else REL_L2)
 
 
 @pytest.mark.parametrize("ty", HOT)
