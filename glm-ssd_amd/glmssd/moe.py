@@ -64,3 +64,142 @@ class ResidentMoeLayer:
         ops.moe_grouped(self.ty_gu, self.ty_down, self.table, self.n_exp, self.d_offs, self.d_idx, self.d_w,
                         self.n_pairs, n_tok, self.rs_gu, self.n_embd, self.n_ff, self.rs_down, x_dev, y_dev, lim,
                         self.work, self.work.nbytes, s)
+
+
+def route(logits, bias, k, weights_norm=True, weights_scale=1.0):
+    """Host routing of forward.rs:964-980 (`Engine::route`): per token, sigmoid scores, the k
+    experts with the largest score + bias (descending), weights score / (sum of the chosen
+    scores + 1e-20) * scale (the sum is 1 without normalisation). logits: [t][n_expert] f32."""
+    logits = np.asarray(logits, dtype=np.float32)
+    bias = np.asarray(bias, dtype=np.float32)
+    out = []
+    for row in logits.reshape(-1, bias.size):
+        scores = (1.0 / (1.0 + np.exp(-row.astype(np.float32)))).astype(np.float32)
+        sel = scores + bias
+        order = sorted(range(bias.size), key=lambda e: -sel[e])[:k]   # stable: ties keep id order
+        wsum = np.float32(sum(scores[e] for e in order)) if weights_norm else np.float32(1.0)
+        out.append([(e, float(scores[e] / (wsum + np.float32(1e-20)) * np.float32(weights_scale))) for e in order])
+    return out
+
+
+class Mat:
+    """A resident weight matrix in GGUF layout: rows of `K` elements of type `ty`."""
+
+    def __init__(self, raw, ty, K, rows, s=None):
+        self.ty, self.K, self.rows = ty, K, rows
+        self.row_bytes = row_bytes(ty, K)
+        self.buf = raw if isinstance(raw, DeviceBuffer) else DeviceBuffer.from_array(np.asarray(raw), s)
+        self.offset = 0
+
+    def ptr(self):
+        return self.buf.ptr(self.offset)
+
+
+class MoeLayer:
+    """One MoE FFN layer with every expert resident: the work of forward.rs:982-1136
+    (`Engine::moe`) without the expert cache. forward(): router logits (F32 GEMV), host routing,
+    shared expert SwiGLU FFN into `out`, routed experts into an accumulator (one token or an MTP
+    pair: gs_moe_ffn over batches of up to 16 experts; more tokens: the grouped MFMA kernel when
+    every expert matrix is IQ2_XXS, else per-expert gather / GEMM / SwiGLU / scatter-add as
+    run_expert_rows), then out += accumulator.
+
+    experts: list of (gate, up, down) host byte arrays; gate/up [n_ff rows x n_embd], down
+    [n_embd rows x n_ff]."""
+    MOE_MAX, MOE_NT = 16, 2
+
+    def __init__(self, router, bias, shared, experts, n_embd, n_ff, ty_gu, ty_down, k=8, weights_norm=True,
+                 weights_scale=1.0, clamp_exp=0.0, clamp_shexp=0.0, router_ty=T.F32, shared_ty=(T.Q6_K,) * 3,
+                 n_ff_shexp=None, s=None):
+        from . import MoeBatch   # noqa: F401  (layout shared with the C ABI)
+        self.n_embd, self.n_ff, self.k = n_embd, n_ff, k
+        self.n_exp = len(experts)
+        self.bias = np.asarray(bias, dtype=np.float32)
+        self.norm, self.scale, self.lim, self.lim_sh = weights_norm, weights_scale, clamp_exp, clamp_shexp
+        self.ty_gu, self.ty_down = ty_gu, ty_down
+        self.router = Mat(router, router_ty, n_embd, self.n_exp, s)
+        nsh = n_ff if n_ff_shexp is None else n_ff_shexp
+        self.sh = [Mat(shared[0], shared_ty[0], n_embd, nsh, s), Mat(shared[1], shared_ty[1], n_embd, nsh, s),
+                   Mat(shared[2], shared_ty[2], nsh, n_embd, s)]
+        self.n_ff_sh = nsh
+        self.gate = [Mat(e[0], ty_gu, n_embd, n_ff, s) for e in experts]
+        self.up = [Mat(e[1], ty_gu, n_embd, n_ff, s) for e in experts]
+        self.down = [Mat(e[2], ty_down, n_ff, n_embd, s) for e in experts]
+        self.grouped = None
+        if ty_gu == T.IQ2_XXS and ty_down == T.IQ2_XXS:
+            self.grouped = ResidentMoeLayer([e[0] for e in experts], [e[1] for e in experts],
+                                            [e[2] for e in experts], n_embd, n_ff, ty_gu, ty_down)
+        self._scratch = {}
+        self.last_routes = None
+
+    def _buf(self, name, nbytes):
+        b = self._scratch.get(name)
+        if b is None or b.nbytes < nbytes:
+            b = self._scratch[name] = DeviceBuffer(max(nbytes, 4))
+        return b
+
+    def _mm(self, m, x, y, t, s, x_stride=None, y_stride=None):
+        """forward.rs:700-710 mm_s: GEMV for up to 8 vectors, else GEMM"""
+        xs = m.K if x_stride is None else x_stride
+        ys = m.rows if y_stride is None else y_stride
+        if t <= 8:
+            ops.gemv(m.ty, m.ptr(), m.row_bytes, m.K, m.rows, x, xs, y, ys, t, False, s)
+        else:
+            ops.gemm(m.ty, m.ptr(), m.row_bytes, m.K, m.rows, x, xs, y, ys, t, False, 1, 0, 0, 0, s)
+
+    def forward(self, xn, out, t, s=None):
+        """xn: device [t][n_embd] (normalised hidden states); out: device [t][n_embd], overwritten
+        with shared-expert FFN + routed-expert FFN. Returns the routes."""
+        from . import MoeBatch
+        n, ne = self.n_embd, self.n_exp
+        logits_d = self._buf("logits", t * ne * 4)
+        self._mm(self.router, xn, logits_d, t, s)
+        logits = logits_d.download(np.float32, t * ne, s)
+        routes = route(logits.reshape(t, ne), self.bias, self.k, self.norm, self.scale)
+        self.last_routes = routes
+        # shared expert (forward.rs:1108-1110, swiglu_ffn :915-921)
+        g, u = self._buf("sh_g", t * self.n_ff_sh * 4), self._buf("sh_u", t * self.n_ff_sh * 4)
+        self._mm(self.sh[0], xn, g, t, s)
+        self._mm(self.sh[1], xn, u, t, s)
+        ops.swiglu(g, u, g, t * self.n_ff_sh, self.lim_sh, s)
+        self._mm(self.sh[2], g, out, t, s)
+        acc = self._buf("acc", t * n * 4)
+        acc.zero(s)
+        groups = [[] for _ in range(ne)]
+        for ti, r in enumerate(routes):
+            for e, w in r:
+                groups[e].append((ti, w))
+        used = [e for e in range(ne) if groups[e]]
+        if t <= self.MOE_NT:
+            # decode / MTP pair: batches of up to 16 experts through the fused FFN
+            h = self._buf("h", self.MOE_MAX * t * self.n_ff * 4)
+            for b0 in range(0, len(used), self.MOE_MAX):
+                chunk = used[b0:b0 + self.MOE_MAX]
+                b = MoeBatch()
+                b.n = len(chunk)
+                for i, e in enumerate(chunk):
+                    b.gate[i], b.up[i], b.down[i] = self.gate[e].ptr().value, self.up[e].ptr().value, self.down[e].ptr().value
+                    for ti, w in groups[e]:
+                        b.w[ti][i] = w
+                ops.moe_ffn(self.ty_gu, self.ty_down, b, t, self.gate[0].row_bytes, n, self.n_ff,
+                            self.down[0].row_bytes, xn, h, acc, self.lim, s)
+        elif self.grouped is not None:
+            self.grouped.upload_routes(routes, s)
+            self.grouped.forward(xn, acc, t, self.lim, s)
+        else:
+            # run_expert_rows (forward.rs:1399-1413) per used expert
+            offs, idx, w, _ = group_pairs(routes, ne)
+            d_idx, d_w = DeviceBuffer.from_array(idx, s), DeviceBuffer.from_array(w, s)
+            m_max = max(len(groups[e]) for e in used)
+            xg = self._buf("xg", m_max * n * 4)
+            eg, eu = self._buf("eg", m_max * self.n_ff * 4), self._buf("eu", m_max * self.n_ff * 4)
+            ey = self._buf("ey", m_max * n * 4)
+            for e in used:
+                m, o = len(groups[e]), int(offs[e])
+                ops.gather_rows(xn, d_idx.ptr(4 * o), xg, m, n, s)
+                self._mm(self.gate[e], xg, eg, m, s)
+                self._mm(self.up[e], xg, eu, m, s)
+                ops.swiglu(eg, eu, eg, m * self.n_ff, self.lim, s)
+                self._mm(self.down[e], eg, ey, m, s)
+                ops.scatter_add_rows(acc, d_idx.ptr(4 * o), d_w.ptr(4 * o), ey, m, n, s)
+        ops.axpy(out, acc, 1.0, t * n, s)
+        return routes

@@ -1,0 +1,81 @@
+"""GPU parity of a whole MoE FFN layer (glmssd.moe.MoeLayer, the work of forward.rs:982-1136 with
+every expert resident): router GEMV (F32, f32 activations), host routing, shared-expert SwiGLU
+FFN (Q6_K), routed experts (the target model's IQ2_XXS gate/up + IQ3_XXS down) through the fused
+FFN for one token and an MTP pair and per-expert gather/GEMM/scatter for more tokens, or the
+grouped MFMA kernel for an all-IQ2_XXS layer. The oracle restates the same composition on the
+CPU; the routes must agree exactly and the output within rel-L2 1e-3."""
+import sys
+
+import numpy as np
+import pytest
+
+import glmssd as G
+from glmssd import GgmlType as T
+from glmssd.moe import MoeLayer, route
+from glmssd import synth
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+REL_L2 = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def _swiglu(g, u, lim):
+    if lim > 0:
+        g, u = np.minimum(g, lim), np.clip(u, -lim, lim)
+    return g / (1.0 + np.exp(-g)) * u
+
+
+@pytest.mark.parametrize("t,ty_dn", [(1, T.IQ3_XXS), (2, T.IQ3_XXS), (5, T.IQ3_XXS), (5, T.IQ2_XXS)])
+def test_moe_layer(t, ty_dn):
+    n_embd, n_ff, n_sh, ne, k = 2048, 512, 1024, 32, 8
+    lim_e, lim_s = 7.0, 0.0
+    nrng = np.random.default_rng(t * 10 + ty_dn)
+    # weight scales of a trained layer's order (|N(0,0.01)| Q6_K, |N(0,0.02)| IQ), so activations
+    # stay finite through the unclamped shared expert
+    router = (nrng.standard_normal((ne, n_embd)) * 0.05).astype(np.float32)
+    bias = (nrng.standard_normal(ne) * 0.1).astype(np.float32)
+    shared = [synth.q6_k_matrix(nrng, n_sh, n_embd), synth.q6_k_matrix(nrng, n_sh, n_embd),
+              synth.q6_k_matrix(nrng, n_embd, n_sh)]
+    experts = [(synth.random_blocks(nrng, T.IQ2_XXS, n_ff * n_embd, 0.02, [0]),
+                synth.random_blocks(nrng, T.IQ2_XXS, n_ff * n_embd, 0.02, [0]),
+                synth.random_blocks(nrng, ty_dn, n_embd * n_ff, 0.02, [0])) for _ in range(ne)]
+    s = G.Stream()
+    layer = MoeLayer(router.view(np.uint8).reshape(-1), bias, shared, experts, n_embd, n_ff, T.IQ2_XXS, ty_dn, k=k,
+                     weights_norm=True, weights_scale=2.5, clamp_exp=lim_e, clamp_shexp=lim_s, n_ff_shexp=n_sh, s=s)
+    x = nrng.standard_normal((t, n_embd)).astype(np.float32)
+    dx, dout = G.DeviceBuffer.from_array(x, s), G.DeviceBuffer(t * n_embd * 4)
+    routes = layer.forward(dx, dout, t, s)
+    got = dout.download(np.float32, t * n_embd, s).reshape(t, n_embd)
+
+    # oracle: the same composition on the CPU
+    logits = O.gemv(T.F32, router.view(np.uint8).reshape(-1), n_embd * 4, n_embd, ne, x, B=t, act="f32")
+    want_routes = route(logits.astype(np.float32), bias, k, True, 2.5)
+    assert [[e for e, _ in r] for r in routes] == [[e for e, _ in r] for r in want_routes]
+    rb_sh = G.row_bytes(T.Q6_K, n_embd)
+    g = O.gemv(T.Q6_K, shared[0], rb_sh, n_embd, n_sh, x, B=t)
+    u = O.gemv(T.Q6_K, shared[1], rb_sh, n_embd, n_sh, x, B=t)
+    h = _swiglu(g, u, lim_s).astype(np.float32)
+    sh = O.gemv(T.Q6_K, shared[2], G.row_bytes(T.Q6_K, n_sh), n_sh, n_embd, h, B=t)
+    pt, pe, pw = [], [], []
+    for ti, r in enumerate(want_routes):
+        for e, w in r:
+            pt.append(ti); pe.append(e); pw.append(w)
+    act = "f16" if (t > 2 and ty_dn == T.IQ2_XXS) else "q8_1"   # grouped MFMA path: the GEMM semantics
+    routed = O.moe_ffn(T.IQ2_XXS, ty_dn, [e[0] for e in experts], [e[1] for e in experts],
+                       [e[2] for e in experts], G.row_bytes(T.IQ2_XXS, n_embd), G.row_bytes(ty_dn, n_ff), n_embd,
+                       n_ff, x, pt, pe, pw, lim=lim_e, nthreads=8, act=act)
+    want = sh + routed
+    acc = layer._scratch["acc"].download(np.float32, t * n_embd, s).reshape(t, n_embd)   # routed part alone
+    e, er, es = rel_l2(got, want), rel_l2(acc, routed), rel_l2(got - acc, sh)
+    say(f"  MoE layer t={t} down={G.TYPE_NAMES[ty_dn]}: rel-L2 {e:.2e}; routed {er:.2e}; shared {es:.2e}")
+    assert e <= REL_L2 and er <= REL_L2 and es <= REL_L2
