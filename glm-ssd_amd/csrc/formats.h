@@ -470,6 +470,15 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
         w.d = m.u16(o);
         w.a = m.u64(o + 2 + 8 * (uint32_t)j);
     }
+    // units j, j+1 of one block (j even): one scale read, one 16-byte read
+    static constexpr bool PAIR = true;
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int j, Raw &w0, Raw &w1) {
+        w0.d = w1.d = m.u16(o);
+        const uint4 a = m.u128(o + 2 + 8 * (uint32_t)j);
+        w0.a = make_uint2(a.x, a.y);
+        w1.a = make_uint2(a.z, a.w);
+    }
     // XNEG: the activation units carry -q (signs applied on the activation side, 2 ops per 8
     // elements); otherwise the signs are applied to the grid bytes (one more op per 4 elements,
     // 8 fewer registers per activation unit).
@@ -534,6 +543,17 @@ struct FIQ3_XXS : UnitGeom<256, 98> {
         w.d = m.u16(o);
         w.a = m.u64(o + 2 + 8 * (uint32_t)j);
         w.s = m.u32(o + 66 + 4 * (uint32_t)j);
+    }
+    static constexpr bool PAIR = true;
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int j, Raw &w0, Raw &w1) {
+        w0.d = w1.d = m.u16(o);
+        const uint4 a = m.u128(o + 2 + 8 * (uint32_t)j);
+        const uint2 sg = m.u64(o + 66 + 4 * (uint32_t)j);
+        w0.a = make_uint2(a.x, a.y);
+        w1.a = make_uint2(a.z, a.w);
+        w0.s = sg.x;
+        w1.s = sg.y;
     }
     struct Dec { uint2 g[4], s[4]; };
     __device__ static __forceinline__ void fetch(const Raw &w, Dec &e) {

@@ -217,6 +217,11 @@ __device__ __forceinline__ void store_h(float *p, float v) {
 // integer, and the two roundings move it by at most 3 * 2^-24 * (u + 0.5) / d, less than that.
 __device__ __forceinline__ int udiv_small(int u, float rd) { return (int)(((float)u + 0.5f) * rd); }
 
+// Formats that load two consecutive units of a block with one wide access (load2): d once and
+// one 16-byte read for both units' indices, half the vector-memory instructions of two loads.
+template <class F, class = void> struct Paired { static constexpr bool value = false; };
+template <class F> struct Paired<F, decltype((void)F::PAIR, void())> { static constexpr bool value = F::PAIR; };
+
 // LP: 0 = lane-group width from the arguments; 64 = fixed 64 (whole rows per wave, so the row
 // index and every row address are wave-uniform scalars)
 template <class F, int KIND, int NV, int UMAX, int LP = 0>
@@ -228,6 +233,11 @@ struct StreamPass {
     // units in flight before the weight loads (a decode-sized x is one pass: 2 loads per thread)
     static constexpr int XT = 4, XPU = GS_WG / XT;
     static constexpr int XP = KIND == 2 ? 4 : (NV < 4 ? NV : 4);
+    // paired units: the lane's units j, j+1 (j even) are consecutive units of one block
+    static constexpr bool PAIRS = Paired<F>::value && UX % 2 == 0;
+    __device__ __forceinline__ int unit_of(int j) const {
+        return PAIRS ? 2 * (lane + lpr * (j >> 1)) + (j & 1) : lane + lpr * j;
+    }
     static_assert(KIND != 1 || UMAX % 2 == 0, "gate/up needs an even unit count");
 
     const StreamArgs &a;
@@ -306,9 +316,9 @@ struct StreamPass {
         // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
 #pragma unroll
         for (int j = 0; j < UX; j++) {
-            const int u0 = lane + lpr * j;
-            const bool valid = j < a.upl && u0 < tot;
-            const int u = valid ? u0 : (lane < tot ? lane : 0);
+            const int u0 = unit_of(j);
+            const bool valid = (PAIRS || j < a.upl) && u0 < tot;
+            const int u = valid ? u0 : (unit_of(0) < tot ? unit_of(0) : 0);
             const int s = KIND == 2 ? udiv_small(u, rnu) : 0;
             const int up = u - s * nu;
             uval[j] = valid;
@@ -343,6 +353,17 @@ struct StreamPass {
     }
     __device__ __forceinline__ void issue_tab() { F::tab_load(tid, treg); }
 
+    // unit j of the row through accessor m into Rp[base + j]; paired formats load units j and
+    // j+1 together at the even j and skip the odd one (its registers are already filled)
+    template <class M>
+    __device__ __forceinline__ void load_unit(const M &m, int j, typename F::Raw (&Rp)[UMAX], int base) {
+        if constexpr (PAIRS) {
+            if ((j & 1) == 0) F::load2(m, uoff[j], usub[j], Rp[base + j], Rp[base + j + 1]);
+        } else {
+            F::load(m, uoff[j], usub[j], Rp[base + j]);
+        }
+    }
+
     // weight batch of PF rows per lane group from row `base` (rows past the end are clamped to a
     // valid row; their results are dropped)
     __device__ __forceinline__ void load_batch(int base) {
@@ -356,7 +377,7 @@ struct StreamPass {
                 const int r = __builtin_amdgcn_readfirstlane(min(base + p * ngroups, last));
                 const BufferAt m(a.wlo, (uint32_t)((int64_t)r * rs));
 #pragma unroll
-                for (int j = 0; j < UX; j++) F::load(m, uoff[j], usub[j], R[p][j]);
+                for (int j = 0; j < UX; j++) load_unit(m, j, R[p], 0);
             }
             return;
         }
@@ -369,8 +390,8 @@ struct StreamPass {
                 const BufferAt mu(KIND == 1 ? wu + (int64_t)r * rs : bg);
 #pragma unroll
                 for (int j = 0; j < UX; j++) {
-                    F::load(mg, uoff[j], usub[j], R[p][j]);
-                    if (KIND == 1) F::load(mu, uoff[j], usub[j], R[p][UX + j]);
+                    load_unit(mg, j, R[p], 0);
+                    if (KIND == 1) load_unit(mu, j, R[p], UX);
                 }
             }
             return;
@@ -382,12 +403,12 @@ struct StreamPass {
             if (KIND == 1) {
 #pragma unroll
                 for (int j = 0; j < UX; j++) {
-                    F::load(GlobalAt{wg + roff}, uoff[j], usub[j], R[p][j]);
-                    F::load(GlobalAt{wu + roff}, uoff[j], usub[j], R[p][UX + j]);
+                    load_unit(GlobalAt{wg + roff}, j, R[p], 0);
+                    load_unit(GlobalAt{wu + roff}, j, R[p], UX);
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < UX; j++) F::load(GlobalAt{ubase[j] + roff}, uoff[j], usub[j], R[p][j]);
+                for (int j = 0; j < UX; j++) load_unit(GlobalAt{ubase[j] + roff}, j, R[p], 0);
             }
         }
     }
@@ -471,7 +492,7 @@ struct StreamPass {
         XU xr[UX][NV];
 #pragma unroll
         for (int j = 0; j < UX; j++) {
-            const int up = lane + lpr * j - uspan[j] * nu;
+            const int up = unit_of(j) - uspan[j] * nu;
 #pragma unroll
             for (int t = 0; t < NV; t++) {
                 const int v = KIND == 2 ? uspan[j] * nv + t : t;
