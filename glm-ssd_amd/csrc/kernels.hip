@@ -120,14 +120,19 @@ __device__ __forceinline__ float swiglu_fast(float g, float u, float lim) {
 //   kind 1 GATEUP:  units of gate_e[r] then up_e[r] (two sums, SwiGLU epilogue)
 //   kind 2 DOWN:    units of down_e[r] for every expert e of the batch (one weighted sum)
 // =============================================================================================
-// Rows in flight per lane group: as many as ~64 VGPRs of raw weight bytes hold (at most 8), so a
-// group's whole share of a decode-sized matrix is requested before the first row is decoded.
+// Rows in flight per lane group: as many as GS_PF_REGS VGPRs of raw weight bytes hold (1..8).
+// Gate/up rows carry twice the units (gate and up), so their budget is smaller: a smaller first
+// batch arrives sooner and the decode starts earlier (measured on the decode shapes: 2 rows per
+// batch beat 4 by ~1 us of 12), while the down and GEMV passes keep deeper batches.
 #ifndef GS_PF_REGS
 #define GS_PF_REGS 48
 #endif
-template <class F, int UMAX>
+#ifndef GS_PF_REGS_GU
+#define GS_PF_REGS_GU 24
+#endif
+template <class F, int UMAX, int KIND = 0>
 __device__ __forceinline__ constexpr int pf_depth() {
-    constexpr int n = GS_PF_REGS / (F::RAW * UMAX);
+    constexpr int n = (KIND == 1 ? GS_PF_REGS_GU : GS_PF_REGS) / (F::RAW * UMAX);
     return n < 1 ? 1 : (n > 8 ? 8 : n);
 }
 
@@ -226,7 +231,7 @@ template <class F> struct Paired<F, decltype((void)F::PAIR, void())> { static co
 // index and every row address are wave-uniform scalars)
 template <class F, int KIND, int NV, int UMAX, int LP = 0>
 struct StreamPass {
-    static constexpr int PF = pf_depth<F, UMAX>();
+    static constexpr int PF = pf_depth<F, UMAX, KIND>();
     static constexpr int UX = KIND == 1 ? UMAX / 2 : UMAX;       // activation units per lane
     static constexpr bool XNEG = NegX<F>::value && UX * NV <= 4;  // -q in registers only while it is cheap
     // activation prologue: 4 threads per 32-element unit (8 floats each), XP passes of GS_WG/4
