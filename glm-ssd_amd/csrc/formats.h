@@ -258,8 +258,10 @@ struct BufferAt {
     __amdgpu_buffer_rsrc_t r;
     const uint8_t *b;
     uint32_t so;   // wave-uniform offset added to every access (the scalar offset operand)
-    __device__ __forceinline__ explicit BufferAt(const uint8_t *base, uint32_t soff = 0)
-        : r(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, -1, 0x00020000)), b(base), so(soff) {}
+    // nrec: the resource's size in bytes; 0 makes every access out of range, so a load is
+    // issued (and counted) but reads no memory and returns zeros
+    __device__ __forceinline__ explicit BufferAt(const uint8_t *base, uint32_t soff = 0, uint32_t nrec = 0xffffffffu)
+        : r(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)nrec, 0x00020000)), b(base), so(soff) {}
     __device__ __forceinline__ uint32_t u16(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b16(r, o, so, 0); }
     __device__ __forceinline__ uint32_t u32(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b32(r, o, so, 0); }
     __device__ __forceinline__ uint2 u64(uint32_t o) const {
@@ -487,11 +489,19 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
     struct Dec { uint2 g[4], s[4]; };
     __device__ static __forceinline__ void fetch(const Raw &w, Dec &e) {
         const uint32_t gofs[4] = {grid_off<0>(w.a.x), grid_off<1>(w.a.x), grid_off<2>(w.a.x), grid_off<3>(w.a.x)};
+        const uint32_t sofs[4] = {sel_off<0>(w.a.y), sel_off<1>(w.a.y), sel_off<2>(w.a.y), sel_off<3>(w.a.y)};
+#ifdef GS_PROBE_NOLDS   // profiling build only: table words replaced by their offsets (wrong results)
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            e.g[l] = make_uint2(gofs[l], gofs[l] ^ 0x01010101u);
+            e.s[l] = make_uint2(sofs[l], sofs[l] ^ 0x02020202u);
+        }
+        return;
+#endif
 #pragma unroll
         for (int l = 0; l < 4; l++) {
             e.g[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_grid_lds + gofs[l]);
         }
-        const uint32_t sofs[4] = {sel_off<0>(w.a.y), sel_off<1>(w.a.y), sel_off<2>(w.a.y), sel_off<3>(w.a.y)};
 #pragma unroll
         for (int l = 0; l < 4; l++) e.s[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_sel_lds + sofs[l]);
     }

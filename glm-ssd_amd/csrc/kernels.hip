@@ -73,6 +73,25 @@ __device__ __forceinline__ float quad_swap(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// q8_1 quantizer arithmetic in fewer operations, bit-identical to the IEEE forms (checked for
+// every input of the ranges below by tests/arith/q8_arith_check.c):
+//   amax / 127: product with RN(1/127) and one fma correction of its residual (Markstein), for
+//     finite amax >= 2^-118 (a normal quotient); other values take the IEEE division;
+//   roundf(v) (half away from zero) as a truncating conversion of v + copysign(0.49999997, v),
+//     for |v| <= 2^23 (the quantizer's |v| <= 127.x).
+__device__ __forceinline__ float q8_div127(float amax) {
+    if (__builtin_expect(!(amax >= 0x1p-118f && amax <= 0x1.fffffep127f), 0)) return amax / 127.0f;
+    const float c = 1.0f / 127.0f;
+    const float q = amax * c;
+    return __builtin_fmaf(__builtin_fmaf(-q, 127.0f, amax), c, q);
+}
+// roundf(x * id) with the product rounded first (no fma contraction, as the check assumes)
+__device__ __forceinline__ int q8_round_mul(float x, float id) {
+#pragma clang fp contract(off)
+    const float v = x * id;
+    return (int)(v + __builtin_copysignf(0.49999997f, v));
+}
+
 // =============================================================================================
 // Cross-lane sum over groups of 16/32/64 lanes with DPP; the group's last lane ends with the total.
 // =============================================================================================
@@ -227,13 +246,25 @@ __device__ __forceinline__ int udiv_small(int u, float rd) { return (int)(((floa
 template <class F, class = void> struct Paired { static constexpr bool value = false; };
 template <class F> struct Paired<F, decltype((void)F::PAIR, void())> { static constexpr bool value = F::PAIR; };
 
+#ifndef GS_RING_SB
+#define GS_RING_SB __builtin_amdgcn_sched_barrier(0);
+#endif
+template <bool B> struct BoolC { static constexpr bool value = B; };
+
 // LP: 0 = lane-group width from the arguments; 64 = fixed 64 (whole rows per wave, so the row
 // index and every row address are wave-uniform scalars)
 template <class F, int KIND, int NV, int UMAX, int LP = 0>
 struct StreamPass {
     static constexpr int PF = pf_depth<F, UMAX, KIND>();
+#ifndef GS_RING_MIN_PF
+#define GS_RING_MIN_PF 2
+#endif
+    static constexpr bool RING = LP == 64 && PF >= GS_RING_MIN_PF;
     static constexpr int UX = KIND == 1 ? UMAX / 2 : UMAX;       // activation units per lane
-    static constexpr bool XNEG = NegX<F>::value && UX * NV <= 4;  // -q in registers only while it is cheap
+#ifndef GS_XNEG_MAX
+#define GS_XNEG_MAX 4
+#endif
+    static constexpr bool XNEG = NegX<F>::value && UX * NV <= GS_XNEG_MAX;  // -q in registers only while it is cheap
     // activation prologue: 4 threads per 32-element unit (8 floats each), XP passes of GS_WG/4
     // units in flight before the weight loads (a decode-sized x is one pass: 2 loads per thread)
     static constexpr int XT = 4, XPU = GS_WG / XT;
@@ -261,6 +292,7 @@ struct StreamPass {
     float xf[XP][8];
     typename F::TabReg treg;
     typename F::Raw R[PF][UMAX];
+    float wtl[NV];   // DOWN: lane i holds vector t's combine weight for expert i
 
     // geometry of this pass; issues no memory access except the pointer-table load (DOWN/GATEUP)
     __device__ __forceinline__ StreamPass(const StreamArgs &a_, uint8_t *smem) : a(a_) {
@@ -305,6 +337,10 @@ struct StreamPass {
         const int L64 = tid & 63;
         const uint64_t tw0 = KIND != 0 && L64 < GS_SEG_MAX ? (uint64_t)a.w0[L64] : 0;
         const uint64_t tw1 = KIND == 1 && L64 < GS_SEG_MAX ? (uint64_t)a.w1[L64] : 0;
+        // combine weights likewise (lane i <- expert i), requested before the weight loads so the
+        // activation setup does not wait for them
+#pragma unroll
+        for (int t = 0; t < NV; t++) wtl[t] = KIND == 2 && L64 < GS_SEG_MAX && t < nv ? a.wt[t][L64] : 0.f;
         auto lane_u64 = [](uint64_t v, int src) -> uint64_t {   // v of lane `src` (per-lane src)
             const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v);
             const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)(v >> 32));
@@ -369,53 +405,50 @@ struct StreamPass {
         }
     }
 
-    // weight batch of PF rows per lane group from row `base` (rows past the end are clamped to a
-    // valid row; their results are dropped)
-    __device__ __forceinline__ void load_batch(int base) {
+    // one row per lane group into slot p. Rows past the end are clamped to a valid row and their
+    // results dropped; with 64-lane groups their loads go through an empty buffer resource
+    // instead (issued, so wait counts stay exact, but no memory is read).
+    __device__ __forceinline__ void load_row(int p, int row) {
         const int last = nrow > 0 ? nrow - 1 : 0;
+        const uint32_t nrec = __builtin_amdgcn_readfirstlane(row < nrow ? 0xffffffffu : 0u);   // SGPR
         // A 64-lane group covers whole rows, so its row index is wave-uniform: the row address is
         // then scalar arithmetic and every load goes through a buffer resource on that address
         // with a 32-bit lane offset (no per-load 64-bit vector adds).
         if (KIND == 2 && LP == 64) {   // experts within 4 GiB of a.wlo: lane offsets + row offset
+            const int r = __builtin_amdgcn_readfirstlane(min(row, last));
+            const BufferAt m(a.wlo, (uint32_t)((int64_t)r * rs), nrec);
 #pragma unroll
-            for (int p = 0; p < PF; p++) {
-                const int r = __builtin_amdgcn_readfirstlane(min(base + p * ngroups, last));
-                const BufferAt m(a.wlo, (uint32_t)((int64_t)r * rs));
-#pragma unroll
-                for (int j = 0; j < UX; j++) load_unit(m, j, R[p], 0);
-            }
+            for (int j = 0; j < UX; j++) load_unit(m, j, R[p], 0);
             return;
         }
         if (KIND != 2 && LP == 64) {
             const uint8_t *bg = KIND == 1 ? wg : wb0;
+            const int r = __builtin_amdgcn_readfirstlane(min(row, last));
+            const BufferAt mg(bg + (int64_t)r * rs, 0, nrec);
+            const BufferAt mu(KIND == 1 ? wu + (int64_t)r * rs : bg, 0, nrec);
 #pragma unroll
-            for (int p = 0; p < PF; p++) {
-                const int r = __builtin_amdgcn_readfirstlane(min(base + p * ngroups, last));
-                const BufferAt mg(bg + (int64_t)r * rs);
-                const BufferAt mu(KIND == 1 ? wu + (int64_t)r * rs : bg);
-#pragma unroll
-                for (int j = 0; j < UX; j++) {
-                    load_unit(mg, j, R[p], 0);
-                    if (KIND == 1) load_unit(mu, j, R[p], UX);
-                }
+            for (int j = 0; j < UX; j++) {
+                load_unit(mg, j, R[p], 0);
+                if (KIND == 1) load_unit(mu, j, R[p], UX);
             }
             return;
         }
+        const int64_t roff = (int64_t)min(row, last) * rs;
+        if (KIND == 1) {
 #pragma unroll
-        for (int p = 0; p < PF; p++) {
-            const int r = min(base + p * ngroups, last);
-            const int64_t roff = (int64_t)r * rs;
-            if (KIND == 1) {
-#pragma unroll
-                for (int j = 0; j < UX; j++) {
-                    load_unit(GlobalAt{wg + roff}, j, R[p], 0);
-                    load_unit(GlobalAt{wu + roff}, j, R[p], UX);
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < UX; j++) load_unit(GlobalAt{ubase[j] + roff}, j, R[p], 0);
+            for (int j = 0; j < UX; j++) {
+                load_unit(GlobalAt{wg + roff}, j, R[p], 0);
+                load_unit(GlobalAt{wu + roff}, j, R[p], UX);
             }
+        } else {
+#pragma unroll
+            for (int j = 0; j < UX; j++) load_unit(GlobalAt{ubase[j] + roff}, j, R[p], 0);
         }
+    }
+    // the first PF rows of the lane group (later rows are requested by run_rows as slots free up)
+    __device__ __forceinline__ void load_batch(int base) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) load_row(p, base + p * ngroups);
     }
 
     // tables + q8_1 quantization of every activation vector into LDS (the caller then syncs).
@@ -451,23 +484,23 @@ struct StreamPass {
             float amax = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(f[e]));
-            amax = fmaxf(amax, quad_swap<0xB1>(amax));   // quad_perm [1,0,3,2]
-            amax = fmaxf(amax, quad_swap<0x4E>(amax));   // quad_perm [2,3,0,1]
-            const float d = amax / 127.0f;
+            // quad max on the bit patterns (non-negative floats order as unsigned integers)
+            uint32_t ab = __builtin_bit_cast(uint32_t, amax);
+            ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0xB1>(__builtin_bit_cast(float, ab))));   // [1,0,3,2]
+            ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0x4E>(__builtin_bit_cast(float, ab))));   // [2,3,0,1]
+            amax = __builtin_bit_cast(float, ab);
+            const float d = q8_div127(amax);
             const float id = d != 0.f ? 1.0f / d : 0.f;
             uint32_t w[2];
-            int sum = 0;
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                uint32_t word = 0;
+                int q[4];
 #pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const int q = (int)__builtin_roundf(f[4 * h + b] * id);
-                    word |= ((uint32_t)q & 0xffu) << (8 * b);
-                    sum += q;
-                }
-                w[h] = word;
+                for (int b = 0; b < 4; b++) q[b] = q8_round_mul(f[4 * h + b], id);
+                w[h] = __builtin_amdgcn_perm((uint32_t)q[1], (uint32_t)q[0], 0x0c0c0400u) |
+                       __builtin_amdgcn_perm((uint32_t)q[3], (uint32_t)q[2], 0x04000c0cu);
             }
+            const int sum = __builtin_amdgcn_sdot4((int)w[1], 0x01010101, __builtin_amdgcn_sdot4((int)w[0], 0x01010101, 0, false), false);
             *(uint2 *)(xq + (size_t)v * K + 32 * u + 8 * sub) = make_uint2(w[0], w[1]);
             const int half = sum + __builtin_bit_cast(int, quad_swap<0xB1>(__builtin_bit_cast(float, sum)));
             const int shi = __builtin_bit_cast(int, quad_swap<0x4E>(__builtin_bit_cast(float, half)));
@@ -501,7 +534,9 @@ struct StreamPass {
 #pragma unroll
             for (int t = 0; t < NV; t++) {
                 const int v = KIND == 2 ? uspan[j] * nv + t : t;
-                const float w = KIND == 2 ? a.wt[t][uspan[j]] : 1.f;   // routing weight folded into D
+                const float w = KIND == 2 ? __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                uspan[j] << 2, __builtin_bit_cast(int, wtl[t])))
+                                          : 1.f;   // routing weight folded into D
                 xr[j][t] = load_xu<F, XNEG>(xq, xm, K, nu, v, up, w, uval[j] && t < nv);
             }
         }
@@ -511,10 +546,20 @@ struct StreamPass {
         const bool gather = PF * NV <= lpr;
         const int bsrc = ((tid & 63) | (lpr - 1)) << 2;    // byte address of the group's last lane
         using TP = TwoPhase<F>;
-        for (int base = gid; base < nrow; base += PF * ngroups) {
-            if (base != gid) load_batch(base);
+        // Row ring (64-lane groups): slot p is refilled with the same slot's row of the next batch
+        // as soon as its units are decoded, so PF rows stay in flight across batches. The refill is
+        // unconditional inside the loop, also in the last batch (past the end it reads nothing):
+        // a branch around it, or a last batch peeled off the loop, makes the compiler copy the
+        // slots and wait for every load at the loop head. Waves with a single batch skip the
+        // refills. Other widths load each batch at its start.
+        auto batch = [&](const int base, auto issue_c) {
+            constexpr bool ISSUE = decltype(issue_c)::value;
             float res0[PF][NV], res1[PF][NV];
             float out0 = 0.f, out1 = 0.f;
+            // ring kernels (one vector, gather lanes): the output a GEMV / down store adds to, read
+            // before this batch's refills so its wait does not cover them (clamped, always issued)
+            float yold = 0.f;
+            if (RING && KIND != 1) yold = y[min(base + min(lane, PF - 1) * ngroups, nrow - 1)];
             // units of the batch in order (row p, unit j), each one's table reads issued one unit
             // ahead (reads of rows past the end fetch valid table entries and are unused)
             typename TP::Dec dec[2];
@@ -558,6 +603,12 @@ struct StreamPass {
                 } else if (p + 1 < PF) {
                     TP::fetch(R[p + 1][0], dec[((p + 1) * UMAX) & 1]);
                 }
+                if (ISSUE) {   // kept after the slot's last use: hoisted above it, the loads would
+                               // need fresh registers and a full wait at the loop head
+                    GS_RING_SB
+                    load_row(p, base + (PF + p) * ngroups);
+                    GS_RING_SB
+                }
 #pragma unroll
                 for (int t = 0; t < NV; t++) {
 #ifdef GS_PROBE_NORED   // profiling build only: no cross-lane reduction
@@ -593,11 +644,11 @@ struct StreamPass {
                 if (lane < PF * NV && t < nv && rr < nrow) {
                     if (KIND == 0) {
                         float *dst = y + (int64_t)t * a.y_stride + rr;
-                        *dst = a.accumulate ? *dst + out0 : out0;
+                        *dst = a.accumulate ? (RING ? yold : *dst) + out0 : out0;
                     } else if (KIND == 1) {
                         store_h(&y[((int64_t)ge * nv + t) * rows + rr], swiglu_fast(out0, out1, a.lim));
                     } else {
-                        y[(int64_t)t * a.y_stride + rr] += out0;
+                        y[(int64_t)t * a.y_stride + rr] = (RING ? yold : y[(int64_t)t * a.y_stride + rr]) + out0;
                     }
                 }
             } else if (lane == lpr - 1) {
@@ -621,19 +672,44 @@ struct StreamPass {
                     }
                 }
             }
+        };
+        if (RING && __builtin_amdgcn_readfirstlane(gid) + PF * ngroups >= nrow) {   // one batch: no refills
+            if (gid < nrow) batch(gid, BoolC<false>{});
+            return;
+        }
+        for (int base = gid; base < nrow; base += PF * ngroups) {
+            if (!RING && base != gid) load_batch(base);
+            batch(base, BoolC<RING>{});
         }
     }
 };
 
+#ifndef GS_WFIRST
+#define GS_WFIRST 0
+#endif
 template <class F, int KIND, int NV, int UMAX, int LP = 0>
 __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     extern __shared__ __align__(16) uint8_t smem[];
     GS_TS(0, 0)
     StreamPass<F, KIND, NV, UMAX, LP> P(a, smem);
+#if GS_WFIRST == 1
+    P.issue_tab();
+    P.load_row(0, P.gid);
+    P.issue_x();
+    GS_TS(1, 0)
+#pragma unroll
+    for (int p = 1; p < P.PF; p++) P.load_row(p, P.gid + p * P.ngroups);
+#elif GS_WFIRST == 2
+    P.issue_tab();
+    P.load_batch(P.gid);
+    GS_TS(1, 0)
+    P.issue_x();
+#else
     P.issue_x();
     P.issue_tab();
     GS_TS(1, 0)
     P.load_batch(P.gid);
+#endif
     GS_TS(2, 0)
     P.stage_x();
 #ifndef GS_STREAM_NOBAR

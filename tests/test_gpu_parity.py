@@ -75,6 +75,47 @@ def test_quant_q8_1_bit_exact(stream):
     assert np.array_equal(got, want)
 
 
+def _probe_x(K, seed):
+    """activations covering the quantizer's edge cases, unit by unit (32 elements each)"""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(K).astype(np.float32)
+    x[:32] = 0                                                        # zero unit: d = 0, id = 0
+    x[32:64] = np.linspace(-3, 3, 32)
+    x[64:96] = 1e-30                                                  # amax / 127 subnormal
+    x[96:128] = rng.standard_normal(32).astype(np.float32) * 3e4      # large (f16 d stays finite)
+    x[128:160] = np.arange(32, dtype=np.float32) - 15.5               # halves: ties away from zero
+    x[160] = 127.0                                                    # d = 1 exactly ...
+    x[161:192] = (np.arange(31, dtype=np.float32) - 15) + 0.5         # ... so every q is a tie
+    x[192:224] = -x[160:192]
+    x[224:256] = np.float32(2.0 ** -118) * (1 + np.arange(32, dtype=np.float32) / 32)   # fast-path edge
+    return x
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_staged_q8_1_bit_exact(B, stream):
+    # One-hot Q8_0 rows (row r: weight 1 at column r, block scale 1.0) make the GEMV return the
+    # kernel's own q8_1 activation f16(d) * q exactly, so the quantization each streaming kernel
+    # stages in LDS is compared bit for bit with the oracle's q8_1.
+    say("staged q8_1 B", B)
+    K = 2048
+    rb = G.row_bytes(T.Q8_0, K)
+    w = np.zeros((K, K // 32, 34), dtype=np.uint8)
+    r = np.arange(K)
+    w[r, r // 32, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), dtype=np.uint8)
+    w[r, r // 32, 2 + r % 32] = 1
+    x = np.concatenate([_probe_x(K, 40 + b) for b in range(B)])
+    want = np.concatenate([O.dequantize_q8_1(O.quantize_q8_1(x[b * K:(b + 1) * K]), K) for b in range(B)])
+    dw = G.DeviceBuffer.from_array(w.reshape(-1))
+    dx = G.DeviceBuffer.from_array(x)
+    dy = G.DeviceBuffer(B * K * 4)
+    G.ops.gemv(T.Q8_0, dw, rb, K, K, dx, K, dy, K, B, False, stream)
+    got = dy.download(np.float32, B * K, stream)
+    bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
+    if bad.size:
+        say("  mismatches", bad.size, bad[:5], got[bad[:5]], want[bad[:5]])
+    assert bad.size == 0
+
+
 def _gemv_case(ty, rows, K, B, stream, seed, x_stride=None, accumulate=False, row_stride=None):
     rb = G.row_bytes(ty, K)
     rs = rb if row_stride is None else row_stride
