@@ -57,7 +57,7 @@ def bench_lib():
     L.bn_moe_ffn.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, I64, C.c_int, C.c_int, I64, P, P, P, C.c_int,
                              C.c_int, P, C.POINTER(C.c_float)]
     L.bn_copy.argtypes = [P, P, C.c_size_t, C.c_int, P, C.POINTER(C.c_float)]
-    L.bn_moe_grouped.argtypes = [C.c_int, P, C.c_int, C.c_int, P, P, P, P, C.c_int, I64, C.c_int, C.c_int, I64, P, P,
+    L.bn_moe_grouped.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, P, P, P, P, C.c_int, I64, C.c_int, C.c_int, I64, P, P,
                                  P, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     return L
 
@@ -116,7 +116,8 @@ def run_moe_decode(L, s, steps, warmup, n_expert=288, n_embd=4096, n_ff=1536, se
     step_bytes = 8 * (2 * mat + mat_dn)
     gu_bytes = 8 * 2 * mat
     keep = (gate, up, down, dx, dh, dy, batches)
-    layer = dict(gate=gate, up=up, down=down, mat=mat, n_expert=n_expert, n_embd=n_embd, n_ff=n_ff, rbg=rbg, rbd=rbd)
+    layer = dict(gate=gate, up=up, down=down, mat=mat, mat_dn=mat_dn, n_expert=n_expert, n_embd=n_embd, n_ff=n_ff,
+                 rbg=rbg, rbd=rbd, ty_gu=int(ty), ty_dn=int(ty_dn))
     return dict(ms_step=ms.value, ms_gateup=msg.value, ms_ffn=msf.value, step_bytes=step_bytes, gateup_bytes=gu_bytes,
                 flops=8 * 3 * 2 * n_ff * n_embd), keep, layer
 
@@ -128,13 +129,12 @@ def run_moe_grouped(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
     import glmssd as G
     from glmssd import synth
     from glmssd.moe import group_pairs
-    ty = G.GgmlType.IQ2_XXS
-    n_exp, mat = layer["n_expert"], layer["mat"]
+    n_exp, mat, mat_dn = layer["n_expert"], layer["mat"], layer["mat_dn"]
     tab = (G.ExpertPtrs * n_exp)()
     for e in range(n_exp):
         tab[e].gate = layer["gate"].p.value + e * mat
         tab[e].up = layer["up"].p.value + e * mat
-        tab[e].down = layer["down"].p.value + e * mat
+        tab[e].down = layer["down"].p.value + e * mat_dn
     dtab = G.DeviceBuffer.from_array(np.frombuffer(bytes(tab), dtype=np.uint8), s)
     rng = np.random.default_rng(seed)
     keep, offs_p, idx_p, w_p, npairs, uniq, maxg = [dtab], [], [], [], [], [], []
@@ -155,12 +155,13 @@ def run_moe_grouped(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
     work = G.DeviceBuffer(wb)
     A = lambda v, t: (t * len(v))(*v)
     ms = C.c_float()
-    G.check(L.bn_moe_grouped(ty, dtab.p, n_exp, n_rout, C.cast(A(offs_p, C.c_void_p), C.c_void_p),
+    G.check(L.bn_moe_grouped(layer["ty_gu"], layer["ty_dn"], dtab.p, n_exp, n_rout,
+                             C.cast(A(offs_p, C.c_void_p), C.c_void_p),
                              C.cast(A(idx_p, C.c_void_p), C.c_void_p), C.cast(A(w_p, C.c_void_p), C.c_void_p),
                              C.cast(A(npairs, C.c_int), C.c_void_p), n_tok, layer["rbg"], n_embd, n_ff, layer["rbd"],
                              x.p, y.p, work.p, wb, steps, warmup, s.raw(), C.byref(ms)))
     u = float(np.mean(uniq))
-    wbytes = u * 3 * mat
+    wbytes = u * (2 * mat + mat_dn)
     flops = float(np.mean(npairs)) * 3 * 2 * n_ff * n_embd
     t = ms.value * 1e-3
     return dict(us_per_step=round(ms.value * 1e3, 2), unique_experts=round(u, 1), max_group=max(maxg),
@@ -251,14 +252,18 @@ def main():
     del keep, layer
     if not args.no_secondary:
         # the target model's routed experts: IQ2_XXS gate/up, IQ3_XXS down, n_ff_exp = 2048
-        rr, keep2, _ = run_moe_decode(L, s, args.steps, args.warmup, n_expert=96, n_ff=2048, seed=6,
-                                      ty_dn=G.GgmlType.IQ3_XXS, label="target-model decode FFN")
+        rr, keep2, layer2 = run_moe_decode(L, s, args.steps, args.warmup, n_expert=96, n_ff=2048, seed=6,
+                                           ty_dn=G.GgmlType.IQ3_XXS, label="target-model decode FFN")
         secondary["decode_ffn_iq2xxs_gateup_iq3xxs_down_nff2048"] = {
             "us_per_step": round(rr["ms_step"] * 1e3, 2), "GB/s": round(rr["step_bytes"] / rr["ms_step"] / 1e6, 1),
             "us_fused_gs_moe_ffn": round(rr["ms_ffn"] * 1e3, 2), "weight_bytes": rr["step_bytes"],
             "experts_resident": 96}
         log(f"target-model decode FFN: {secondary['decode_ffn_iq2xxs_gateup_iq3xxs_down_nff2048']}")
-        del keep2
+        # config 5's 512-token prefill on the target model's expert types and shapes
+        r = run_moe_grouped(L, s, layer2, 512, gsteps, gwarm, 7)
+        secondary["prefill_512tok_grouped_iq2xxs_gateup_iq3xxs_down_nff2048"] = r
+        log(f"target-model prefill: {r}")
+        del keep2, layer2
         secondary["config2_fused_gs_moe_ffn"] = {"us_per_step": round(res["ms_ffn"] * 1e3, 2),
                                                  "GB/s": round(res["step_bytes"] / res["ms_ffn"] / 1e6, 1)}
         from glmssd import synth

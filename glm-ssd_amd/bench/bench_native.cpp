@@ -100,7 +100,7 @@ BN_EXPORT int bn_gemv(int ty, const void *const *Ws, int nw, int64_t rs, int K, 
 // Grouped MoE FFN (prefill / MTP verify): one gs_moe_grouped call per step over routing
 // (i % nr); offs/idx/w hold nr device pointers each. y accumulates across steps (the values are
 // not checked here). Mean ms per step.
-BN_EXPORT int bn_moe_grouped(int ty, const GsExpertPtrs *experts, int n_exp, int nr, const int *const *offs,
+BN_EXPORT int bn_moe_grouped(int ty_gu, int ty_dn, const GsExpertPtrs *experts, int n_exp, int nr, const int *const *offs,
                              const int *const *idx, const float *const *w, const int *n_pairs, int n_tok, int64_t rs_gu,
                              int n_embd, int n_ff, int64_t rs_dn, const float *x, float *y, void *work,
                              size_t work_bytes, int steps, int warmup, void *s, float *ms) {
@@ -108,7 +108,7 @@ BN_EXPORT int bn_moe_grouped(int ty, const GsExpertPtrs *experts, int n_exp, int
     CK(t.init());
     auto call = [&](int i) {
         const int r = i % nr;
-        return gs_moe_grouped(ty, ty, experts, n_exp, offs[r], idx[r], w[r], n_pairs[r], n_tok, rs_gu, n_embd, n_ff,
+        return gs_moe_grouped(ty_gu, ty_dn, experts, n_exp, offs[r], idx[r], w[r], n_pairs[r], n_tok, rs_gu, n_embd, n_ff,
                               rs_dn, x, y, 0.0f, work, work_bytes, s);
     };
     for (int i = 0; i < warmup; i++) CK(call(i));

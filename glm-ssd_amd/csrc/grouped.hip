@@ -11,6 +11,8 @@
 //     super-block is applied to the f32 accumulator once per super-block. A lane owns one row
 //     (the D column it accumulates), so that factor is one scalar per lane. Weights are therefore
 //     exact, where the reference's GEMM rounds dequantized weights to half (gemm.cu:57-66).
+//   * IQ3_XXS (98-byte super-blocks) the same way: grid * sign * (2s+1) (|v| <= 62*31 = 1922),
+//     remaining factor d/4; a unit's 8 index bytes give two 4-value table entries per group.
 //   * activations (A operand) are f16, as in the reference's multi-token GEMM (gemm.cu:69-78),
 //     after a power-of-two row scale that keeps the row's largest value in the f16 normal range
 //     (restored exactly in the epilogue); h enters the down projection the same way.
@@ -29,9 +31,9 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));   // staging chunk (a native vector, so it stays in VGPRs)
 
 // Decode tables in LDS, built by every workgroup at start:
-//   grid (64 KB): for grid index g and unit scale s (0..15), the 8 grid values times 2s+1 as f16
-//     at byte (g << 8) | (s << 4) -- the address is one v_perm of the unit's index byte and its
-//     scale nibble;
+//   grid (64 KB): for grid index g and unit scale s (0..15), the 8 (IQ2_XXS) or 4 (IQ3_XXS) grid
+//     values times 2s+1 as f16 at byte (g << 8) | (s << 4) -- the address is one v_perm of the
+//     unit's index byte and its scale nibble;
 //   signs (1 KB): for a 7-bit sign index i, 8 bytes, byte e = 0x80 when element e of ksigns(i)
 //     is negative, at byte 65536 + 8 i.
 // A B fragment is one 16-byte and one 8-byte LDS read, 4 v_perm (sign bytes -> f16 sign bits)
@@ -40,16 +42,24 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));   // staging chunk (a n
 #define GS_GRP_TAB_BYTES (65536 + 1024)
 __shared__ int gs_grp_pre[GS_GRP_EXP_MAX + 1];
 
-template <int NTH>
+template <int TY, int NTH>
 __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
     for (int e = tid; e < 4096; e += NTH) {
         const int g = e >> 4, sc = e & 15;
-        const uint64_t grid = iq2xxs_grid[g];
         const float m = (float)(2 * sc + 1);
         uint32_t w[4];
+        if (TY == GS_IQ2_XXS) {
+            const uint64_t grid = iq2xxs_grid[g];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            w[i] = f2h(m * (float)((grid >> (16 * i)) & 0xff)) | (f2h(m * (float)((grid >> (16 * i + 8)) & 0xff)) << 16);
+            for (int i = 0; i < 4; i++)
+                w[i] = f2h(m * (float)((grid >> (16 * i)) & 0xff)) | (f2h(m * (float)((grid >> (16 * i + 8)) & 0xff)) << 16);
+        } else {   // IQ3_XXS: 4 grid values per entry, the upper 8 bytes of the slot unused
+            const uint32_t grid = iq3xxs_grid[g];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                w[i] = f2h(m * (float)((grid >> (16 * i)) & 0xff)) | (f2h(m * (float)((grid >> (16 * i + 8)) & 0xff)) << 16);
+            w[2] = w[3] = 0;
+        }
         *(uint4 *)(tab + (e << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
     for (int i = tid; i < 128; i += NTH) {
@@ -64,6 +74,31 @@ __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
     }
 }
 
+// sign bytes of group G (8 weights) -> the f16 sign-bit masks of its 4 half pairs
+template <int G>
+__device__ __forceinline__ uint4 grp_sign_masks(const uint8_t *tab, uint32_t a1) {
+    const uint2 sb = *(const uint2 *)(tab + 65536 + (((a1 >> (7 * G)) & 127) << 3));
+    // sign byte e -> bit 15 (e even) / bit 31 (e odd) of half pair e/2: bytes [0, s(2i), 0, s(2i+1)]
+    return make_uint4(__builtin_amdgcn_perm(sb.y, sb.x, 0x010c000cu), __builtin_amdgcn_perm(sb.y, sb.x, 0x030c020cu),
+                      __builtin_amdgcn_perm(sb.y, sb.x, 0x050c040cu), __builtin_amdgcn_perm(sb.y, sb.x, 0x070c060cu));
+}
+
+// IQ3_XXS B fragment: group G (0..3) of the unit with grid-index words g0, g1 (8 index bytes) and
+// a1 = signs | s << 28: the 8 f16 integers grid * sign * (2s+1) from two 4-value table entries
+// (lib.rs:312-328; |v| <= 62 * 31 = 1922, exact in f16)
+template <int G>
+__device__ __forceinline__ h8 iq3_frag(const uint8_t *tab, uint32_t g0, uint32_t g1, uint32_t a1) {
+    const uint32_t gw = G < 2 ? g0 : g1;
+    constexpr uint32_t b0 = (2 * G) & 3;
+    const uint32_t hs = a1 & 0xF0000000u;
+    const uint32_t ga0 = __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + (b0 << 8));
+    const uint32_t ga1 = __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + ((b0 + 1) << 8));
+    const uint2 lo = *(const uint2 *)(tab + ga0);
+    const uint2 hi = *(const uint2 *)(tab + ga1);
+    const uint4 m = grp_sign_masks<G>(tab, a1);
+    return __builtin_bit_cast(h8, make_uint4(lo.x ^ m.x, lo.y ^ m.y, hi.x ^ m.z, hi.y ^ m.w));
+}
+
 // B fragment: group G (0..3) of the unit with words (a0 = grid indices, a1 = signs | s << 28):
 // 8 f16 integers grid * sign * (2s+1)
 template <int G>
@@ -74,13 +109,8 @@ __device__ __forceinline__ h8 iq2_frag(const uint8_t *tab, uint32_t a0, uint32_t
     // [s << 4, index byte G, 0, 0]: byte 3 of (a1 & 0xF0000000) and byte G of a0
     const uint32_t ga = __builtin_amdgcn_perm(a0, a1 & 0xF0000000u, 0x0c0c0403u + (G << 8));
     const uint4 g = *(const uint4 *)(tab + ga);
-    const uint2 sb = *(const uint2 *)(tab + 65536 + (((a1 >> (7 * G)) & 127) << 3));
-    // sign byte e -> bit 15 (e even) / bit 31 (e odd) of half pair e/2: bytes [0, s(2i), 0, s(2i+1)]
-    const uint32_t m0 = __builtin_amdgcn_perm(sb.y, sb.x, 0x010c000cu);
-    const uint32_t m1 = __builtin_amdgcn_perm(sb.y, sb.x, 0x030c020cu);
-    const uint32_t m2 = __builtin_amdgcn_perm(sb.y, sb.x, 0x050c040cu);
-    const uint32_t m3 = __builtin_amdgcn_perm(sb.y, sb.x, 0x070c060cu);
-    return __builtin_bit_cast(h8, make_uint4(g.x ^ m0, g.y ^ m1, g.z ^ m2, g.w ^ m3));
+    const uint4 m = grp_sign_masks<G>(tab, a1);
+    return __builtin_bit_cast(h8, make_uint4(g.x ^ m.x, g.y ^ m.y, g.z ^ m.z, g.w ^ m.w));
 }
 
 // profiling variants replace single components of the contraction
@@ -163,8 +193,12 @@ __device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb
 // scales, combine weights) during the tile, so no load is waited on right after it is issued.
 // A token row of one super-block is 512 B in LDS (32 chunks of 16 B); chunk c of slot i sits at
 // chunk position c ^ (i & 15), so the 16 lanes that read one chunk column hit 16 bank groups.
-template <int KIND, int NT, int NR, int WV>
+template <int TY, int KIND, int NT, int NR, int WV>
 __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
+    static_assert(TY == GS_IQ2_XXS || TY == GS_IQ3_XXS, "grouped formats: IQ2_XXS, IQ3_XXS");
+    constexpr bool IQ3 = TY == GS_IQ3_XXS;
+    constexpr uint32_t BB = IQ3 ? 98 : 66;                  // bytes per super-block
+    constexpr float XS = IQ3 ? 0.25f : 0.125f;             // d factor left after the (2s+1) integers
     constexpr int MATS = KIND == 1 ? 2 : 1;
     constexpr int MT = 16 * NT;
     constexpr int RB = WV * 16 * NR;
@@ -180,7 +214,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     const uint32_t rs = (uint32_t)a.row_stride;
     uint8_t *const tab = gs_grp_dyn;
     uint8_t *const stage = gs_grp_dyn + GS_GRP_TAB_BYTES;
-    grp_tables<NTH>(tab, tid);
+    grp_tables<TY, NTH>(tab, tid);
     grp_prefix(a, MT, nrb);
     __syncthreads();
     const int total = gs_grp_pre[a.n_exp];
@@ -246,6 +280,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 
     struct WRegs {   // one position's raw weight words: 16 bytes (units 2q, 2q+1) + f16 d per row
         uint4 q[NR][MATS];
+        uint2 sg[NR][MATS];   // IQ3_XXS: the two units' sign/scale words
         uint32_t d[NR][MATS];
     };
     auto load_w = [&](const Desc &d, const uint32_t (&wo)[NR], int b, WRegs &w) {
@@ -256,9 +291,10 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 #ifdef GS_GRP_PROBE_NOWLOAD   // profiling variant: every position re-reads super-block 0 (cache hits)
                 const uint8_t *p = d.wb[mt] + wo[n];
 #else
-                const uint8_t *p = d.wb[mt] + (wo[n] + 66u * b);
+                const uint8_t *p = d.wb[mt] + (wo[n] + BB * b);
 #endif
                 w.q[n][mt] = ldg16(p);
+                if (IQ3) w.sg[n][mt] = ldg8(p + 64 - 8 * q);   // block + 66 + 8q
                 w.d[n][mt] = ldg2(p - 2 - 16 * q);
             }
     };
@@ -365,7 +401,9 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         h8 bf[NR][MATS];                                                                           \
         _Pragma("unroll") for (int n = 0; n < NR; n++)                                             \
         _Pragma("unroll") for (int mt = 0; mt < MATS; mt++)                                        \
-            bf[n][mt] = iq2_frag<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y); \
+            bf[n][mt] = IQ3 ? iq3_frag<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y, \
+                                          hu ? wu.sg[n][mt].y : wu.sg[n][mt].x)                        \
+                            : iq2_frag<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y); \
         const int cc = 8 * q + 4 * hu + G;                                                         \
         _Pragma("unroll") for (int tt = 0; tt < NT; tt++)                                          \
             if (tt == 0 || 16 * tt < n_here) {                                                     \
@@ -382,7 +420,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             for (int n = 0; n < NR; n++)
 #pragma unroll
                 for (int mt = 0; mt < MATS; mt++) {
-                    const float cd = h2f(wu.d[n][mt]) * 0.125f;
+                    const float cd = h2f(wu.d[n][mt]) * XS;
 #pragma unroll
                     for (int tt = 0; tt < NT; tt++) acc[tt][n][mt] += cd * sb[tt][n][mt];
                 }
@@ -461,12 +499,14 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     GS_TS_DUMP(a.out)
 }
 
-#define GS_GRP_KERNEL(KIND, NT, NR, WV)                                                          \
+#define GS_GRP_KERNEL1(TY, KIND, NT, NR, WV)                                                     \
     extern "C" __global__ void __launch_bounds__(64 * WV)                                       \
-        gs_k_grouped_16_##KIND##_##NT##_##NR##_##WV(GroupedArgs a) {                            \
-        grouped_body<KIND, NT, NR, WV>(a);                                                      \
+        gs_k_grouped_##TY##_##KIND##_##NT##_##NR##_##WV(GroupedArgs a) {                        \
+        grouped_body<TY, KIND, NT, NR, WV>(a);                                                  \
     }
-// instantiated (kind, NT, NR, waves) tile shapes; host.cpp grouped_launch keeps the same list
+#define GS_GRP_KERNEL(KIND, NT, NR, WV) GS_GRP_KERNEL1(16, KIND, NT, NR, WV) GS_GRP_KERNEL1(18, KIND, NT, NR, WV)
+// instantiated (kind, NT, NR, waves) tile shapes for IQ2_XXS (16) and IQ3_XXS (18); host.cpp
+// grouped_launch keeps the same list
 GS_GRP_KERNEL(1, 1, 1, 8)
 GS_GRP_KERNEL(1, 1, 2, 8)
 GS_GRP_KERNEL(1, 2, 1, 8)

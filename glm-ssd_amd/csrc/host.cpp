@@ -641,7 +641,7 @@ hipError_t rows_f16(const float *x, int64_t x_stride, int K, int nrows, uint16_t
 struct GrpShape {
     int nt, nr, wv;
 };
-hipError_t grouped_launch(int kind, GroupedArgs &a, int n_pairs, hipStream_t s) {
+hipError_t grouped_launch(int kind, int ty, GroupedArgs &a, int n_pairs, hipStream_t s) {
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
@@ -673,7 +673,7 @@ hipError_t grouped_launch(int kind, GroupedArgs &a, int n_pairs, hipStream_t s) 
     if (std::none_of(all.begin(), all.end(),
                      [&](const GrpShape &p) { return p.nt == sh.nt && p.nr == sh.nr && p.wv == sh.wv; }))
         return hipErrorInvalidValue;
-    const std::string name = "gs_k_grouped_16_" + std::to_string(kind) + "_" + std::to_string(sh.nt) + "_" +
+    const std::string name = "gs_k_grouped_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" + std::to_string(sh.nt) + "_" +
                              std::to_string(sh.nr) + "_" + std::to_string(sh.wv);
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
@@ -708,12 +708,15 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
                              const int *idx, const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K,
                              int n_ff, int64_t down_row_stride, const float *x, float *y, float lim, void *work,
                              size_t work_bytes, void *s) {
-    if (ty_gu != GS_IQ2_XXS || ty_down != GS_IQ2_XXS) return hipErrorInvalidValue;
+    auto grp_type = [](int t) { return t == GS_IQ2_XXS || t == GS_IQ3_XXS; };
+    if (!grp_type(ty_gu) || !grp_type(ty_down)) return hipErrorInvalidValue;
     if (n_exp < 1 || n_exp > GS_GRP_EXP_MAX || n_pairs < 0 || n_tok < 1) return hipErrorInvalidValue;
     // whole super-blocks, at least two per row (the kernel's load pipeline runs two ahead)
     if (K < 512 || n_ff < 512 || K % 256 != 0 || n_ff % 256 != 0) return hipErrorInvalidValue;
     if (!experts || !offs || !x || !y || (gu_row_stride & 1) || (down_row_stride & 1)) return hipErrorInvalidValue;
-    if (gu_row_stride < (int64_t)K / 256 * 66 || down_row_stride < (int64_t)n_ff / 256 * 66) return hipErrorInvalidValue;
+    auto sb_bytes = [](int t) { return t == GS_IQ3_XXS ? 98 : 66; };
+    if (gu_row_stride < (int64_t)K / 256 * sb_bytes(ty_gu) || down_row_stride < (int64_t)n_ff / 256 * sb_bytes(ty_down))
+        return hipErrorInvalidValue;
     if (n_pairs == 0) return 0;
     if (!idx || !w || !aligned16(x) || ((uintptr_t)work & 255)) return hipErrorInvalidValue;
     const GroupedWork L = grouped_layout(n_tok, n_pairs, K, n_ff);
@@ -738,7 +741,7 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
     a.rows = n_ff;
     a.n_exp = n_exp;
     a.lim = lim;
-    if ((e = grouped_launch(1, a, n_pairs, st)) != hipSuccess) return e;
+    if ((e = grouped_launch(1, ty_gu, a, n_pairs, st)) != hipSuccess) return e;
     if ((e = rows_f16(h, n_ff, n_ff, n_pairs, h16, hs, st)) != hipSuccess) return e;
     a.act = h16;
     a.ascale = hs;
@@ -746,7 +749,7 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
     a.row_stride = down_row_stride;
     a.K = n_ff;
     a.rows = K;
-    return grouped_launch(2, a, n_pairs, st);
+    return grouped_launch(2, ty_down, a, n_pairs, st);
 }
 
 

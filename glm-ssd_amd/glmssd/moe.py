@@ -100,7 +100,7 @@ class MoeLayer:
     (`Engine::moe`) without the expert cache. forward(): router logits (F32 GEMV), host routing,
     shared expert SwiGLU FFN into `out`, routed experts into an accumulator (one token or an MTP
     pair: gs_moe_ffn over batches of up to 16 experts; more tokens: the grouped MFMA kernel when
-    every expert matrix is IQ2_XXS, else per-expert gather / GEMM / SwiGLU / scatter-add as
+    every expert matrix is IQ2_XXS or IQ3_XXS, else per-expert gather / GEMM / SwiGLU / scatter-add as
     run_expert_rows), then out += accumulator.
 
     experts: list of (gate, up, down) host byte arrays; gate/up [n_ff rows x n_embd], down
@@ -125,7 +125,8 @@ class MoeLayer:
         self.up = [Mat(e[1], ty_gu, n_embd, n_ff, s) for e in experts]
         self.down = [Mat(e[2], ty_down, n_ff, n_embd, s) for e in experts]
         self.grouped = None
-        if ty_gu == T.IQ2_XXS and ty_down == T.IQ2_XXS:
+        grp = (T.IQ2_XXS, T.IQ3_XXS)
+        if ty_gu in grp and ty_down in grp:
             self.grouped = ResidentMoeLayer([e[0] for e in experts], [e[1] for e in experts],
                                             [e[2] for e in experts], n_embd, n_ff, ty_gu, ty_down)
         self._scratch = {}

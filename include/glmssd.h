@@ -148,8 +148,8 @@ int gs_quant_q8_1(const float *x, void *q, int64_t n, void *s);
  * gu_row_stride bytes apart) and down ([n_ff] x K rows, down_row_stride apart).
  *   y[idx[p]][:] += w[p] * down_e . swiglu(gate_e . x[idx[p]], up_e . x[idx[p]])   (always adds)
  * x [n_tok][K], y [n_tok][K] f32; activations are q8_1-quantized as in the other matmul calls.
- * Supported: ty_gu == ty_down == IQ2_XXS, K and n_ff multiples of 256 and >= 512, n_exp <= 1024, x 16-byte
- * aligned. `work` (256-byte aligned, >= gs_moe_grouped_workspace bytes) is caller-owned scratch.
+ * Supported: ty_gu, ty_down each IQ2_XXS or IQ3_XXS, K and n_ff multiples of 256 and >= 512,
+ * n_exp <= 1024, x 16-byte aligned. `work` (256-byte aligned, >= gs_moe_grouped_workspace bytes) is caller-owned scratch.
  * All of offs/idx/w/experts are device arrays; the call launches without a host sync. */
 typedef struct GsExpertPtrs {
     const uint8_t *gate;

@@ -5,7 +5,10 @@ MTP verify) against the CPU oracle's per-pair FFN:
     forward.rs:1399-1413): rel-L2 <= 1e-3, the north-star bound for FFN outputs;
   * act="f16x" -- half activations with exact weights, which is what the kernel computes (its
     weights are exact integers times the block scale): rel-L2 <= 1e-4, so the kernel's own error
-    (f32 accumulation order) is checked well inside the reference bound."""
+    (f32 accumulation order) is checked well inside the reference bound.
+Where the reference semantics' own weight rounding exceeds 1e-3 against exact weights (random
+IQ3_XXS blocks), the first bound becomes that distance + 1e-4 (the triangle inequality with the
+second bound)."""
 import sys
 
 import numpy as np
@@ -32,24 +35,25 @@ def rel_l2(got, want):
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
 
 
-def run_case(n_exp, n_tok, k, n_embd, n_ff, seed, lim=0.0, routes=None, zero_w=False):
-    say(f"grouped: n_exp={n_exp} n_tok={n_tok} top{k} K={n_embd} n_ff={n_ff} lim={lim} seed={seed}")
-    ty = T.IQ2_XXS
+def run_case(n_exp, n_tok, k, n_embd, n_ff, seed, lim=0.0, routes=None, zero_w=False, ty_gu=T.IQ2_XXS,
+             ty_down=T.IQ2_XXS):
+    say(f"grouped: {G.TYPE_NAMES[ty_gu]}/{G.TYPE_NAMES[ty_down]} n_exp={n_exp} n_tok={n_tok} top{k} K={n_embd} "
+        f"n_ff={n_ff} lim={lim} seed={seed}")
     orng = O.Rng(1000 + seed)
-    gate = [orng.random_blocks(ty, n_ff * n_embd) for _ in range(n_exp)]
-    up = [orng.random_blocks(ty, n_ff * n_embd) for _ in range(n_exp)]
-    down = [orng.random_blocks(ty, n_embd * n_ff) for _ in range(n_exp)]
+    gate = [orng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(n_exp)]
+    up = [orng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(n_exp)]
+    down = [orng.random_blocks(ty_down, n_embd * n_ff) for _ in range(n_exp)]
     rng = np.random.default_rng(seed)
     if routes is None:
         routes = [list(zip(e, w)) for e, w in synth.zipf_topk(rng, n_tok, n_exp, k)]
     if zero_w:
         routes[0][0] = (routes[0][0][0], 0.0)
     x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
-    layer = M.ResidentMoeLayer(gate, up, down, n_embd, n_ff)
+    layer = M.ResidentMoeLayer(gate, up, down, n_embd, n_ff, ty_gu, ty_down)
     offs, idx, w, pe = layer.upload_routes(routes)
-    want = O.moe_ffn(ty, ty, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, x, idx, pe, w, lim=lim,
+    want = O.moe_ffn(ty_gu, ty_down, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, x, idx, pe, w, lim=lim,
                      nthreads=8, act="f16")
-    wantx = O.moe_ffn(ty, ty, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, x, idx, pe, w, lim=lim,
+    wantx = O.moe_ffn(ty_gu, ty_down, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, x, idx, pe, w, lim=lim,
                       nthreads=8, act="f16x")
     y0 = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
     s = G.Stream()
@@ -57,9 +61,13 @@ def run_case(n_exp, n_tok, k, n_embd, n_ff, seed, lim=0.0, routes=None, zero_w=F
     layer.forward(dx, dy, n_tok, lim, s)
     got = dy.download(np.float32, n_tok * n_embd, s).reshape(n_tok, n_embd).astype(np.float64) - y0
     err, errx = rel_l2(got, want), rel_l2(got, wantx)
+    err_ref = rel_l2(want, wantx)   # the reference semantics' own half-rounding of the weights
     say(f"  pairs={idx.size} max group={np.diff(offs).max()} rel-L2 vs reference GEMM semantics {err:.2e}, "
-        f"vs exact weights {errx:.2e}")
-    assert err <= REL_L2
+        f"vs exact weights {errx:.2e} (reference semantics vs exact weights {err_ref:.2e})")
+    # Within 1e-3 of the reference's result, unless the reference's own weight rounding already
+    # moves it further than that from the exact-weight result (random IQ3_XXS blocks can): then
+    # within that distance plus the kernel's own bound below.
+    assert err <= max(REL_L2, err_ref + 1e-4)
     assert errx <= 1e-4
     return layer, got
 
@@ -84,3 +92,14 @@ def test_grouped_repeat_is_stable():
     # two calls into fresh outputs agree to f32 atomic-order noise
     layer, a = run_case(n_exp=16, n_tok=20, k=4, n_embd=512, n_ff=768, seed=11)
     assert np.all(np.isfinite(a))
+
+
+def test_grouped_iq3_xxs_down_target_types():
+    # the target model's expert types: IQ2_XXS gate/up, IQ3_XXS down (n_ff 2048 shape family)
+    run_case(n_exp=16, n_tok=40, k=4, n_embd=1024, n_ff=2048, seed=21, ty_down=T.IQ3_XXS)
+
+
+def test_grouped_iq3_xxs_everywhere_decode_sized():
+    # random IQ3_XXS gate/up blocks drive h past the f16 range of the reference semantics (inf in
+    # the oracle); the SwiGLU clamp the model uses keeps it finite
+    run_case(n_exp=32, n_tok=4, k=8, n_embd=768, n_ff=512, seed=22, lim=7.0, ty_gu=T.IQ3_XXS, ty_down=T.IQ3_XXS)
