@@ -8,6 +8,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -519,6 +520,38 @@ static bool ffn_pair(int ty_gu, int ty_dn) {
 // Routed-expert FFN of one layer: exactly gs_moe_gateup followed by gs_moe_down (h is written
 // too). For one token whose down pass fits one launch this is a single fused launch (gate/up,
 // grid barrier, down); otherwise, or with GLMSSD_NO_FFN_FUSION set, the two launches.
+// bound of the fused FFN's grid-barrier wait, in ticks of the 100 MHz clock (0.2 s)
+constexpr uint64_t kFfnWaitTicks = 20000000ull;
+std::atomic<uint64_t> g_ffn_wait_ticks{kFfnWaitTicks};
+
+GS_EXPORT int gs_moe_ffn_set_wait_limit(uint64_t ticks) {
+    g_ffn_wait_ticks.store(ticks ? ticks : kFfnWaitTicks);
+    return 0;
+}
+
+GS_EXPORT int gs_moe_ffn_status(int *expired) {
+    if (!expired) return hipErrorInvalidValue;
+    *expired = 0;
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+    for (hipModule_t m : c->mods) {   // every per-format code object holds its own flag
+        hipDeviceptr_t p;
+        size_t sz;
+        if (hipModuleGetGlobal(&p, &sz, m, "gs_ffn_timeout") != hipSuccess || sz != sizeof(unsigned)) continue;
+        unsigned v = 0;
+        if ((e = hipMemcpyDtoH(&v, p, sizeof v)) != hipSuccess) return e;
+        if (v) {
+            *expired = 1;
+            const unsigned zero = 0;
+            if ((e = hipMemcpyHtoD(p, (void *)&zero, sizeof zero)) != hipSuccess) return e;
+        }
+    }
+    (void)hipGetLastError();   // clear the lookup misses of modules without fused kernels
+    return 0;
+}
+
 GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int64_t rs_gu, int n_embd, int n_ff,
                          int64_t rs_dn, const float *x, float *h, float *y, float lim, void *s) {
     int rc = moe_check(ty_gu, b, nt, n_embd, n_ff, rs_gu);
@@ -538,6 +571,7 @@ GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int6
                fa.gu.lpr == 64 && fa.dn.lpr == 64 && fa.dn.wlo;   // what the fused kernels fix
     }
     if (fuse) {
+        fa.wait_ticks = g_ffn_wait_ticks.load();
         const std::string name = "gs_k_ffn_" + std::to_string(ty_gu) + "_" + std::to_string(ty_dn) + "_" +
                                  std::to_string(P1.um) + "_" + std::to_string(P2.um);
         const size_t lds = std::max(P1.lds, P2.lds);

@@ -48,8 +48,9 @@ struct StreamArgs {
 
 // Fused MoE FFN (gate/up + SwiGLU, grid barrier, down + combine) for one token
 struct FfnArgs {
-    StreamArgs gu;   // kind 1: gate/up -> h
-    StreamArgs dn;   // kind 2: h -> y (accumulated)
+    StreamArgs gu;         // kind 1: gate/up -> h
+    StreamArgs dn;         // kind 2: h -> y (accumulated)
+    uint64_t wait_ticks;   // bound of the grid-barrier wait (100 MHz clock ticks)
 };
 
 // Whole-tensor dequantization

@@ -767,13 +767,11 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
 // across XCDs needs no cache flush: the gate/up pass stores h at device scope (written through),
 // every workgroup waits for its own stores to complete before it arrives, and nothing reads h
 // before the barrier. The barrier counters only grow (see gs_ffn_sync); the wait is bounded in
-// time (GS_BAR_TICKS of the 100 MHz clock): on expiry gs_ffn_timeout is set and the kernel
-// runs to completion with undefined results instead of hanging. Launches of this kernel must
-// not overlap on one device (they share the counters).
+// time (FfnArgs::wait_ticks of the 100 MHz clock, 0.2 s unless the host sets another bound): on
+// expiry gs_ffn_timeout is set and the kernel runs to completion with undefined results instead
+// of hanging; the host reads and clears the flag (gs_moe_ffn_status). Launches of this kernel
+// must not overlap on one device (they share the counters).
 // =============================================================================================
-#ifndef GS_BAR_TICKS
-#define GS_BAR_TICKS 20000000ull   // 0.2 s
-#endif
 // Barrier counters, one 128-byte line each: arrivals of workgroup group g = blockIdx.x % 8
 // (groups arrive on separate lines, so their atomics proceed in parallel), and completed groups.
 // They only ever grow: a launch adds exactly its group sizes and group count, so each launch
@@ -805,13 +803,13 @@ __device__ __forceinline__ void grid_arrive() {
 }
 
 // Wait (thread 0) until every group of this launch has arrived; bounded in time.
-__device__ __forceinline__ void grid_wait(unsigned long long top0) {
+__device__ __forceinline__ void grid_wait(unsigned long long top0, uint64_t ticks) {
     const unsigned nblk = gridDim.x;
     const unsigned ng = nblk < GS_BAR_GROUPS ? nblk : GS_BAR_GROUPS;
     const unsigned long long target = (top0 / ng + 1) * ng;
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (__hip_atomic_load(&gs_ffn_sync[8].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        if (__builtin_amdgcn_s_memrealtime() - t0 > GS_BAR_TICKS) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 > ticks) {
             __hip_atomic_store(&gs_ffn_timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
@@ -840,7 +838,7 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
     D.issue_tab();
     D.load_batch(D.gid);   // down weights in flight across the barrier
     GS_TS(2, 0)
-    if (threadIdx.x == 0) grid_wait(top0);
+    if (threadIdx.x == 0) grid_wait(top0, fa.wait_ticks);
     __builtin_amdgcn_s_barrier();   // no memory wait: the down weights keep streaming
     GS_TS(3, 0)
     D.issue_x();           // h, complete in every expert

@@ -118,6 +118,16 @@ int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, 
 int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int64_t rs_gu, int n_embd, int n_ff, int64_t rs_dn,
                const float *x, float *h, float *y, float lim, void *s);
 
+/* Additive (no counterpart in the reference): health of the fused launches of gs_moe_ffn. Their
+ * grid-wide barrier waits at most a bounded time (0.2 s by default); if a wait expires (a
+ * workgroup never arrived: the grid was not co-resident, or the device was preempted) the kernel
+ * still completes, sets a flag and its results are undefined. gs_moe_ffn_status waits for the
+ * device to finish, then reports in *expired whether any fused launch on the current device
+ * expired since the previous call, and clears the flag. gs_moe_ffn_set_wait_limit sets the bound
+ * (ticks of the 100 MHz clock) for later launches from any thread; 0 restores the default. */
+int gs_moe_ffn_status(int *expired);
+int gs_moe_ffn_set_wait_limit(uint64_t ticks);
+
 /* ---- GEMM and MoE glue (crates/cuda/src/lib.rs:71-74,115-122; kernels/gemm.cu, ops.cu) ---- */
 /* SwiGLU with clamp: y = silu(min(g,L)) * clamp(u,-L,L); L <= 0: no clamp (lib.rs:76; ops.cu:101-115) */
 int gs_swiglu(const float *g, const float *u, float *y, int64_t n, float lim, void *s);
