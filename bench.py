@@ -170,6 +170,44 @@ def run_moe_grouped(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
                 frac_mfma_f16_peak=round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4), routings_rotated=n_rout)
 
 
+def run_moe_per_token(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
+    """Config 4 the way the MoE layer runs up to 4 tokens: one fused gs_moe_ffn call per token over
+    its own top-k experts (Zipf(1.1) routings as run_moe_grouped draws them, n_rout rotated).
+    Timed per call by bn_moe_ffn; a step is n_tok calls."""
+    import glmssd as G
+    from glmssd import synth
+    n_exp, mat, mat_dn = layer["n_expert"], layer["mat"], layer["mat_dn"]
+    rng = np.random.default_rng(seed)
+    batches = (G.MoeBatch * (n_rout * n_tok))()
+    uniq = []
+    for r in range(n_rout):
+        routes = synth.zipf_topk(rng, n_tok, n_exp, k)
+        uniq.append(len({int(e) for ex, _ in routes for e in ex}))
+        for t, (ex, w) in enumerate(routes):
+            b = batches[r * n_tok + t]
+            b.n = len(ex)
+            for j, (e, wj) in enumerate(zip(ex, w)):
+                e = int(e)
+                b.gate[j] = layer["gate"].p.value + e * mat
+                b.up[j] = layer["up"].p.value + e * mat
+                b.down[j] = layer["down"].p.value + e * mat_dn
+                b.w[0][j] = float(wj)
+    n_embd, n_ff = layer["n_embd"], layer["n_ff"]
+    x = G.DeviceBuffer.from_array(rng.standard_normal(n_embd).astype(np.float32), s)
+    h = G.DeviceBuffer(k * n_ff * 4)
+    y = G.DeviceBuffer(n_embd * 4)
+    y.zero(s)
+    ms = C.c_float()
+    G.check(L.bn_moe_ffn(layer["ty_gu"], layer["ty_dn"], C.cast(batches, C.c_void_p), n_rout * n_tok, 1,
+                         layer["rbg"], n_embd, n_ff, layer["rbd"], x.p, h.p, y.p, steps * n_tok, warmup * n_tok,
+                         s.raw(), C.byref(ms)))
+    t = ms.value * n_tok * 1e-3
+    wbytes = float(np.mean(uniq)) * (2 * mat + mat_dn)
+    return dict(us_per_step=round(t * 1e6, 2), unique_experts=round(float(np.mean(uniq)), 1),
+                weight_bytes=int(wbytes), GBps=round(wbytes / t / 1e9, 1),
+                frac_hbm_peak=round(wbytes / t / 1e9 / HBM_PEAK_GBPS, 4), calls_per_step=n_tok, routings_rotated=n_rout)
+
+
 def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 20):
     import glmssd as G
     rng = np.random.default_rng(seed)
@@ -249,6 +287,9 @@ def main():
             r = run_moe_grouped(L, s, layer, n_tok, gsteps, gwarm, seed)
             secondary[name] = r
             log(f"{name}: {r}")
+        r = run_moe_per_token(L, s, layer, 4, gsteps, gwarm, 4)
+        secondary["config4_mtp_verify_4tok_per_token_ffn"] = r
+        log(f"config4_mtp_verify_4tok_per_token_ffn: {r}")
     del keep, layer
     if not args.no_secondary:
         # the target model's routed experts: IQ2_XXS gate/up, IQ3_XXS down, n_ff_exp = 2048
