@@ -321,11 +321,15 @@ struct StreamPass {
         rnu = 1.0f / (float)nu;
         ge = 0;
         if (KIND == 1) {
-            ge = __builtin_amdgcn_readfirstlane(wave_all % a.nseg);
+            // each expert owns a block of consecutive waves, so its adjacent rows (which share a
+            // 128-byte line when rows are not line multiples) go to waves of one workgroup and
+            // one XCD's L2 rather than to two XCDs that would both fetch the shared line
             const int wpe = nwaves_all / a.nseg;                    // waves per expert
+            const int wq = wave_all / wpe;
+            ge = __builtin_amdgcn_readfirstlane(wq < a.nseg ? wq : a.nseg - 1);
             ngroups = wpe * gpw;
-            gid = (wave_all / a.nseg) * gpw + gin;
-            nrow = wave_all >= wpe * a.nseg ? 0 : rows;             // leftover waves idle
+            gid = (wave_all - wq * wpe) * gpw + gin;
+            nrow = wq >= a.nseg ? 0 : rows;                         // leftover waves idle
         } else {
             ngroups = nwaves_all * gpw;
             gid = wave_all * gpw + gin;
