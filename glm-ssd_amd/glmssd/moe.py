@@ -98,15 +98,15 @@ class Mat:
 class MoeLayer:
     """One MoE FFN layer with every expert resident: the work of forward.rs:982-1136
     (`Engine::moe`) without the expert cache. forward(): router logits (F32 GEMV), host routing,
-    shared expert SwiGLU FFN into `out`, routed experts into an accumulator (one token or an MTP
-    pair: gs_moe_ffn over batches of up to 16 experts; 3 or 4 tokens: one fused gs_moe_ffn per token;
-    more tokens: the grouped MFMA kernel when
+    shared expert SwiGLU FFN into `out`, routed experts into an accumulator (up to 4 tokens: one
+    fused gs_moe_ffn per token over its own experts, where the engine's decode branch batches up
+    to 16 experts for 1-2 tokens; more tokens: the grouped MFMA kernel when
     every expert matrix is IQ2_XXS or IQ3_XXS, else per-expert gather / GEMM / SwiGLU / scatter-add as
     run_expert_rows), then out += accumulator.
 
     experts: list of (gate, up, down) host byte arrays; gate/up [n_ff rows x n_embd], down
     [n_embd rows x n_ff]."""
-    MOE_MAX, MOE_NT, PER_TOKEN_MAX = 16, 2, 4
+    MOE_MAX, PER_TOKEN_MAX = 16, 4
 
     def __init__(self, router, bias, shared, experts, n_embd, n_ff, ty_gu, ty_down, k=8, weights_norm=True,
                  weights_scale=1.0, clamp_exp=0.0, clamp_shexp=0.0, router_ty=T.F32, shared_ty=(T.Q6_K,) * 3,
@@ -171,22 +171,10 @@ class MoeLayer:
             for e, w in r:
                 groups[e].append((ti, w))
         used = [e for e in range(ne) if groups[e]]
-        if t <= self.MOE_NT:
-            # decode / MTP pair: batches of up to 16 experts through the fused FFN
-            h = self._buf("h", self.MOE_MAX * t * self.n_ff * 4)
-            for b0 in range(0, len(used), self.MOE_MAX):
-                chunk = used[b0:b0 + self.MOE_MAX]
-                b = MoeBatch()
-                b.n = len(chunk)
-                for i, e in enumerate(chunk):
-                    b.gate[i], b.up[i], b.down[i] = self.gate[e].ptr().value, self.up[e].ptr().value, self.down[e].ptr().value
-                    for ti, w in groups[e]:
-                        b.w[ti][i] = w
-                ops.moe_ffn(self.ty_gu, self.ty_down, b, t, self.gate[0].row_bytes, n, self.n_ff,
-                            self.down[0].row_bytes, xn, h, acc, self.lim, s)
-        elif t <= self.PER_TOKEN_MAX:
-            # MTP verify sizes: one fused one-token FFN per token over its own experts (measured
-            # faster than the grouped GEMM at 4 tokens: 4 x 18.7 us against 116 us on config 4)
+        if t <= self.PER_TOKEN_MAX:
+            # decode and MTP sizes: one fused one-token FFN per token over its own experts (on the
+            # config-2 experts: 2 tokens 36 us against 52 us as one 2-token batch over the union of
+            # their experts, 4 tokens 71 us against 116 us through the grouped GEMM)
             h = self._buf("h", self.MOE_MAX * self.n_ff * 4)
             for ti, r in enumerate(routes):
                 for b0 in range(0, len(r), self.MOE_MAX):

@@ -1,8 +1,7 @@
 """GPU parity of a whole MoE FFN layer (glmssd.moe.MoeLayer, the work of forward.rs:982-1136 with
 every expert resident): router GEMV (F32, f32 activations), host routing, shared-expert SwiGLU
 FFN (Q6_K), routed experts (the target model's IQ2_XXS gate/up + IQ3_XXS down) through the fused
-FFN for one token and an MTP pair, one fused FFN per token for 3-4 tokens, the grouped MFMA kernel
-for more. The oracle restates the same composition on the
+FFN, one fused one-token FFN per token for up to 4 tokens, the grouped MFMA kernel for more. The oracle restates the same composition on the
 CPU; the routes must agree exactly and the output within rel-L2 1e-3."""
 import sys
 
