@@ -9,6 +9,12 @@ from . import DeviceBuffer, ExpertPtrs, ops
 from .types import GgmlType as T, row_bytes
 
 
+def _at(buf, offset):
+    """device address buf + offset bytes (buf: DeviceBuffer or c_void_p)"""
+    base = buf.p.value if isinstance(buf, DeviceBuffer) else C.c_void_p(buf).value if isinstance(buf, int) else buf.value
+    return C.c_void_p(base + offset)
+
+
 def group_pairs(routes, n_exp):
     """routes: per token a sequence of (expert, weight). Returns (offs[n_exp+1], idx, w, pair_exp):
     pairs sorted by expert (ascending id), within an expert in token order, as forward.rs
@@ -186,7 +192,7 @@ class MoeLayer:
                                                          self.down[e].ptr().value)
                         b.w[0][i] = w
                     ops.moe_ffn(self.ty_gu, self.ty_down, b, 1, self.gate[0].row_bytes, n, self.n_ff,
-                                self.down[0].row_bytes, xn.ptr(ti * n * 4), h, acc.ptr(ti * n * 4), self.lim, s)
+                                self.down[0].row_bytes, _at(xn, ti * n * 4), h, acc.ptr(ti * n * 4), self.lim, s)
         elif self.grouped is not None:
             self.grouped.upload_routes(routes, s)
             self.grouped.forward(xn, acc, t, self.lim, s)
