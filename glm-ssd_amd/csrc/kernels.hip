@@ -249,6 +249,12 @@ template <class F> struct Paired<F, decltype((void)F::PAIR, void())> { static co
 #ifndef GS_RING_SB
 #define GS_RING_SB __builtin_amdgcn_sched_barrier(0);
 #endif
+// Formats whose units can be decoded ahead of the activations (PreUnit, predecode, dot_pre)
+template <class A, class B> struct is_same_t { static constexpr bool value = false; };
+template <class A> struct is_same_t<A, A> { static constexpr bool value = true; };
+template <class F, class = void> struct HasPre { static constexpr bool value = false; };
+template <class F> struct HasPre<F, decltype((void)F::PRE, void())> { static constexpr bool value = F::PRE; };
+
 template <bool B> struct BoolC { static constexpr bool value = B; };
 
 // LP: 0 = lane-group width from the arguments; 64 = fixed 64 (whole rows per wave, so the row
@@ -293,6 +299,10 @@ struct StreamPass {
     typename F::TabReg treg;
     typename F::Raw R[PF][UMAX];
     float wtl[NV];   // DOWN: lane i holds vector t's combine weight for expert i
+    // one-token 64-lane down with an IQ format: the batch's units decoded ahead of the activations
+    // (at most 12 units: 10 registers each)
+    static constexpr bool PRE = KIND == 2 && LP == 64 && NV == 1 && !XNEG && HasPre<F>::value && PF * UX <= 12;
+    PreUnit P[PRE ? PF : 1][PRE ? UX : 1];
 
     // geometry of this pass; issues no memory access except the pointer-table load (DOWN/GATEUP)
     __device__ __forceinline__ StreamPass(const StreamArgs &a_, uint8_t *smem) : a(a_) {
@@ -527,9 +537,25 @@ struct StreamPass {
         }
     }
 
+    // PRE: decode the first batch's units (waits for their weights; the tables must be staged)
+    __device__ __forceinline__ void predecode() {
+        if constexpr (PRE) {
+#pragma unroll
+            for (int p = 0; p < PF; p++)
+#pragma unroll
+                for (int j = 0; j < UX; j++) F::predecode(R[p][j], P[p][j]);
+        }
+    }
+    // whether this wave's rows fit one batch (then run_rows<true> can use the predecoded units)
+    __device__ __forceinline__ bool single_batch() const {
+        return __builtin_amdgcn_readfirstlane(gid) + PF * ngroups >= nrow;
+    }
+
     // activation units from LDS into registers, then every batch of rows (the first batch is
-    // already loaded) with the results stored
+    // already loaded) with the results stored. USE_PRE: one batch whose units predecode() decoded.
+    template <bool USE_PRE = false>
     __device__ __forceinline__ void run_rows() {
+        static_assert(!USE_PRE || PRE, "predecoded rows need a PRE pass");
         const uint32_t *xm = (const uint32_t *)(xq + (size_t)nxv * K);
         XU xr[UX][NV];
 #pragma unroll
@@ -567,7 +593,7 @@ struct StreamPass {
             // units of the batch in order (row p, unit j), each one's table reads issued one unit
             // ahead (reads of rows past the end fetch valid table entries and are unused)
             typename TP::Dec dec[2];
-            TP::fetch(R[0][0], dec[0]);
+            if (!USE_PRE) TP::fetch(R[0][0], dec[0]);
 #pragma unroll
             for (int p = 0; p < PF; p++) {
                 float acc0[NV], acc1[NV];
@@ -590,6 +616,10 @@ struct StreamPass {
                             acc0[0] += __builtin_bit_cast(float, ((const uint32_t *)&R[p][j])[w] & 0x3fffffffu);
                     if (false)
 #endif
+                    if constexpr (USE_PRE) {
+#pragma unroll
+                        for (int j = 0; j < UX; j++) dot_pre<NV>(P[PRE ? p : 0][PRE ? j : 0], xr[j], nv, acc0);
+                    } else
 #pragma unroll
                     for (int j = 0; j < UMAX; j++) {
                         const int i = p * UMAX + j;
@@ -604,7 +634,7 @@ struct StreamPass {
                         else
                             TP::template dot<NV, XNEG>(R[p][j], dec[i & 1], usub[jx], tab, xr[jx], nv, acc0);
                     }
-                } else if (p + 1 < PF) {
+                } else if (!USE_PRE && p + 1 < PF) {
                     TP::fetch(R[p + 1][0], dec[((p + 1) * UMAX) & 1]);
                 }
                 if (ISSUE) {   // kept after the slot's last use: hoisted above it, the loads would
@@ -677,7 +707,7 @@ struct StreamPass {
                 }
             }
         };
-        if (RING && __builtin_amdgcn_readfirstlane(gid) + PF * ngroups >= nrow) {   // one batch: no refills
+        if (USE_PRE || (RING && single_batch())) {   // one batch: no refills
             if (gid < nrow) batch(gid, BoolC<false>{});
             return;
         }
@@ -826,12 +856,18 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
     extern __shared__ __align__(16) uint8_t smem[];
     GS_TS(0, 0)
     const unsigned long long top0 = threadIdx.x == 0 ? barrier_epoch() : 0;
+    // a down format with other tables: staged with the gate/up ones (separate LDS arrays; the
+    // sign selectors are common), so the down units can be decoded before the barrier
+    constexpr bool SAME = is_same_t<F1, F2>::value;
+    typename F2::TabReg t2;
+    if (!SAME) F2::tab_load(threadIdx.x, t2);
     {
         StreamPass<F1, 1, 1, UM1, 64> G(fa.gu, smem);   // the host fuses only 64-lane gate/up plans
         G.issue_x();
         G.issue_tab();
         G.load_batch(G.gid);
         G.stage_x();
+        if (!SAME) F2::tab_store(threadIdx.x, t2);
         __syncthreads();
         G.run_rows();
     }
@@ -842,6 +878,11 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
     D.issue_tab();
     D.load_batch(D.gid);   // down weights in flight across the barrier
     GS_TS(2, 0)
+    // IQ formats, one batch of rows per wave: the down units are decoded (table reads, signs)
+    // while the workgroup waits for the grid and for h, leaving only the dots for afterwards.
+    constexpr bool PRE = decltype(D)::PRE;
+    const bool pre = PRE && D.single_batch();
+    if (pre) D.predecode();
     if (threadIdx.x == 0) grid_wait(top0, fa.wait_ticks);
     __builtin_amdgcn_s_barrier();   // no memory wait: the down weights keep streaming
     GS_TS(3, 0)
@@ -849,7 +890,12 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
     D.stage_x();
     __syncthreads();
     GS_TS(6, 0)
-    D.run_rows();
+    if constexpr (PRE) {
+        if (pre) D.template run_rows<true>();
+        else D.run_rows();
+    } else {
+        D.run_rows();
+    }
     GS_TS(7, 0)
 }
 
