@@ -291,6 +291,7 @@ struct StreamPass {
     float rnu;   // 1/nu
     int64_t rs;
     const uint8_t *wg, *wu, *wb0;   // GATEUP gate / up, GEMV matrix (wave-uniform)
+    uint64_t tw0, tw1;              // expert pointer tables (lane i: expert i), until bind()
     int uspan[UX], usub[UX];
     uint32_t uoff[UX];
     bool uval[UX];
@@ -349,25 +350,14 @@ struct StreamPass {
         // expert pointer tables: one vector load (lane i <- entry i), then readlane / bpermute, so no
         // weight address waits on a second, dependent kernel-argument fetch
         const int L64 = tid & 63;
-        const uint64_t tw0 = KIND != 0 && L64 < GS_SEG_MAX ? (uint64_t)a.w0[L64] : 0;
-        const uint64_t tw1 = KIND == 1 && L64 < GS_SEG_MAX ? (uint64_t)a.w1[L64] : 0;
+        tw0 = KIND != 0 && L64 < GS_SEG_MAX ? (uint64_t)a.w0[L64] : 0;
+        tw1 = KIND == 1 && L64 < GS_SEG_MAX ? (uint64_t)a.w1[L64] : 0;
         // combine weights likewise (lane i <- expert i), requested before the weight loads so the
         // activation setup does not wait for them
 #pragma unroll
         for (int t = 0; t < NV; t++) wtl[t] = KIND == 2 && L64 < GS_SEG_MAX && t < nv ? a.wt[t][L64] : 0.f;
-        auto lane_u64 = [](uint64_t v, int src) -> uint64_t {   // v of lane `src` (per-lane src)
-            const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v);
-            const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)(v >> 32));
-            return (uint64_t)lo | ((uint64_t)hi << 32);
-        };
         wg = wu = nullptr;
         wb0 = wb;
-        if (KIND == 1) {
-            wg = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw0 >> 32), ge) << 32) |
-                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw0, ge));
-            wu = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw1 >> 32), ge) << 32) |
-                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw1, ge));
-        }
         // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
 #pragma unroll
         for (int j = 0; j < UX; j++) {
@@ -382,12 +372,33 @@ struct StreamPass {
             usub[j] = F::sub(up);
         }
 #pragma unroll
-        for (int j = 0; j < UX; j++) {
-            ubase[j] = KIND == 2 ? (const uint8_t *)lane_u64(tw0, uspan[j]) : (KIND == 1 ? nullptr : wb);
-            if (KIND == 2 && LP == 64) uoff[j] += (uint32_t)(ubase[j] - a.wlo);
-        }
+        for (int j = 0; j < UX; j++) ubase[j] = KIND == 0 ? wb : nullptr;
         nxv = KIND == 2 ? a.nseg * nv : nv;
         nxu = nxv * nu;
+    }
+
+    // Expert addresses from the pointer tables the constructor requested. Called after issue_x
+    // and issue_tab: waiting for the tables (in issue order) then leaves the activation loads in
+    // flight instead of holding them back behind the tables.
+    __device__ __forceinline__ void bind() {
+        auto lane_u64 = [](uint64_t v, int src) -> uint64_t {   // v of lane `src` (per-lane src)
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)(v >> 32));
+            return (uint64_t)lo | ((uint64_t)hi << 32);
+        };
+        if (KIND == 1) {
+            wg = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw0 >> 32), ge) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw0, ge));
+            wu = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw1 >> 32), ge) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw1, ge));
+        }
+        if (KIND == 2) {
+#pragma unroll
+            for (int j = 0; j < UX; j++) {
+                ubase[j] = (const uint8_t *)lane_u64(tw0, uspan[j]);
+                if (LP == 64) uoff[j] += (uint32_t)(ubase[j] - a.wlo);
+            }
+        }
     }
 
     __device__ __forceinline__ const float *xsrc(int v, int u) const {
@@ -718,32 +729,16 @@ struct StreamPass {
     }
 };
 
-#ifndef GS_WFIRST
-#define GS_WFIRST 0
-#endif
 template <class F, int KIND, int NV, int UMAX, int LP = 0>
 __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     extern __shared__ __align__(16) uint8_t smem[];
     GS_TS(0, 0)
     StreamPass<F, KIND, NV, UMAX, LP> P(a, smem);
-#if GS_WFIRST == 1
-    P.issue_tab();
-    P.load_row(0, P.gid);
-    P.issue_x();
-    GS_TS(1, 0)
-#pragma unroll
-    for (int p = 1; p < P.PF; p++) P.load_row(p, P.gid + p * P.ngroups);
-#elif GS_WFIRST == 2
-    P.issue_tab();
-    P.load_batch(P.gid);
-    GS_TS(1, 0)
-    P.issue_x();
-#else
     P.issue_x();
     P.issue_tab();
+    P.bind();
     GS_TS(1, 0)
     P.load_batch(P.gid);
-#endif
     GS_TS(2, 0)
     P.stage_x();
 #ifndef GS_STREAM_NOBAR
@@ -865,6 +860,7 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
         StreamPass<F1, 1, 1, UM1, 64> G(fa.gu, smem);   // the host fuses only 64-lane gate/up plans
         G.issue_x();
         G.issue_tab();
+        G.bind();
         G.load_batch(G.gid);
         G.stage_x();
         if (!SAME) F2::tab_store(threadIdx.x, t2);
@@ -876,6 +872,7 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
     if (threadIdx.x == 0) grid_arrive();
     StreamPass<F2, 2, 1, UM2, 64> D(fa.dn, smem);   // the host fuses only 64-lane down plans with wlo
     D.issue_tab();
+    D.bind();
     D.load_batch(D.gid);   // down weights in flight across the barrier
     GS_TS(2, 0)
     // IQ formats, one batch of rows per wave: the down units are decoded (table reads, signs)
