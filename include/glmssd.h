@@ -99,7 +99,9 @@ int gs_gemv_batched(int ty, const void *W, int64_t row_stride, int K, int rows, 
                     int64_t w_bs, int64_t x_bs, int64_t y_bs, void *s);
 
 /* fused routed-expert gate/up + SwiGLU: h[e][t][r] = swiglu(gate_e[r].x[t], up_e[r].x[t]);
- * x [nt][K], h [b->n][nt][rows] (lib.rs:62-65; quants.cu:378-393) */
+ * x [nt][K], h [b->n][nt][rows] (lib.rs:62-65; quants.cu:378-393). K <= 8192 for one token and
+ * K <= 4096 for two (a lane holds its share of the row's units; the target model has K = 4096);
+ * larger K returns hipErrorInvalidValue. */
 int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *x, float *h,
                   float lim, void *s);
 

@@ -40,7 +40,10 @@ CASES = [(T.IQ2_XXS, T.IQ2_XXS, 1, 8, 4096, 1536, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 1
          (T.IQ2_XXS, T.IQ2_XXS, 2, 6, 2048, 1024, 0.0), (T.Q5_K, T.Q5_K, 1, 2, 1024, 512, 0.0),
          # the target model's routed experts: IQ2_XXS gate/up, IQ3_XXS down, n_ff_exp = 2048
          # (validate.rs:376-386), one decode token and a 2-token MTP step
-         (T.IQ2_XXS, T.IQ3_XXS, 1, 8, 4096, 2048, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 2, 8, 4096, 2048, 0.0)]
+         (T.IQ2_XXS, T.IQ3_XXS, 1, 8, 4096, 2048, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 2, 8, 4096, 2048, 0.0),
+         # down with more rows than one batch per wave (n_embd 8192: the down row ring, and the
+         # fused kernel's fallback from its early decode)
+         (T.IQ2_XXS, T.IQ2_XXS, 1, 4, 8192, 512, 0.0)]
 
 
 @pytest.mark.parametrize("ty_gu,ty_dn,nt,n,n_embd,n_ff,lim", CASES)

@@ -155,6 +155,16 @@ def test_gemv_matches_oracle(ty, rows, K, stream):
         assert _gemv_case(ty, rows, K, B, stream, seed=1000 * ty + rows + B) <= (REL_L2_F32 if ty in FLOAT else REL_L2)
 
 
+# Rows beyond one batch per wave (more than 2 x 2048 rows for one vector): the one-token kernels
+# refill their row slots as they go (the row ring), including the last batch's empty refills and
+# rows that end inside a batch; config 3's Q4_K shape among them.
+@pytest.mark.parametrize("ty,rows,K", [(T.Q4_K, 12288, 4096), (T.Q8_0, 8191, 4096), (T.IQ2_XXS, 10001, 4096),
+                                       (T.IQ3_XXS, 9000, 2048), (T.Q6_K, 6000, 12288)])
+def test_gemv_many_rows_ring(ty, rows, K, stream):
+    assert _gemv_case(ty, rows, K, 1, stream, seed=31 * ty + rows) <= REL_L2
+    assert _gemv_case(ty, rows, K, 1, stream, seed=37 * ty + rows, accumulate=True) <= REL_L2
+
+
 @pytest.mark.parametrize("ty", HOT)
 def test_gemv_accumulate_and_strides(ty, stream):
     K = 1024
