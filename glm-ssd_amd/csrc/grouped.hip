@@ -74,42 +74,40 @@ __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
     }
 }
 
-// sign bytes of group G (8 weights) -> the f16 sign-bit masks of its 4 half pairs
+// B fragment of group G (0..3) of one unit: 8 f16 integers grid * sign * (2s+1). Two phases, so
+// a decode step issues the table reads of all its fragments before it waits for any of them
+// (one fragment at a time, every read waited for in turn, config 5 took 6 % longer):
+//   IQ2_XXS: a0 = the unit's 4 grid-index bytes, a1 = signs | s << 28; one 16-byte grid read;
+//   IQ3_XXS: g0, g1 = its 8 index bytes, a1 as above; two 8-byte reads of 4-value entries
+//     (lib.rs:312-328; |v| <= 62 * 31 = 1922, exact in f16);
+// both: one 8-byte sign-byte read; finish turns sign byte e into bit 15 (e even) / bit 31 (e odd)
+// of half pair e/2 and applies it with XOR.
+struct FragRaw {
+    uint4 g;
+    uint2 sb;
+    uint2 g2;   // IQ3_XXS: the second 4-value entry
+};
 template <int G>
-__device__ __forceinline__ uint4 grp_sign_masks(const uint8_t *tab, uint32_t a1) {
-    const uint2 sb = *(const uint2 *)(tab + 65536 + (((a1 >> (7 * G)) & 127) << 3));
-    // sign byte e -> bit 15 (e even) / bit 31 (e odd) of half pair e/2: bytes [0, s(2i), 0, s(2i+1)]
-    return make_uint4(__builtin_amdgcn_perm(sb.y, sb.x, 0x010c000cu), __builtin_amdgcn_perm(sb.y, sb.x, 0x030c020cu),
-                      __builtin_amdgcn_perm(sb.y, sb.x, 0x050c040cu), __builtin_amdgcn_perm(sb.y, sb.x, 0x070c060cu));
+__device__ __forceinline__ void iq2_frag_fetch(const uint8_t *tab, uint32_t a0, uint32_t a1, FragRaw &r) {
+    const uint32_t ga = __builtin_amdgcn_perm(a0, a1 & 0xF0000000u, 0x0c0c0403u + (G << 8));
+    r.g = *(const uint4 *)(tab + ga);
+    r.sb = *(const uint2 *)(tab + 65536 + (((a1 >> (7 * G)) & 127) << 3));
 }
-
-// IQ3_XXS B fragment: group G (0..3) of the unit with grid-index words g0, g1 (8 index bytes) and
-// a1 = signs | s << 28: the 8 f16 integers grid * sign * (2s+1) from two 4-value table entries
-// (lib.rs:312-328; |v| <= 62 * 31 = 1922, exact in f16)
 template <int G>
-__device__ __forceinline__ h8 iq3_frag(const uint8_t *tab, uint32_t g0, uint32_t g1, uint32_t a1) {
+__device__ __forceinline__ void iq3_frag_fetch(const uint8_t *tab, uint32_t g0, uint32_t g1, uint32_t a1, FragRaw &r) {
     const uint32_t gw = G < 2 ? g0 : g1;
     constexpr uint32_t b0 = (2 * G) & 3;
     const uint32_t hs = a1 & 0xF0000000u;
-    const uint32_t ga0 = __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + (b0 << 8));
-    const uint32_t ga1 = __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + ((b0 + 1) << 8));
-    const uint2 lo = *(const uint2 *)(tab + ga0);
-    const uint2 hi = *(const uint2 *)(tab + ga1);
-    const uint4 m = grp_sign_masks<G>(tab, a1);
-    return __builtin_bit_cast(h8, make_uint4(lo.x ^ m.x, lo.y ^ m.y, hi.x ^ m.z, hi.y ^ m.w));
+    const uint2 lo = *(const uint2 *)(tab + __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + (b0 << 8)));
+    r.g2 = *(const uint2 *)(tab + __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + ((b0 + 1) << 8)));
+    r.g = make_uint4(lo.x, lo.y, 0u, 0u);
+    r.sb = *(const uint2 *)(tab + 65536 + (((a1 >> (7 * G)) & 127) << 3));
 }
-
-// B fragment: group G (0..3) of the unit with words (a0 = grid indices, a1 = signs | s << 28):
-// 8 f16 integers grid * sign * (2s+1)
-template <int G>
-__device__ __forceinline__ h8 iq2_frag(const uint8_t *tab, uint32_t a0, uint32_t a1) {
-#ifdef GS_GRP_PROBE_NODECODE   // profiling variant: no table lookups
-    return __builtin_bit_cast(h8, make_uint4(a0, a1, a0 ^ a1, a0 + a1));
-#endif
-    // [s << 4, index byte G, 0, 0]: byte 3 of (a1 & 0xF0000000) and byte G of a0
-    const uint32_t ga = __builtin_amdgcn_perm(a0, a1 & 0xF0000000u, 0x0c0c0403u + (G << 8));
-    const uint4 g = *(const uint4 *)(tab + ga);
-    const uint4 m = grp_sign_masks<G>(tab, a1);
+template <bool IQ3>
+__device__ __forceinline__ h8 frag_finish(const FragRaw &r) {
+    const uint4 m = make_uint4(__builtin_amdgcn_perm(r.sb.y, r.sb.x, 0x010c000cu), __builtin_amdgcn_perm(r.sb.y, r.sb.x, 0x030c020cu),
+                               __builtin_amdgcn_perm(r.sb.y, r.sb.x, 0x050c040cu), __builtin_amdgcn_perm(r.sb.y, r.sb.x, 0x070c060cu));
+    const uint4 g = IQ3 ? make_uint4(r.g.x, r.g.y, r.g2.x, r.g2.y) : r.g;
     return __builtin_bit_cast(h8, make_uint4(g.x ^ m.x, g.y ^ m.y, g.z ^ m.z, g.w ^ m.w));
 }
 
@@ -396,14 +394,20 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                     for (int mt = 0; mt < MATS; mt++) sb[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int hu = 0; hu < 2; hu++) {    // unit 2q + hu
+#define GS_GRP_FRAGS(G)                                                                            \
+        FragRaw fr[NR][MATS];                                                                      \
+        _Pragma("unroll") for (int n = 0; n < NR; n++)                                             \
+        _Pragma("unroll") for (int mt = 0; mt < MATS; mt++) {                                      \
+            if (IQ3) iq3_frag_fetch<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y, \
+                                       hu ? wu.sg[n][mt].y : wu.sg[n][mt].x, fr[n][mt]);          \
+            else iq2_frag_fetch<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y, fr[n][mt]); \
+        }                                                                                          \
+        _Pragma("unroll") for (int n = 0; n < NR; n++)                                             \
+        _Pragma("unroll") for (int mt = 0; mt < MATS; mt++) bf[n][mt] = frag_finish<IQ3>(fr[n][mt]);
 #define GS_GRP_STEP(G)                                                                             \
     {                                                                                              \
         h8 bf[NR][MATS];                                                                           \
-        _Pragma("unroll") for (int n = 0; n < NR; n++)                                             \
-        _Pragma("unroll") for (int mt = 0; mt < MATS; mt++)                                        \
-            bf[n][mt] = IQ3 ? iq3_frag<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y, \
-                                          hu ? wu.sg[n][mt].y : wu.sg[n][mt].x)                        \
-                            : iq2_frag<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y); \
+        GS_GRP_FRAGS(G)                                                                            \
         const int cc = 8 * q + 4 * hu + G;                                                         \
         _Pragma("unroll") for (int tt = 0; tt < NT; tt++)                                          \
             if (tt == 0 || 16 * tt < n_here) {                                                     \
