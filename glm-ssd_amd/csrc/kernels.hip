@@ -140,14 +140,19 @@ __device__ __forceinline__ float swiglu_fast(float g, float u, float lim) {
 //   kind 2 DOWN:    units of down_e[r] for every expert e of the batch (one weighted sum)
 // =============================================================================================
 // Rows in flight per lane group: as many as GS_PF_REGS VGPRs of raw weight bytes hold (1..8).
-// Gate/up rows carry twice the units (gate and up), so their budget is smaller: a smaller first
-// batch arrives sooner and the decode starts earlier (measured on the decode shapes: 2 rows per
-// batch beat 4 by ~1 us of 12), while the down and GEMV passes keep deeper batches.
+// Gate/up rows carry twice the units (gate and up), so their budget is smaller: 3 ring slots, of
+// which only 2 are requested before the activation staging (config 2 gate/up: 9.9 -> 9.5 us
+// against 2 slots; 4 slots, or 3 requested at once, were slower: the first request grows and
+// arrives later), while the down and GEMV passes keep deeper batches.
 #ifndef GS_PF_REGS
 #define GS_PF_REGS 48
 #endif
 #ifndef GS_PF_REGS_GU
-#define GS_PF_REGS_GU 24
+#define GS_PF_REGS_GU 36
+#endif
+// ring slots requested before the activation staging (the others right after it)
+#ifndef GS_RING_EARLY
+#define GS_RING_EARLY 2
 #endif
 template <class F, int UMAX, int KIND = 0>
 __device__ __forceinline__ constexpr int pf_depth() {
@@ -470,10 +475,12 @@ struct StreamPass {
             for (int j = 0; j < UX; j++) load_unit(GlobalAt{ubase[j] + roff}, j, R[p], 0);
         }
     }
-    // the first PF rows of the lane group (later rows are requested by run_rows as slots free up)
-    __device__ __forceinline__ void load_batch(int base) {
+    // the first PF rows of the lane group (later rows are requested by run_rows as slots free up);
+    // slots [p0, p1) only
+    __device__ __forceinline__ void load_batch(int base, int p0 = 0, int p1 = PF) {
 #pragma unroll
-        for (int p = 0; p < PF; p++) load_row(p, base + p * ngroups);
+        for (int p = 0; p < PF; p++)
+            if (p >= p0 && p < p1) load_row(p, base + p * ngroups);
     }
 
     // tables + q8_1 quantization of every activation vector into LDS (the caller then syncs).
@@ -738,12 +745,16 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     P.issue_tab();
     P.bind();
     GS_TS(1, 0)
-    P.load_batch(P.gid);
+    // ring kernels: only the first GS_RING_EARLY slots before the activation staging (a smaller
+    // first request arrives sooner), the rest after it
+    constexpr int E = P.RING && GS_RING_EARLY < P.PF ? GS_RING_EARLY : P.PF;
+    P.load_batch(P.gid, 0, E);
     GS_TS(2, 0)
     P.stage_x();
 #ifndef GS_STREAM_NOBAR
     __syncthreads();
 #endif
+    P.load_batch(P.gid, E, P.PF);
     GS_TS(3, 0)
     P.run_rows();
     GS_TS(5, 0)
@@ -861,10 +872,12 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
         G.issue_x();
         G.issue_tab();
         G.bind();
-        G.load_batch(G.gid);
+        constexpr int E = G.RING && GS_RING_EARLY < G.PF ? GS_RING_EARLY : G.PF;
+        G.load_batch(G.gid, 0, E);
         G.stage_x();
         if (!SAME) F2::tab_store(threadIdx.x, t2);
         __syncthreads();
+        G.load_batch(G.gid, E, G.PF);
         G.run_rows();
     }
     GS_TS(1, 0)
