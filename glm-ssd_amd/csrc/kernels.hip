@@ -140,10 +140,12 @@ __device__ __forceinline__ float swiglu_fast(float g, float u, float lim) {
 //   kind 2 DOWN:    units of down_e[r] for every expert e of the batch (one weighted sum)
 // =============================================================================================
 // Rows in flight per lane group: as many as GS_PF_REGS VGPRs of raw weight bytes hold (1..8).
-// Gate/up rows carry twice the units (gate and up), so their budget is smaller: 3 ring slots, of
-// which only 2 are requested before the activation staging (config 2 gate/up: 9.9 -> 9.5 us
-// against 2 slots; 4 slots, or 3 requested at once, were slower: the first request grows and
-// arrives later), while the down and GEMV passes keep deeper batches.
+// Gate/up rows carry twice the units (gate and up), so their budget is smaller: 3 ring slots
+// (config 2 gate/up: 9.9 -> 9.4 us against 2; 4 were slower), while the down and GEMV passes
+// keep deeper batches. The MoE ring kernels request only their first slot before the activation
+// staging and the others right after it: a smaller first request arrives sooner (config 2 down
+// 9.35 -> 9.0 us; all slots at once, the first batch grows and comes later). The GEMVs request
+// all at once (Q4_K's three batches per wave: 8.8 us against 8.97 with the split).
 #ifndef GS_PF_REGS
 #define GS_PF_REGS 48
 #endif
@@ -152,7 +154,7 @@ __device__ __forceinline__ float swiglu_fast(float g, float u, float lim) {
 #endif
 // ring slots requested before the activation staging (the others right after it)
 #ifndef GS_RING_EARLY
-#define GS_RING_EARLY 2
+#define GS_RING_EARLY 1
 #endif
 template <class F, int UMAX, int KIND = 0>
 __device__ __forceinline__ constexpr int pf_depth() {
@@ -747,7 +749,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     GS_TS(1, 0)
     // ring kernels: only the first GS_RING_EARLY slots before the activation staging (a smaller
     // first request arrives sooner), the rest after it
-    constexpr int E = P.RING && GS_RING_EARLY < P.PF ? GS_RING_EARLY : P.PF;
+    constexpr int E = P.RING && KIND != 0 && GS_RING_EARLY < P.PF ? GS_RING_EARLY : P.PF;
     P.load_batch(P.gid, 0, E);
     GS_TS(2, 0)
     P.stage_x();
