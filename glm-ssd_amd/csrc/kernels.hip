@@ -253,9 +253,6 @@ __device__ __forceinline__ int udiv_small(int u, float rd) { return (int)(((floa
 template <class F, class = void> struct Paired { static constexpr bool value = false; };
 template <class F> struct Paired<F, decltype((void)F::PAIR, void())> { static constexpr bool value = F::PAIR; };
 
-#ifndef GS_RING_SB
-#define GS_RING_SB __builtin_amdgcn_sched_barrier(0);
-#endif
 // Formats whose units can be decoded ahead of the activations (PreUnit, predecode, dot_pre)
 template <class A, class B> struct is_same_t { static constexpr bool value = false; };
 template <class A> struct is_same_t<A, A> { static constexpr bool value = true; };
@@ -269,15 +266,11 @@ template <bool B> struct BoolC { static constexpr bool value = B; };
 template <class F, int KIND, int NV, int UMAX, int LP = 0>
 struct StreamPass {
     static constexpr int PF = pf_depth<F, UMAX, KIND>();
-#ifndef GS_RING_MIN_PF
-#define GS_RING_MIN_PF 2
-#endif
-    static constexpr bool RING = LP == 64 && PF >= GS_RING_MIN_PF;
+    // (one slot gains nothing from the ring: measured slower on Q6_K's two rows per wave)
+    static constexpr bool RING = LP == 64 && PF >= 2;
     static constexpr int UX = KIND == 1 ? UMAX / 2 : UMAX;       // activation units per lane
-#ifndef GS_XNEG_MAX
-#define GS_XNEG_MAX 4
-#endif
-    static constexpr bool XNEG = NegX<F>::value && UX * NV <= GS_XNEG_MAX;  // -q in registers only while it is cheap
+    // -q in registers only while it is cheap (down's 6 units per lane measured no faster with it)
+    static constexpr bool XNEG = NegX<F>::value && UX * NV <= 4;
     // activation prologue: 4 threads per 32-element unit (8 floats each), XP passes of GS_WG/4
     // units in flight before the weight loads (a decode-sized x is one pass: 2 loads per thread)
     static constexpr int XT = 4, XPU = GS_WG / XT;
@@ -659,9 +652,9 @@ struct StreamPass {
                 }
                 if (ISSUE) {   // kept after the slot's last use: hoisted above it, the loads would
                                // need fresh registers and a full wait at the loop head
-                    GS_RING_SB
+                    __builtin_amdgcn_sched_barrier(0);
                     load_row(p, base + (PF + p) * ngroups);
-                    GS_RING_SB
+                    __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int t = 0; t < NV; t++) {
