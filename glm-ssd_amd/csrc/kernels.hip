@@ -274,7 +274,8 @@ struct StreamPass {
     // activation prologue: 4 threads per 32-element unit (8 floats each), XP passes of GS_WG/4
     // units in flight before the weight loads (a decode-sized x is one pass: 2 loads per thread)
     static constexpr int XT = 4, XPU = GS_WG / XT;
-    static constexpr int XP = KIND == 2 ? 4 : (NV < 4 ? NV : 4);
+    // (down: a row's units, at most 64 * UX for the whole activation set, need UX / 2 passes)
+    static constexpr int XP = KIND == 2 ? (UX / 2 < 1 ? 1 : (UX / 2 > 4 ? 4 : UX / 2)) : (NV < 4 ? NV : 4);
     // paired units: the lane's units j, j+1 (j even) are consecutive units of one block
     static constexpr bool PAIRS = Paired<F>::value && UX % 2 == 0;
     __device__ __forceinline__ int unit_of(int j) const {
