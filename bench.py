@@ -57,6 +57,7 @@ def bench_lib():
     L.bn_moe_ffn.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, I64, C.c_int, C.c_int, I64, P, P, P, C.c_int,
                              C.c_int, P, C.POINTER(C.c_float)]
     L.bn_copy.argtypes = [P, P, C.c_size_t, C.c_int, P, C.POINTER(C.c_float)]
+    L.bn_read.argtypes = [P, C.c_int, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_moe_grouped.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, P, P, P, P, C.c_int, I64, C.c_int, C.c_int, I64, P, P,
                                  P, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     return L
@@ -208,7 +209,24 @@ def run_moe_per_token(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
                 frac_hbm_peak=round(wbytes / t / 1e9 / HBM_PEAK_GBPS, 4), calls_per_step=n_tok, routings_rotated=n_rout)
 
 
-def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 20):
+def run_read_ceiling(L, s, sizes, steps, warmup, pool_bytes=768 << 20):
+    """Plain HBM read (bench_kernels.hip bn_k_read) of each byte count, the start address rotated
+    over a 768 MB pool so no call is served from the last-level cache: the achievable ceiling the
+    streaming kernels are compared with at the same byte count."""
+    import glmssd as G
+    pool = G.DeviceBuffer(pool_bytes)
+    out = {}
+    for n in sizes:
+        n = (n + 4095) // 4096 * 4096
+        nb = max(1, min(64, pool_bytes // n))
+        bases = (C.c_void_p * nb)(*[pool.p.value + i * (pool_bytes // nb) // 4096 * 4096 for i in range(nb)])
+        ms = C.c_float()
+        G.check(L.bn_read(C.cast(bases, C.c_void_p), nb, n, steps, warmup, s.raw(), C.byref(ms)))
+        out[str(n)] = {"bytes": n, "us": round(ms.value * 1e3, 2), "GB/s": round(n / (ms.value * 1e-3) / 1e9, 1)}
+    return out
+
+
+def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 20, B=1):
     import glmssd as G
     rng = np.random.default_rng(seed)
     raw = make(rng, rows, K)
@@ -219,16 +237,29 @@ def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 
         G.check(G.lib().gs_memcpy_d2d(buf.ptr(i * raw.nbytes), buf.p, raw.nbytes, s.raw()))
     s.sync()
     ptrs = (C.c_void_p * n)(*[buf.p.value + i * raw.nbytes for i in range(n)])
-    x = G.DeviceBuffer.from_array(rng.standard_normal(K).astype(np.float32), s)
-    y = G.DeviceBuffer(rows * 4)
+    x = G.DeviceBuffer.from_array(rng.standard_normal(B * K).astype(np.float32), s)
+    y = G.DeviceBuffer(B * rows * 4)
     ms = C.c_float()
-    G.check(L.bn_gemv(ty, C.cast(ptrs, C.c_void_p), n, G.row_bytes(ty, K), K, rows, x.p, y.p, 1, steps, warmup,
+    G.check(L.bn_gemv(ty, C.cast(ptrs, C.c_void_p), n, G.row_bytes(ty, K), K, rows, x.p, y.p, B, steps, warmup,
                       s.raw(), C.byref(ms)))
     return dict(ms=ms.value, bytes=raw.nbytes, gbps=raw.nbytes / (ms.value * 1e-3) / 1e9, copies=n)
 
 
-def cpu_baseline(budget_s=12.0, n_embd=4096, n_ff=1536, seed=2):
-    """Oracle (C port of crates/quants dequantize + f64 dot) on the config-2 FFN, all host cores."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(budget_s=10.0, n_embd=4096, n_ff=1536, seed=2):
+    """Oracle (C port of crates/quants dequantize + f64 dot, the reference CPU path of
+    crates/engine/src/qtest.rs:77-108) on the config-2 FFN: one thread, as the reference runs it,
+    then every host core."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     from glmssd import synth
@@ -239,20 +270,33 @@ def cpu_baseline(budget_s=12.0, n_embd=4096, n_ff=1536, seed=2):
     gate, up, down = [e[0] for e in experts], [e[1] for e in experts], [e[2] for e in experts]
     x = rng.standard_normal((1, n_embd)).astype(np.float32)
     w = synth.softmax(rng.standard_normal(8))
-    cores = min(16, os.cpu_count() or 1)
     rbg, rbd = G.row_bytes(ty, n_embd), G.row_bytes(ty, n_ff)
-    t0 = time.perf_counter()
-    steps = 0
-    while True:
-        O.moe_ffn(ty, ty, gate, up, down, rbg, rbd, n_embd, n_ff, x, [0] * 8, list(range(8)), w, nthreads=cores)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 200:
-            break
     step_bytes = 8 * 3 * n_ff * rbg
-    return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{steps} config-2 steps (8 IQ2_XXS experts, 1 token) in {el:.1f} s, oracle C port "
-                      f"(dequantize + f64 dot), {cores} threads"}
+
+    def timed(threads, budget):
+        t0 = time.perf_counter()
+        steps = 0
+        while True:
+            O.moe_ffn(ty, ty, gate, up, down, rbg, rbd, n_embd, n_ff, x, [0] * 8, list(range(8)), w, nthreads=threads)
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or steps >= 200:
+                return steps, el
+
+    n1, t1 = timed(1, budget_s)
+    host = os.cpu_count() or 1
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host
+    cores = min(16, avail)   # a GPU box's CPU share is 16 threads whatever the host has
+    na, ta = timed(cores, budget_s / 2)
+    model = cpu_model()
+    return {"value": round(step_bytes * n1 / t1 / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n1} config-2 steps (8 IQ2_XXS experts, 1 token) in {t1:.1f} s, oracle C port "
+                      f"(dequantize + f64 dot), 1 thread as the reference CPU path runs",
+            "ms_per_step": round(t1 / n1 * 1e3, 2), "cpu_model": model, "host_cores": host,
+            "cores_available": avail,
+            "all_cores": {"value": round(step_bytes * na / ta / 1e9, 4), "unit": "GB/s", "cores": cores,
+                          "ms_per_step": round(ta / na * 1e3, 2),
+                          "sample": f"{na} config-2 steps in {ta:.1f} s, {cores} threads (rows split)"}}
 
 
 def main():
@@ -311,6 +355,15 @@ def main():
         r1 = run_gemv(L, s, G.GgmlType.Q8_0, 4096, 4096, synth.q8_0_matrix, args.steps, args.warmup, 1)
         r3a = run_gemv(L, s, G.GgmlType.Q4_K, 12288, 4096, synth.q4_k_matrix, args.steps, args.warmup, 3)
         r3b = run_gemv(L, s, G.GgmlType.Q6_K, 4096, 12288, synth.q6_k_matrix, args.steps, args.warmup, 4)
+        for B in (2, 4, 8):
+            rb = run_gemv(L, s, G.GgmlType.Q8_0, 4096, 4096, synth.q8_0_matrix, args.steps, args.warmup, 1, B=B)
+            secondary[f"config1_q8_0_gemv_4096x4096_B{B}"] = {
+                "GB/s": round(rb["gbps"], 1), "us_per_call": round(rb["ms"] * 1e3, 2),
+                "frac_hbm_peak": round(rb["gbps"] / HBM_PEAK_GBPS, 4), "weight_bytes": rb["bytes"], "vectors": B}
+            log(f"config1 B={B}: {rb['ms'] * 1e3:.2f} us, {rb['gbps']:.1f} GB/s")
+        rc = run_read_ceiling(L, s, [17825792, 25952256, 38928384, 41287680, 1 << 30], args.steps, args.warmup)
+        secondary["plain_read_ceiling"] = rc
+        log(f"plain-read ceiling: {rc}")
         for name, r in [("config1_q8_0_gemv_4096x4096", r1), ("config3_q4_k_gemv_k4096_rows12288", r3a),
                         ("config3_q6_k_gemv_k12288_rows4096", r3b)]:
             secondary[name] = {"GB/s": round(r["gbps"], 1), "us_per_call": round(r["ms"] * 1e3, 2),

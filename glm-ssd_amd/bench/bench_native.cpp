@@ -136,3 +136,47 @@ BN_EXPORT int bn_copy(void *dst, const void *src, size_t n, int reps, void *s, f
     *ms /= reps;
     return 0;
 }
+
+// ---- plain-read ceiling ------------------------------------------------------------------------
+#include <hip/hip_runtime_api.h>
+extern "C" const unsigned char bn_blob_start[];
+
+// Read `bytes` (a multiple of 16) starting at bases[i % nb] per call (the rotation keeps the reads
+// out of the last-level cache), `steps` calls after `warmup`; mean ms per call.
+BN_EXPORT int bn_read(const void *const *bases, int nb, size_t bytes, int steps, int warmup, void *s, float *ms) {
+    static hipModule_t mod = nullptr;
+    static hipFunction_t fn = nullptr;
+    static uint32_t *sink = nullptr;
+    if (!mod) {
+        CK(hipModuleLoadData(&mod, bn_blob_start));
+        CK(hipModuleGetFunction(&fn, mod, "bn_k_read"));
+        CK(hipMalloc((void **)&sink, 256));
+    }
+    int cus = 0;
+    CK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    const int64_t n16 = (int64_t)(bytes / 16);
+    const int64_t want = (n16 + 512 * 4 - 1) / (512 * 4);
+    const unsigned grid = (unsigned)(want < 1 ? 1 : (want > 4 * cus ? 4 * cus : want));
+    struct {
+        const void *p;
+        int64_t n16;
+        uint32_t *sink;
+    } args;
+    size_t sz = sizeof(args);
+    auto call = [&](int i) {
+        args = {bases[i % nb], n16, sink};
+        void *cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz, HIP_LAUNCH_PARAM_END};
+        return (int)hipModuleLaunchKernel(fn, grid, 1, 1, 512, 1, 1, 0, (hipStream_t)s, nullptr, cfg);
+    };
+    Timer t;
+    CK(t.init());
+    for (int i = 0; i < warmup; i++) CK(call(i));
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    for (int i = 0; i < steps; i++) CK(call(warmup + i));
+    CK(gs_event_record(t.b, s));
+    CK(gs_event_sync(t.b));
+    CK(gs_event_elapsed_ms(ms, t.a, t.b));
+    *ms /= steps;
+    return 0;
+}

@@ -1,10 +1,9 @@
 // gfx950 device-side decoders of the ggml block formats.
 //
 // Two families:
-//   * deq8_*  : exact dequantization of the 8 elements [8g, 8g+8) of one block, bit-identical to
-//               the CPU reference (crates/quants/src/lib.rs:131-343). Used by gs_dequant_* and by
-//               the generic matmul path. The f32 operation order is the reference's and FP
-//               contraction is off in this section, so no multiply-add gets fused.
+//   * exact::* (exact.h): exact dequantization of one 32-element unit, bit-identical to the CPU
+//               reference (crates/quants/src/lib.rs:131-343). Used by gs_dequant_* and by the
+//               generic matmul path.
 //   * F*::load/dot : the fast integer paths for Q8_0 / Q4_K / Q6_K / IQ2_XXS. load() fetches one
 //               32-element "unit" of a weight row straight from HBM into registers; dot() decodes it
 //               and dots it with up to NV q8_1 activation units held in registers (v_dot4_i32_i8),
@@ -36,151 +35,8 @@ __device__ __forceinline__ uint32_t rb32(const uint8_t *p, int i) {
 // ksigns_iq2xs[i] == i | parity(i) << 7  (closed form of crates/quants/src/tables.rs:9-18)
 __device__ __forceinline__ uint32_t ksigns(uint32_t i) { return i | ((__builtin_popcount(i) & 1u) << 7); }
 
-// =============================================================================================
-// Exact decoders (bit-identical to crates/quants/src/lib.rs)
-// =============================================================================================
-#pragma clang fp contract(off)
-
-__device__ __forceinline__ void scale_min_k4(int j, const uint8_t *q, uint32_t &sc, uint32_t &m) {
-    if (j < 4) {
-        sc = q[j] & 63;
-        m = q[j + 4] & 63;
-    } else {
-        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-    }
-}
-
-// block_q8_0 { half d; int8 qs[32]; }  lib.rs:131-136
-__device__ __forceinline__ void deq8_q8_0(const uint8_t *b, int g, float *v) {
-    const float d = h2f(rb16(b, 0));
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = (float)(int8_t)b[2 + 8 * g + i] * d;
-}
-// block_q2_K { u8 scales[16]; u8 qs[64]; half d; half dmin; }  lib.rs:139-160
-__device__ __forceinline__ void deq8_q2_k(const uint8_t *b, int g, float *v) {
-    const int e0 = 8 * g, half = e0 >> 7, r = e0 & 127, j = r >> 5, part = (r >> 4) & 1, l0 = r & 15;
-    const uint32_t sc = b[8 * half + 2 * j + part];
-    const float dl = h2f(rb16(b, 80)) * (float)(sc & 15), ml = h2f(rb16(b, 82)) * (float)(sc >> 4);
-    const uint8_t *q = b + 16 + 32 * half + 16 * part + l0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = dl * (float)((q[i] >> (2 * j)) & 3) - ml;
-}
-// block_q3_K { u8 hmask[32]; u8 qs[64]; u8 scales[12]; half d; }  lib.rs:163-201
-__device__ __forceinline__ void deq8_q3_k(const uint8_t *b, int g, float *v) {
-    const int e0 = 8 * g, half = e0 >> 7, r = e0 & 127, j = r >> 5, part = (r >> 4) & 1, l0 = r & 15;
-    const int is = 8 * half + 2 * j + part;
-    const uint8_t *raw = b + 96;
-    const int low = is < 8 ? (raw[is] & 15) : (raw[is - 8] >> 4);
-    const int high = (raw[8 + (is & 3)] >> (2 * (is >> 2))) & 3;
-    const float dl = h2f(rb16(b, 108)) * (float)((low | (high << 4)) - 32);
-    const uint32_t m = 1u << (4 * half + j);
-    const uint8_t *hm = b + 16 * part + l0;
-    const uint8_t *q = b + 32 + 32 * half + 16 * part + l0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = dl * (float)((int)((q[i] >> (2 * j)) & 3) - ((hm[i] & m) ? 0 : 4));
-}
-// block_q4_K { half d; half dmin; u8 scales[12]; u8 qs[128]; }  lib.rs:204-218
-__device__ __forceinline__ void deq8_q4_k(const uint8_t *b, int g, float *v) {
-    const int e0 = 8 * g, jb = e0 >> 6, hi = (e0 >> 5) & 1, l0 = e0 & 31;
-    uint32_t sc, mn;
-    scale_min_k4(2 * jb + hi, b + 4, sc, mn);
-    const float d = h2f(rb16(b, 0)) * (float)sc, m = h2f(rb16(b, 2)) * (float)mn;
-    const uint8_t *q = b + 16 + 32 * jb + l0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = d * (float)(hi ? (q[i] >> 4) : (q[i] & 15)) - m;
-}
-// block_q5_K { half d; half dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]; }  lib.rs:221-240
-__device__ __forceinline__ void deq8_q5_k(const uint8_t *b, int g, float *v) {
-    const int e0 = 8 * g, jb = e0 >> 6, hi = (e0 >> 5) & 1, l0 = e0 & 31;
-    uint32_t sc, mn;
-    scale_min_k4(2 * jb + hi, b + 4, sc, mn);
-    const float d = h2f(rb16(b, 0)) * (float)sc, m = h2f(rb16(b, 2)) * (float)mn;
-    const uint8_t *qh = b + 16 + l0, *q = b + 48 + 32 * jb + l0;
-    const int hb = 2 * jb + hi;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const uint32_t lo = hi ? (q[i] >> 4) : (q[i] & 15);
-        v[i] = d * (float)(lo + (((qh[i] >> hb) & 1) << 4)) - m;
-    }
-}
-// block_q6_K { u8 ql[128]; u8 qh[64]; i8 scales[16]; half d; }  lib.rs:243-262
-__device__ __forceinline__ void deq8_q6_k(const uint8_t *b, int g, float *v) {
-    const int e0 = 8 * g, half = e0 >> 7, r = e0 & 127, quarter = r >> 5, l0 = r & 31;
-    const uint8_t *ql = b + 64 * half + l0 + 32 * (quarter & 1);
-    const uint8_t *qh = b + 128 + 32 * half + l0;
-    const float dsc = h2f(rb16(b, 208)) * (float)(int8_t)b[192 + 8 * half + (l0 >> 4) + 2 * quarter];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int nib = quarter >= 2 ? (ql[i] >> 4) : (ql[i] & 15);
-        const int hb = (qh[i] >> (2 * quarter)) & 3;
-        v[i] = dsc * (float)((nib | (hb << 4)) - 32);
-    }
-}
-__device__ __forceinline__ void grid8_signed(uint64_t grid, uint32_t signs, float db, float *v) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const float x = db * (float)((grid >> (8 * j)) & 0xff);
-        v[j] = ((signs >> j) & 1) ? -x : x;
-    }
-}
-// block_iq2_xxs { half d; u16 qs[32]; }  lib.rs:274-288
-__device__ __forceinline__ void deq8_iq2_xxs(const uint8_t *b, int g, float *v) {
-    const int ib32 = g >> 2, l = g & 3;
-    const uint32_t a0 = rb32(b, 2 + 8 * ib32), a1 = rb32(b, 6 + 8 * ib32);
-    const float db = h2f(rb16(b, 0)) * (0.5f + (float)(a1 >> 28)) * 0.25f;
-    grid8_signed(iq2xxs_grid[(a0 >> (8 * l)) & 0xff], ksigns((a1 >> (7 * l)) & 127), db, v);
-}
-// block_iq2_s { half d; u8 qs[32]; u8 signs[32]; u8 qh[8]; u8 scales[8]; }  lib.rs:291-310
-__device__ __forceinline__ void deq8_iq2_s(const uint8_t *b, int g, float *v) {
-    const int ib32 = g >> 2, l = g & 3;
-    const float dl = h2f(rb16(b, 0)) * (0.5f + (float)((b[74 + ib32] >> (4 * (l >> 1))) & 15)) * 0.25f;
-    const int idx = b[2 + 4 * ib32 + l] | ((b[66 + ib32] << (8 - 2 * l)) & 0x300);
-    grid8_signed(iq2s_grid[idx], b[34 + 4 * ib32 + l], dl, v);
-}
-// block_iq3_xxs { half d; u8 qs[64]; u8 scales_and_signs[32]; }  lib.rs:312-328
-__device__ __forceinline__ void deq8_iq3_xxs(const uint8_t *b, int g, float *v) {
-    const int ib32 = g >> 2, l = g & 3;
-    const uint32_t aux = rb32(b, 66 + 4 * ib32);
-    const float db = h2f(rb16(b, 0)) * (0.5f + (float)(aux >> 28)) * 0.5f;
-    const uint64_t g1 = iq3xxs_grid[b[2 + 8 * ib32 + 2 * l]], g2 = iq3xxs_grid[b[2 + 8 * ib32 + 2 * l + 1]];
-    grid8_signed(g1 | (g2 << 32), ksigns((aux >> (7 * l)) & 127), db, v);
-}
-// block_iq4_xs { half d; u16 scales_h; u8 scales_l[4]; u8 qs[128]; }  lib.rs:331-343
-__device__ __forceinline__ void deq8_iq4_xs(const uint8_t *b, int g, float *v) {
-    const int e0 = 8 * g, ib = e0 >> 5, hi = (e0 >> 4) & 1, j0 = e0 & 15;
-    const uint32_t scales_h = rb16(b, 2);
-    const int ls = ((b[4 + (ib >> 1)] >> (4 * (ib & 1))) & 15) | (((scales_h >> (2 * ib)) & 3) << 4);
-    const float dl = h2f(rb16(b, 0)) * (float)(ls - 32);
-    const uint8_t *q = b + 8 + 16 * ib + j0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = dl * (float)kvalues_iq4nl[hi ? (q[i] >> 4) : (q[i] & 15)];
-}
-// 8 consecutive plain elements
-__device__ __forceinline__ void deq8_f32(const uint8_t *b, int, float *v) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(float, rb32(b, 4 * i));
-}
-__device__ __forceinline__ void deq8_f16(const uint8_t *b, int, float *v) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = h2f(rb16(b, 2 * i));
-}
-__device__ __forceinline__ void deq8_bf16(const uint8_t *b, int, float *v) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(float, rb16(b, 2 * i) << 16);
-}
-
-#pragma clang fp contract(fast)
-
-// Type traits. QK = elements per block, BB = bytes per block (types.rs:85-113).
-// For QK < 8 (plain types) one "block" here is 8 elements so deq8 always sees a whole group.
-// X(type id, QK, BB, decoder); the id is spelled as a number because it names kernels
-#define GS_TYPE_LIST(X)                                                                         \
-    X(0, 8, 32, deq8_f32) X(1, 8, 16, deq8_f16) X(30, 8, 16, deq8_bf16)                         \
-    X(8, 32, 34, deq8_q8_0) X(10, 256, 84, deq8_q2_k) X(11, 256, 110, deq8_q3_k)               \
-    X(12, 256, 144, deq8_q4_k) X(13, 256, 176, deq8_q5_k) X(14, 256, 210, deq8_q6_k)           \
-    X(16, 256, 66, deq8_iq2_xxs) X(22, 256, 82, deq8_iq2_s)                                    \
-    X(18, 256, 98, deq8_iq3_xxs) X(23, 256, 136, deq8_iq4_xs)
+__device__ __forceinline__ uint32_t ksigns_of(uint32_t i) { return ksigns(i); }
+#include "exact.h"
 
 // =============================================================================================
 // Fast unit dot products against q8_1 activations
@@ -523,14 +379,6 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
     __device__ static __forceinline__ void fetch(const Raw &w, Dec &e) {
         const uint32_t gofs[4] = {grid_off<0>(w.a.x), grid_off<1>(w.a.x), grid_off<2>(w.a.x), grid_off<3>(w.a.x)};
         const uint32_t sofs[4] = {sel_off<0>(w.a.y), sel_off<1>(w.a.y), sel_off<2>(w.a.y), sel_off<3>(w.a.y)};
-#ifdef GS_PROBE_NOLDS   // profiling build only: table words replaced by their offsets (wrong results)
-#pragma unroll
-        for (int l = 0; l < 4; l++) {
-            e.g[l] = make_uint2(gofs[l], gofs[l] ^ 0x01010101u);
-            e.s[l] = make_uint2(sofs[l], sofs[l] ^ 0x02020202u);
-        }
-        return;
-#endif
 #pragma unroll
         for (int l = 0; l < 4; l++) {
             e.g[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_grid_lds + gofs[l]);
@@ -640,7 +488,7 @@ struct FIQ3_XXS : UnitGeom<256, 98> {
 //
 // The plain float formats (F32, F16, BF16 — the router and other unquantized matrices) take the
 // activations in f32, as the reference's GEMV does for every type (quants.cu:81-96): F32X.
-template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float *)>
+template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float (&)[32])>
 struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
     static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0, RAW = 2;
     static constexpr bool F32X = T == GS_F32 || T == GS_F16 || T == GS_BF16;
@@ -651,13 +499,7 @@ struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
     __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {
         float v[32];
-        if (QK >= 32) {
-#pragma unroll
-            for (int g = 0; g < 4; g++) DEQ(w.p, 4 * j + g, v + 8 * g);
-        } else {
-#pragma unroll
-            for (int g = 0; g < 4; g++) DEQ(w.p + g * BB, 0, v + 8 * g);
-        }
+        DEQ(w.p, QK >= 32 ? j : 0, v);   // plain types: w.p is the unit's first element
 #pragma unroll
         for (int t = 0; t < NV; t++) {
             if (t < nv) {
@@ -674,11 +516,11 @@ struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
         }
     }
 };
-using FF32 = FGeneric<GS_F32, 8, 32, deq8_f32>;
-using FF16 = FGeneric<GS_F16, 8, 16, deq8_f16>;
-using FBF16 = FGeneric<GS_BF16, 8, 16, deq8_bf16>;
-using FQ2_K = FGeneric<GS_Q2_K, 256, 84, deq8_q2_k>;
-using FQ3_K = FGeneric<GS_Q3_K, 256, 110, deq8_q3_k>;
-using FQ5_K = FGeneric<GS_Q5_K, 256, 176, deq8_q5_k>;
-using FIQ2_S = FGeneric<GS_IQ2_S, 256, 82, deq8_iq2_s>;
-using FIQ4_XS = FGeneric<GS_IQ4_XS, 256, 136, deq8_iq4_xs>;
+using FF32 = FGeneric<GS_F32, 8, 32, exact::f32>;
+using FF16 = FGeneric<GS_F16, 8, 16, exact::f16>;
+using FBF16 = FGeneric<GS_BF16, 8, 16, exact::bf16>;
+using FQ2_K = FGeneric<GS_Q2_K, 256, 84, exact::q2_k>;
+using FQ3_K = FGeneric<GS_Q3_K, 256, 110, exact::q3_k>;
+using FQ5_K = FGeneric<GS_Q5_K, 256, 176, exact::q5_k>;
+using FIQ2_S = FGeneric<GS_IQ2_S, 256, 82, exact::iq2_s>;
+using FIQ4_XS = FGeneric<GS_IQ4_XS, 256, 136, exact::iq4_xs>;

@@ -111,40 +111,7 @@ __device__ __forceinline__ h8 frag_finish(const FragRaw &r) {
     return __builtin_bit_cast(h8, make_uint4(g.x ^ m.x, g.y ^ m.y, g.z ^ m.z, g.w ^ m.w));
 }
 
-// profiling variants replace single components of the contraction
-#ifdef GS_GRP_PROBE_NOLDSA
-#define GS_GRP_AV(p) __builtin_bit_cast(h8, make_uint4(cc, j, 0, tt))
-#else
-#define GS_GRP_AV(p) __builtin_bit_cast(h8, *(const uint4 *)(p))
-#endif
-#ifdef GS_GRP_PROBE_NOBAR   // profiling variant: activation fragments from L2, no staging barrier
-#define GS_GRP_AV_LOAD(tt, cc) __builtin_bit_cast(h8, *(const GS_GLOBAL u4 *)(const GS_GLOBAL uint16_t *)(a.act + ((uint32_t)ar_cur[0] * (uint32_t)K + 256u * b + 8u * (cc) + 16u * (tt))))
-#else
-#define GS_GRP_AV_LOAD(tt, cc) GS_GRP_AV(slab + (16 * (tt) + j) * 512 + (((cc) ^ j) << 4))
-#endif
-#ifdef GS_GRP_PROBE_NOMFMA
-#define GS_GRP_MFMA(A, B, C) ((C) + __builtin_bit_cast(f4, (A) + (B)))
-#else
-#define GS_GRP_MFMA(A, B, C) __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, C, 0, 0, 0)
-#endif
-
-// profiling variant: per-wave cycle sums of the loop phases, written over the first rows of the
-// kernel's output at exit (results are then meaningless; timing runs only)
-#ifdef GS_GRP_PROBE_TS
-#define GS_TS_DECL uint64_t ts_acc[6] = {0, 0, 0, 0, 0, 0}; uint64_t ts_prev = __builtin_readcyclecounter(); const uint64_t ts_begin = ts_prev;
-#define GS_TS_MARK(i) { const uint64_t now_ = __builtin_readcyclecounter(); ts_acc[i] += now_ - ts_prev; ts_prev = now_; }
-#define GS_TS_DUMP(out)                                                                           \
-    if ((threadIdx.x & 63) == 0) {                                                                \
-        float *o_ = (out) + ((size_t)blockIdx.x * WV + (threadIdx.x >> 6)) * 8;                     \
-        for (int i_ = 0; i_ < 6; i_++) o_[i_] = (float)ts_acc[i_];                                \
-        o_[6] = (float)(__builtin_readcyclecounter() - ts_begin);                                 \
-        o_[7] = 1.f;                                                                              \
-    }
-#else
-#define GS_TS_DECL
-#define GS_TS_MARK(i)
-#define GS_TS_DUMP(out)
-#endif
+#define GS_GRP_AV_LOAD(tt, cc) __builtin_bit_cast(h8, *(const uint4 *)(slab + (16 * (tt) + j) * 512 + ((((cc) ^ j)) << 4)))
 
 __device__ __forceinline__ float grp_swiglu(float g, float u, float lim) {   // ops.cu:101-115
     if (lim > 0.f) {
@@ -286,11 +253,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         for (int n = 0; n < NR; n++)
 #pragma unroll
             for (int mt = 0; mt < MATS; mt++) {
-#ifdef GS_GRP_PROBE_NOWLOAD   // profiling variant: every position re-reads super-block 0 (cache hits)
-                const uint8_t *p = d.wb[mt] + wo[n];
-#else
                 const uint8_t *p = d.wb[mt] + (wo[n] + BB * b);
-#endif
                 w.q[n][mt] = ldg16(p);
                 if (IQ3) w.sg[n][mt] = ldg8(p + 64 - 8 * q);   // block + 66 + 8q
                 w.d[n][mt] = ldg2(p - 2 - 16 * q);
@@ -301,11 +264,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         for (int k = 0; k < NLD; k++) {
             const int z = tid + NTH * k;
             if (NCH % NTH != 0 && z >= NCH) continue;
-#ifdef GS_GRP_PROBE_NOSTG   // profiling variant: no activation staging loads
-            stg[k] = u4{(uint32_t)ar[k], (uint32_t)b, (uint32_t)z, 0u};
-#else
             stg[k] = *(const GS_GLOBAL u4 *)(const GS_GLOBAL uint16_t *)(a.act + ((uint32_t)ar[k] * (uint32_t)K + 256u * b + 8u * (z & 31)));
-#endif
         }
     };
 
@@ -349,7 +308,6 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             for (int mt = 0; mt < MATS; mt++) acc[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
 
     int b = 0, buf = 0;
-    GS_TS_DECL
     auto step = [&](WRegs &wu, WRegs &wl) __attribute__((always_inline)) -> bool {
         // ---- issue: activations of position +1, weights of position +2 -------------------
         const bool last_sb = b == nsb - 1;
@@ -380,7 +338,6 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 for (int i = 0; i < 4; i++) ep_sc[tt][i] = a.ascale[ep_tok[tt][i]];
         }
 
-        GS_TS_MARK(0)
         // ---- contract position (cur, b) ------------------------------------------------------
         {
             const uint8_t *slab = stage + buf * SLAB;
@@ -414,7 +371,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 const h8 av = GS_GRP_AV_LOAD(tt, cc);                                              \
                 _Pragma("unroll") for (int n = 0; n < NR; n++)                                     \
                 _Pragma("unroll") for (int mt = 0; mt < MATS; mt++)                                \
-                    sb[tt][n][mt] = GS_GRP_MFMA(av, bf[n][mt], sb[tt][n][mt]);                     \
+                    sb[tt][n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[n][mt], sb[tt][n][mt], 0, 0, 0);                     \
             }                                                                                      \
     }
                 GS_GRP_STEP(0) GS_GRP_STEP(1) GS_GRP_STEP(2) GS_GRP_STEP(3)
@@ -430,7 +387,6 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 }
         }
 
-        GS_TS_MARK(1)
         // ---- tile epilogue: lane holds tokens 16t + 4q + i (i < 4) of row row0 + 16n + j ----
         if (last_sb) {
 #pragma unroll
@@ -461,7 +417,6 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 #pragma unroll
                     for (int mt = 0; mt < MATS; mt++) acc[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
         }
-        GS_TS_MARK(2)
         if (!have1) return false;
 
         // ---- advance: stage position +1, rotate the weight registers -------------------------
@@ -469,7 +424,6 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         for (int k = 0; k < NLD; k++)
             if (NCH % NTH == 0 || tid + NTH * k < NCH) *(u4 *)(stage + (buf ^ 1) * SLAB + dst[k]) = stg[k];
         buf ^= 1;
-        GS_TS_MARK(3)
         if (last_sb) {   // enter the next tile; fetch the one after it
             b = 0;
             t += tstep;
@@ -488,11 +442,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         } else {
             b++;
         }
-        GS_TS_MARK(4)
-#ifndef GS_GRP_PROBE_NOBAR
         __syncthreads();
-#endif
-        GS_TS_MARK(5)
         return true;
     };
     for (;;) {
@@ -500,7 +450,6 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         if (!step(W1, W0)) break;
         if (!step(W2, W1)) break;
     }
-    GS_TS_DUMP(a.out)
 }
 
 #define GS_GRP_KERNEL1(TY, KIND, NT, NR, WV)                                                     \

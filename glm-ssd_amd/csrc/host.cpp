@@ -20,6 +20,8 @@
 #include "../../include/glmssd.h"
 #include "kargs.h"
 
+#define GS_BAR_SLOTS 64   // grid-barrier counter slots per code object (gridbar.h)
+
 #define GS_EXPORT extern "C" __attribute__((visibility("default")))
 
 // ---- embedded code objects --------------------------------------------------------------------
@@ -50,6 +52,7 @@ struct DeviceCtx {
     size_t max_lds = 0;
     hipError_t init_err = hipSuccess;
     std::map<std::pair<std::string, int>, int> occ;  // (kernel, lds) -> blocks per CU
+    std::atomic<uint64_t> bar_seq{0};                // fused-FFN launches (grid-barrier slot rotation)
 };
 
 std::mutex g_mu;
@@ -81,22 +84,9 @@ DeviceCtx *ctx(hipError_t *err) {
         }
     }
     if (e == hipSuccess) {
-        // profiling builds only: GLMSSD_GROUPED_HSACO names a code object that replaces the
-        // embedded grouped-GEMM one (kernel variants are timed without relinking the library)
-        std::vector<char> grouped_override;
-        if (const char *path = getenv("GLMSSD_GROUPED_HSACO")) {
-            if (FILE *f = fopen(path, "rb")) {
-                char buf[1 << 16];
-                size_t n;
-                while ((n = fread(buf, 1, sizeof buf, f)) > 0) grouped_override.insert(grouped_override.end(), buf, buf + n);
-                fclose(f);
-            }
-            if (grouped_override.empty()) fprintf(stderr, "glmssd: cannot read %s\n", path);
-        }
         for (const Blob &b : blobs()) {
             hipModule_t m;
-            const bool swap = !grouped_override.empty() && b.p == gs_blob_grouped_start;
-            e = hipModuleLoadData(&m, swap ? (const void *)grouped_override.data() : (const void *)b.p);
+            e = hipModuleLoadData(&m, (const void *)b.p);
             if (e != hipSuccess) break;
             c->mods.push_back(m);
         }
@@ -185,12 +175,7 @@ hipError_t plan_stream(DeviceCtx *c, int kind, int ty, StreamArgs &a, StreamPlan
                 : NVt == 4 ? std::vector<int>{1, 2} : std::vector<int>{1};
     int best_lpr = -1, best_um = 0;
     double best_eff = -1.0;
-    // GLMSSD_LPR_GU / GLMSSD_LPR_DN: tuning override of the lane-group width (16, 32 or 64)
-    static const int lpr_gu = getenv("GLMSSD_LPR_GU") ? atoi(getenv("GLMSSD_LPR_GU")) : 0;
-    static const int lpr_dn = getenv("GLMSSD_LPR_DN") ? atoi(getenv("GLMSSD_LPR_DN")) : 0;
-    const int force = kind == 1 ? lpr_gu : kind == 2 ? lpr_dn : 0;
     for (int lpr : {64, 32, 16}) {
-        if (force && lpr != force) continue;
         const int upl = (tot + lpr - 1) / lpr;
         int um = 0;
         for (int u : umaxes)
@@ -243,13 +228,11 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
                              std::to_string(NVt) + "_" + std::to_string(P.um) + (w64 ? "_w" : "");
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
-    const int per_cu = std::max(1, blocks_per_cu(c, name, f, P.lds));
     const int G = GS_WG / a.lpr;
     const int nrow = kind == 1 ? a.nseg * a.rows : a.rows;
     // one workgroup per CU by default: each workgroup pays the activation prologue once, and the
     // row pipeline inside it supplies the memory parallelism
-    static const int gmult = getenv("GLMSSD_GRID_MULT") ? std::max(1, atoi(getenv("GLMSSD_GRID_MULT"))) : 1;
-    int grid = std::max(1, std::min((nrow + G - 1) / G, c->cu_count * std::min(gmult, per_cu)));
+    int grid = std::max(1, std::min((nrow + G - 1) / G, c->cu_count));
     if (kind == 1) {   // waves are pinned to experts: at least one per expert, a whole number each
         const int wpw = GS_WG / 64;
         const int waves = std::max(grid * wpw, a.nseg) / a.nseg * a.nseg;
@@ -347,9 +330,9 @@ GS_EXPORT int gs_saxpy(int n, float a, const float *x, float *y, void *s) {
 static int dequant(int ty, const void *src, int64_t n, void *dst, void *s, const char *suffix) {
     int qk, bb;
     if (n <= 0 || n % 8 != 0 || !geometry(ty, qk, bb) || n % ggml_block_elems(ty) != 0) return hipErrorInvalidValue;
-    DequantArgs a{(const uint8_t *)src, dst, n / 8};
+    DequantArgs a{(const uint8_t *)src, dst, n, (n + 31) / 32, aligned16(dst)};
     const std::string name = std::string("gs_k_dequant_") + suffix + "_" + std::to_string(ty);
-    return launch(name, dim3((unsigned)((a.n_groups + 255) / 256)), dim3(256), 0, (hipStream_t)s, a);
+    return launch(name, dim3((unsigned)((a.n_units + 255) / 256)), dim3(256), 0, (hipStream_t)s, a);
 }
 GS_EXPORT int gs_dequant_f32(int ty, const void *src, int64_t n, float *dst, void *s) {
     return dequant(ty, src, n, dst, s, "f32");
@@ -519,7 +502,7 @@ static bool ffn_pair(int ty_gu, int ty_dn) {
 
 // Routed-expert FFN of one layer: exactly gs_moe_gateup followed by gs_moe_down (h is written
 // too). For one token whose down pass fits one launch this is a single fused launch (gate/up,
-// grid barrier, down); otherwise, or with GLMSSD_NO_FFN_FUSION set, the two launches.
+// grid barrier, down); otherwise the two launches.
 // bound of the fused FFN's grid-barrier wait, in ticks of the 100 MHz clock (0.2 s)
 constexpr uint64_t kFfnWaitTicks = 20000000ull;
 std::atomic<uint64_t> g_ffn_wait_ticks{kFfnWaitTicks};
@@ -557,8 +540,7 @@ GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int6
     int rc = moe_check(ty_gu, b, nt, n_embd, n_ff, rs_gu);
     if (rc) return rc;
     if ((rc = moe_check(ty_dn, b, nt, n_ff, n_embd, rs_dn))) return rc;
-    static const bool no_fusion = getenv("GLMSSD_NO_FFN_FUSION") != nullptr;
-    bool fuse = !no_fusion && nt == 1 && ffn_pair(ty_gu, ty_dn) && b->n <= down_per_launch(nt, n_ff);
+    bool fuse = nt == 1 && ffn_pair(ty_gu, ty_dn) && b->n <= down_per_launch(nt, n_ff);
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
@@ -572,6 +554,7 @@ GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int6
     }
     if (fuse) {
         fa.wait_ticks = g_ffn_wait_ticks.load();
+        fa.slot = (int)(c->bar_seq.fetch_add(1) % GS_BAR_SLOTS);
         const std::string name = "gs_k_ffn_" + std::to_string(ty_gu) + "_" + std::to_string(ty_dn) + "_" +
                                  std::to_string(P1.um) + "_" + std::to_string(P2.um);
         const size_t lds = std::max(P1.lds, P2.lds);
@@ -679,9 +662,6 @@ hipError_t grouped_launch(int kind, int ty, GroupedArgs &a, int n_pairs, hipStre
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
-    auto env = [](const char *n) { return getenv(n) ? atoi(getenv(n)) : 0; };
-    static const int nt1 = env("GLMSSD_GRP_NT1"), nr1 = env("GLMSSD_GRP_NR1"), wv1 = env("GLMSSD_GRP_WV1");
-    static const int nt2 = env("GLMSSD_GRP_NT2"), nr2 = env("GLMSSD_GRP_NR2"), wv2 = env("GLMSSD_GRP_WV2");
     static const std::vector<GrpShape> all1 = {{1, 1, 8}, {1, 2, 8}, {2, 1, 8}, {2, 2, 8}, {4, 1, 8}, {1, 1, 16}};
     static const std::vector<GrpShape> all2 = {{1, 1, 8}, {1, 2, 8}, {1, 4, 8}, {2, 1, 8}, {2, 2, 8}, {2, 4, 8},
                                                {4, 1, 8}, {4, 2, 8}, {1, 1, 16}, {1, 2, 16}, {2, 1, 16}};
@@ -699,10 +679,6 @@ hipError_t grouped_launch(int kind, int ty, GroupedArgs &a, int n_pairs, hipStre
         sh = p;
         if (tiles(p) >= 2 * (int64_t)c->cu_count) break;
     }
-    const int ent = kind == 1 ? nt1 : nt2, enr = kind == 1 ? nr1 : nr2, ewv = kind == 1 ? wv1 : wv2;
-    if (ent > 0) sh.nt = ent;
-    if (enr > 0) sh.nr = enr;
-    if (ewv > 0) sh.wv = ewv;
     const auto &all = kind == 1 ? all1 : all2;
     if (std::none_of(all.begin(), all.end(),
                      [&](const GrpShape &p) { return p.nt == sh.nt && p.nr == sh.nr && p.wv == sh.wv; }))
@@ -787,28 +763,3 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
 }
 
 
-#ifdef GS_STREAM_TS
-// profiling build only: copy the per-wave phase timestamps of the last stream launch
-GS_EXPORT int gs_debug_stream_timestamps(void *host, size_t n) {
-    hipError_t e;
-    DeviceCtx *c = ctx(&e);
-    if (!c) return e;
-    for (hipModule_t m : c->mods) {
-        hipDeviceptr_t p;
-        size_t sz;
-        if (hipModuleGetGlobal(&p, &sz, m, "gs_stream_ts") == hipSuccess) {
-            // every per-format code object has its own copy; the launched one holds nonzero data
-            std::vector<unsigned long long> tmp(sz / 8);
-            if ((e = hipMemcpy(tmp.data(), p, sz, hipMemcpyDeviceToHost)) != hipSuccess) return e;
-            bool any = false;
-            for (auto v : tmp) any |= v != 0;
-            if (any) {
-                memcpy(host, tmp.data(), std::min(n, sz));
-                return hipMemset(p, 0, sz);
-            }
-        }
-    }
-    (void)hipGetLastError();
-    return hipErrorNotFound;
-}
-#endif

@@ -51,13 +51,16 @@ struct FfnArgs {
     StreamArgs gu;         // kind 1: gate/up -> h
     StreamArgs dn;         // kind 2: h -> y (accumulated)
     uint64_t wait_ticks;   // bound of the grid-barrier wait (100 MHz clock ticks)
+    int slot;              // barrier counter slot of this launch (0 .. GS_BAR_SLOTS-1)
 };
 
 // Whole-tensor dequantization
 struct DequantArgs {
     const uint8_t *src;
     void *dst;
-    int64_t n_groups;   // 8-element groups
+    int64_t n;          // elements
+    int64_t n_units;    // 32-element units (the last one may be partial for plain types)
+    int aligned;        // dst is 16-byte aligned (vector stores)
 };
 
 // q8_1 quantization of f32 rows: out = n/32 blocks of {f16 d; f16 s; int8 qs[32]}

@@ -5,6 +5,7 @@
 #include <stdint.h>
 #include "kargs.h"
 #include "formats.h"
+#include "gridbar.h"
 
 // =============================================================================================
 // q8_1 activation quantization of one 32-element unit, in registers.
@@ -203,16 +204,6 @@ __device__ __forceinline__ XU load_xu(const uint8_t *xq, const uint32_t *xm, int
 // unconditionally (rows past the end are clamped to a valid row and their results dropped), so
 // the waits before each row are exact in-order counts and decoding row 0 overlaps the arrival of
 // rows 1..PF-1. Results are stored after the batch.
-#ifdef GS_STREAM_TS
-// profiling build only: per-wave phase timestamps (100 MHz s_memrealtime)
-__device__ unsigned long long gs_stream_ts[1 << 16];
-#define GS_TS(i, extra)                                                                          \
-    if ((threadIdx.x & 63) == 0)                                                                \
-        gs_stream_ts[((size_t)blockIdx.x * (GS_WG / 64) + (threadIdx.x >> 6)) * 8 + (i)] =       \
-            __builtin_amdgcn_s_memrealtime() + (extra);
-#else
-#define GS_TS(i, extra)
-#endif
 
 // Unit decode in two phases where the format has them (LDS table reads, then arithmetic), so
 // the row loop can issue unit i+1's reads before unit i's arithmetic; one phase otherwise.
@@ -613,23 +604,7 @@ struct StreamPass {
                 float acc0[NV], acc1[NV];
 #pragma unroll
                 for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
-#ifdef GS_STREAM_TS
-                if (base == gid && p == 0) {
-                    uint32_t h = 0;
-#pragma unroll
-                    for (int j = 0; j < UMAX; j++) h ^= ((const uint32_t *)&R[0][j])[0];
-                    GS_TS(4, h == 0x9e3779b9u)
-                }
-#endif
                 if (base + p * ngroups < nrow) {   // no loads inside: the waits stay exact
-#ifdef GS_STREAM_NODOT   // profiling build only: consume the weight words, skip the decode
-#pragma unroll
-                    for (int j = 0; j < UMAX; j++)
-#pragma unroll
-                        for (int w = 0; w < (int)(sizeof(typename F::Raw) / 4); w++)
-                            acc0[0] += __builtin_bit_cast(float, ((const uint32_t *)&R[p][j])[w] & 0x3fffffffu);
-                    if (false)
-#endif
                     if constexpr (USE_PRE) {
 #pragma unroll
                         for (int j = 0; j < UX; j++) dot_pre<NV>(P[PRE ? p : 0][PRE ? j : 0], xr[j], nv, acc0);
@@ -639,9 +614,6 @@ struct StreamPass {
                         const int i = p * UMAX + j;
                         if (i + 1 < PF * UMAX) TP::fetch(R[(i + 1) / UMAX][(i + 1) % UMAX], dec[(i + 1) & 1]);
                         if (KIND != 1 && j >= UX) continue;
-#ifdef GS_STREAM_HALFDOT   // profiling build only: decode every other unit
-                        if (j & 1) continue;
-#endif
                         const int jx = j % UX;
                         if (KIND == 1 && j >= UX)
                             TP::template dot<NV, XNEG>(R[p][j], dec[i & 1], usub[jx], tab, xr[jx], nv, acc1);
@@ -659,18 +631,8 @@ struct StreamPass {
                 }
 #pragma unroll
                 for (int t = 0; t < NV; t++) {
-#ifdef GS_PROBE_NORED   // profiling build only: no cross-lane reduction
-                    res0[p][t] = acc0[t];
-                    res1[p][t] = acc1[t];
-                    if (gather) {
-                        out0 = lane == p * NV + t ? res0[p][t] : out0;
-                        out1 = lane == p * NV + t ? res1[p][t] : out1;
-                    }
-                    if (false) {
-#else
                     res0[p][t] = group_sum(acc0[t], lpr);
                     if (KIND == 1) res1[p][t] = group_sum(acc1[t], lpr);
-#endif
                     if (gather) {
                         const float v0 = __builtin_bit_cast(
                             float, __builtin_amdgcn_ds_bpermute(bsrc, __builtin_bit_cast(int, res0[p][t])));
@@ -681,9 +643,6 @@ struct StreamPass {
                             out1 = lane == p * NV + t ? v1 : out1;
                         }
                     }
-#ifdef GS_PROBE_NORED
-                    }
-#endif
                 }
             }
             if (gather) {
@@ -735,25 +694,18 @@ struct StreamPass {
 template <class F, int KIND, int NV, int UMAX, int LP = 0>
 __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    GS_TS(0, 0)
     StreamPass<F, KIND, NV, UMAX, LP> P(a, smem);
     P.issue_x();
     P.issue_tab();
     P.bind();
-    GS_TS(1, 0)
     // ring kernels: only the first GS_RING_EARLY slots before the activation staging (a smaller
     // first request arrives sooner), the rest after it
     constexpr int E = P.RING && KIND != 0 && GS_RING_EARLY < P.PF ? GS_RING_EARLY : P.PF;
     P.load_batch(P.gid, 0, E);
-    GS_TS(2, 0)
     P.stage_x();
-#ifndef GS_STREAM_NOBAR
     __syncthreads();
-#endif
     P.load_batch(P.gid, E, P.PF);
-    GS_TS(3, 0)
     P.run_rows();
-    GS_TS(5, 0)
 }
 
 // waves per SIMD the streaming kernels are register-allocated for (HBM latency hiding)
@@ -799,65 +751,13 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
 // fetch, first-load latency) disappears, and the down weights are requested before the
 // barrier, so they stream in while the slowest workgroups finish gate/up.
 //
-// The grid must be co-resident (the host sizes it to the occupancy limit). Visibility of h
-// across XCDs needs no cache flush: the gate/up pass stores h at device scope (written through),
-// every workgroup waits for its own stores to complete before it arrives, and nothing reads h
-// before the barrier. The barrier counters only grow (see gs_ffn_sync); the wait is bounded in
-// time (FfnArgs::wait_ticks of the 100 MHz clock, 0.2 s unless the host sets another bound): on
-// expiry gs_ffn_timeout is set and the kernel runs to completion with undefined results instead
-// of hanging; the host reads and clears the flag (gs_moe_ffn_status). Launches of this kernel
-// must not overlap on one device (they share the counters).
+// The grid must be co-resident (the host sizes it to the occupancy limit); the barrier and its
+// memory ordering are gridbar.h's.
 // =============================================================================================
-// Barrier counters, one 128-byte line each: arrivals of workgroup group g = blockIdx.x % 8
-// (groups arrive on separate lines, so their atomics proceed in parallel), and completed groups.
-// They only ever grow: a launch adds exactly its group sizes and group count, so each launch
-// finds them at multiples of those and derives its own targets (no reset, nothing to clear).
-struct __attribute__((aligned(128))) BarLine {
-    unsigned long long v;
-    unsigned long long pad[15];
-};
-__device__ BarLine gs_ffn_sync[9];
-__device__ unsigned gs_ffn_timeout;   // set when a barrier wait expired (results undefined)
-
-#define GS_BAR_GROUPS 8u
-// completed-group count at kernel start (read before this workgroup can arrive)
-__device__ __forceinline__ unsigned long long barrier_epoch() {
-    return __hip_atomic_load(&gs_ffn_sync[8].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Arrival of this workgroup (thread 0, after a workgroup barrier that waited for every wave's
-// h stores to complete; they were made at device scope, so completion means visibility).
-__device__ __forceinline__ void grid_arrive() {
-    const unsigned nblk = gridDim.x;
-    const unsigned ng = nblk < GS_BAR_GROUPS ? nblk : GS_BAR_GROUPS;
-    const unsigned g = blockIdx.x % ng;
-    const unsigned size_g = (nblk - g + ng - 1) / ng;   // workgroups in group g
-    const unsigned long long old =
-        __hip_atomic_fetch_add(&gs_ffn_sync[g].v, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((old + 1) % size_g == 0)   // last of its group in this launch
-        __hip_atomic_fetch_add(&gs_ffn_sync[8].v, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Wait (thread 0) until every group of this launch has arrived; bounded in time.
-__device__ __forceinline__ void grid_wait(unsigned long long top0, uint64_t ticks) {
-    const unsigned nblk = gridDim.x;
-    const unsigned ng = nblk < GS_BAR_GROUPS ? nblk : GS_BAR_GROUPS;
-    const unsigned long long target = (top0 / ng + 1) * ng;
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (__hip_atomic_load(&gs_ffn_sync[8].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        if (__builtin_amdgcn_s_memrealtime() - t0 > ticks) {
-            __hip_atomic_store(&gs_ffn_timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-}
-
 template <class F1, class F2, int UM1, int UM2>
 __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
     extern __shared__ __align__(16) uint8_t smem[];
-    GS_TS(0, 0)
-    const unsigned long long top0 = threadIdx.x == 0 ? barrier_epoch() : 0;
+    const unsigned gen0 = threadIdx.x == 0 ? bar_generation(fa.slot) : 0;
     // a down format with other tables: staged with the gate/up ones (separate LDS arrays; the
     // sign selectors are common), so the down units can be decoded before the barrier
     constexpr bool SAME = is_same_t<F1, F2>::value;
@@ -876,33 +776,35 @@ __device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
         G.load_batch(G.gid, E, G.PF);
         G.run_rows();
     }
-    GS_TS(1, 0)
-    __syncthreads();   // waits for this workgroup's h stores
-    if (threadIdx.x == 0) grid_arrive();
+    __syncthreads();   // orders every wave's h stores before thread 0's release
+    if (threadIdx.x == 0) {
+        bar_release();
+        bar_arrive(fa.slot);
+    }
     StreamPass<F2, 2, 1, UM2, 64> D(fa.dn, smem);   // the host fuses only 64-lane down plans with wlo
     D.issue_tab();
     D.bind();
     D.load_batch(D.gid);   // down weights in flight across the barrier
-    GS_TS(2, 0)
     // IQ formats, one batch of rows per wave: the down units are decoded (table reads, signs)
     // while the workgroup waits for the grid and for h, leaving only the dots for afterwards.
     constexpr bool PRE = decltype(D)::PRE;
     const bool pre = PRE && D.single_batch();
     if (pre) D.predecode();
-    if (threadIdx.x == 0) grid_wait(top0, fa.wait_ticks);
-    __builtin_amdgcn_s_barrier();   // no memory wait: the down weights keep streaming
-    GS_TS(3, 0)
+    if (threadIdx.x == 0) bar_wait(fa.slot, gen0, fa.wait_ticks);
+    // the other waves order their h loads after thread 0's acquire through the workgroup barrier
+    // (a workgroup-scope acquire: it waits for no outstanding load, so the down weights keep
+    // streaming)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     D.issue_x();           // h, complete in every expert
     D.stage_x();
     __syncthreads();
-    GS_TS(6, 0)
     if constexpr (PRE) {
         if (pre) D.template run_rows<true>();
         else D.run_rows();
     } else {
         D.run_rows();
     }
-    GS_TS(7, 0)
 }
 
 #define GS_FFN_KERNEL(F1, N1, F2, N2, UM1, UM2)                                                  \
@@ -936,34 +838,62 @@ GS_FFN_ALL(FIQ2_XXS, 16, FIQ3_XXS, 18)
 #if defined(GS_COMMON)
 
 // =============================================================================================
-// Whole-tensor dequantization (gs_dequant_f32 / gs_dequant_f16): one thread per 8 elements.
+// Whole-tensor dequantization (gs_dequant_f32 / gs_dequant_f16): one thread per 32-element unit
+// (exact.h), stored as 8 (f32) or 4 (f16) 16-byte writes when the destination allows it.
 // =============================================================================================
-#define GS_DEQ_KERNEL(TY, QK, BB, DEQ)                                                           \
+// Decode unit u of a tensor of n elements into v; returns the number of valid elements (32,
+// except a plain-type tensor's last unit, which is decoded from a zero-padded copy so no byte
+// past the tensor is read).
+template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
+__device__ __forceinline__ int dequant_unit(const uint8_t *src, int64_t u, int64_t n, float (&v)[32]) {
+    if (QKB >= 32) {
+        constexpr int UPB = QKB / 32;
+        DEC(src + (u / UPB) * BB, (int)(u % UPB), v);
+        return 32;
+    }
+    const uint8_t *base = src + u * 32 * BB;
+    const int cnt = (int)(n - 32 * u < 32 ? n - 32 * u : 32);
+    if (cnt == 32) {
+        DEC(base, 0, v);
+    } else {
+        uint8_t tmp[32 * BB];
+        for (int i = 0; i < 32 * BB; i++) tmp[i] = i < cnt * BB ? base[i] : 0;
+        DEC(tmp, 0, v);
+    }
+    return cnt;
+}
+#define GS_DEQ_KERNEL(TY, QKB, BB, DEC)                                                          \
     extern "C" __global__ void __launch_bounds__(256) gs_k_dequant_f32_##TY(DequantArgs a) {    \
-        const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;                        \
-        if (g >= a.n_groups) return;                                                            \
-        constexpr int GPB = QK / 8;                                                             \
-        float v[8];                                                                             \
-        DEQ(a.src + (g / GPB) * BB, (int)(g % GPB), v);                                         \
-        float4 *d = (float4 *)((float *)a.dst + g * 8);                                         \
-        d[0] = make_float4(v[0], v[1], v[2], v[3]);                                             \
-        d[1] = make_float4(v[4], v[5], v[6], v[7]);                                             \
+        const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;                        \
+        if (u >= a.n_units) return;                                                             \
+        float v[32];                                                                            \
+        const int cnt = dequant_unit<QKB, BB, DEC>(a.src, u, a.n, v);                           \
+        float *d = (float *)a.dst + 32 * u;                                                     \
+        if (cnt == 32 && a.aligned) {                                                           \
+            for (int i = 0; i < 8; i++)                                                         \
+                ((float4 *)d)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]); \
+        } else {                                                                                \
+            for (int i = 0; i < cnt; i++) d[i] = v[i];                                          \
+        }                                                                                       \
     }                                                                                           \
     extern "C" __global__ void __launch_bounds__(256) gs_k_dequant_f16_##TY(DequantArgs a) {    \
-        const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;                        \
-        if (g >= a.n_groups) return;                                                            \
-        constexpr int GPB = QK / 8;                                                             \
-        float v[8];                                                                             \
-        DEQ(a.src + (g / GPB) * BB, (int)(g % GPB), v);                                         \
-        /* opaque to the optimizer: keeps the f32 value (and the sign of a zero) intact before  \
-           the single f32 -> f16 rounding */                                                   \
-        for (int i = 0; i < 8; i++) asm volatile("" : "+v"(v[i]));                              \
-        uint4 o;                                                                                \
-        o.x = f2h(v[0]) | (f2h(v[1]) << 16);                                                    \
-        o.y = f2h(v[2]) | (f2h(v[3]) << 16);                                                    \
-        o.z = f2h(v[4]) | (f2h(v[5]) << 16);                                                    \
-        o.w = f2h(v[6]) | (f2h(v[7]) << 16);                                                    \
-        *(uint4 *)((uint16_t *)a.dst + g * 8) = o;                                              \
+        const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;                        \
+        if (u >= a.n_units) return;                                                             \
+        float v[32];                                                                            \
+        const int cnt = dequant_unit<QKB, BB, DEC>(a.src, u, a.n, v);                           \
+        /* opaque to the optimizer: the f32 value (and the sign of a zero) reaches the single   \
+           f32 -> f16 rounding unchanged */                                                     \
+        for (int i = 0; i < 32; i++) asm volatile("" : "+v"(v[i]));                             \
+        uint16_t *d = (uint16_t *)a.dst + 32 * u;                                               \
+        if (cnt == 32 && a.aligned) {                                                           \
+            for (int i = 0; i < 4; i++)                                                         \
+                ((uint4 *)d)[i] = make_uint4(f2h(v[8 * i]) | (f2h(v[8 * i + 1]) << 16),           \
+                                             f2h(v[8 * i + 2]) | (f2h(v[8 * i + 3]) << 16),       \
+                                             f2h(v[8 * i + 4]) | (f2h(v[8 * i + 5]) << 16),       \
+                                             f2h(v[8 * i + 6]) | (f2h(v[8 * i + 7]) << 16));      \
+        } else {                                                                                \
+            for (int i = 0; i < cnt; i++) d[i] = (uint16_t)f2h(v[i]);                           \
+        }                                                                                       \
     }
 GS_TYPE_LIST(GS_DEQ_KERNEL)
 

@@ -159,7 +159,11 @@ int gs_quant_q8_1(const float *x, void *q, int64_t n, void *s);
  * allowed). experts[e] holds the device pointers of expert e's gate/up ([K] x n_ff rows,
  * gu_row_stride bytes apart) and down ([n_ff] x K rows, down_row_stride apart).
  *   y[idx[p]][:] += w[p] * down_e . swiglu(gate_e . x[idx[p]], up_e . x[idx[p]])   (always adds)
- * x [n_tok][K], y [n_tok][K] f32; activations are q8_1-quantized as in the other matmul calls.
+ * x [n_tok][K], y [n_tok][K] f32. Numerics are the reference's multi-token GEMM's (gemm.cu:57-78):
+ * x and h enter the contractions as f16 (after a power-of-two row scale that keeps each row in
+ * the f16 normal range), accumulation is f32; the weights are exact (the reference rounds the
+ * dequantized weights to f16). The experts' outputs are combined into y with f32 atomics, so the
+ * summation order (and the last bits of y) can differ between runs.
  * Supported: ty_gu, ty_down each IQ2_XXS or IQ3_XXS, K and n_ff multiples of 256 and >= 512,
  * n_exp <= 1024, x 16-byte aligned. `work` (256-byte aligned, >= gs_moe_grouped_workspace bytes) is caller-owned scratch.
  * All of offs/idx/w/experts are device arrays; the call launches without a host sync. */
