@@ -446,7 +446,7 @@ static void *gemv_worker(void *p) {
     float *w = (float *)malloc(sizeof(float) * (size_t)j->K);
     for (int r = j->r0; r < j->r1; r++) {
         or_dequantize(j->ty, j->W + (int64_t)r * j->row_stride, j->K, w);
-        if (j->mode == OR_ACT_F16)
+        if (j->mode == OR_ACT_F16 || j->mode == OR_ACT_F16S)
             for (int k = 0; k < j->K; k++) w[k] = or_f16_to_f32(or_f32_to_f16(w[k]));
         for (int b = 0; b < j->B; b++) {
             const float *xv = j->xh + (int64_t)b * j->K;
@@ -465,6 +465,15 @@ static void quant_dequant_row(const float *x, int K, float *xh, int mode) {
         for (int k = 0; k < K; k++) xh[k] = or_f16_to_f32(or_f32_to_f16(x[k]));
         return;
     }
+    if (mode == OR_ACT_F16S || mode == OR_ACT_F16SX) {
+        float amax = 0.0f;
+        for (int k = 0; k < K; k++) amax = fmaxf(amax, fabsf(x[k]));
+        int E = 0;
+        if (amax > 0.0f && amax <= 3.4e38f) (void)frexpf(amax, &E);   /* amax < 2^E */
+        E -= 15;
+        for (int k = 0; k < K; k++) xh[k] = ldexpf(or_f16_to_f32(or_f32_to_f16(ldexpf(x[k], -E))), E);
+        return;
+    }
     uint8_t *q = (uint8_t *)malloc((size_t)(K / 32) * OR_Q8_1_BYTES);
     or_quantize_q8_1(x, K, q);
     or_dequantize_q8_1(q, K, xh);
@@ -474,7 +483,7 @@ static void quant_dequant_row(const float *x, int K, float *xh, int mode) {
 int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
             int B, int quant_x, double *y, int nthreads) {
     int be, bb;
-    if (or_block(ty, &be, &bb) != 0 || K % be != 0 || K % 32 != 0 || B < 1 || quant_x < 0 || quant_x > 3) return -1;
+    if (or_block(ty, &be, &bb) != 0 || K % be != 0 || K % 32 != 0 || B < 1 || quant_x < 0 || quant_x > 5) return -1;
     float *xh = (float *)malloc(sizeof(float) * (size_t)K * B);
     for (int b = 0; b < B; b++) quant_dequant_row(x + (int64_t)b * x_stride, K, xh + (int64_t)b * K, quant_x);
     if (nthreads < 1) nthreads = 1;

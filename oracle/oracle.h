@@ -46,11 +46,17 @@ int or_random_blocks(int ty, int64_t n_elems, uint64_t *state, uint8_t *out);
  *                    activations converted to half, f32 accumulation)
  *   OR_ACT_F16X (3): xhat = f16(x), what = deq(W)                 (half activations, exact weights:
  *                    what this build's grouped MFMA GEMM computes)
+ *   OR_ACT_F16S (4), OR_ACT_F16SX (5): as F16 / F16X, with each activation row first scaled by the
+ *                    power of two 2^-E that puts its largest magnitude in [2^14, 2^15) and scaled
+ *                    back after the half rounding (equal to F16 / F16X wherever those stay finite;
+ *                    rows beyond the half range do not overflow)
  * nthreads > 1 splits rows over pthreads. */
 #define OR_ACT_F32 0
 #define OR_ACT_Q8_1 1
 #define OR_ACT_F16 2
 #define OR_ACT_F16X 3
+#define OR_ACT_F16S 4
+#define OR_ACT_F16SX 5
 int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
             int B, int quant_x, double *y, int nthreads);
 

@@ -111,7 +111,7 @@ class Rng:
         return out
 
 
-ACT = {"f32": 0, "q8_1": 1, "f16": 2, "f16x": 3}
+ACT = {"f32": 0, "q8_1": 1, "f16": 2, "f16x": 3, "f16s": 4, "f16sx": 5}
 
 
 def gemv(ty, W, row_stride, K, rows, x, B=1, x_stride=None, quant_x=True, nthreads=1, act=None):

@@ -1,9 +1,9 @@
 """GPU parity of the grouped routed-expert FFN (gs_moe_grouped, the MFMA path for prefill and
 MTP verify) against the CPU oracle's per-pair FFN:
-  * act="f16"  -- the reference's multi-token GEMM semantics (half activations x and h,
+  * act="f16s"  -- the reference's multi-token GEMM semantics (half activations x and h,
     half-rounded dequantized weights, crates/cuda/kernels/gemm.cu:57-78 under
     forward.rs:1399-1413): rel-L2 <= 1e-3, the north-star bound for FFN outputs;
-  * act="f16x" -- half activations with exact weights, which is what the kernel computes (its
+  * act="f16sx" -- half activations with exact weights, which is what the kernel computes (its
     weights are exact integers times the block scale): rel-L2 <= 1e-4, so the kernel's own error
     (f32 accumulation order) is checked well inside the reference bound.
 Where the reference semantics' own weight rounding exceeds 1e-3 against exact weights (random
@@ -52,9 +52,9 @@ def run_case(n_exp, n_tok, k, n_embd, n_ff, seed, lim=0.0, routes=None, zero_w=F
     layer = M.ResidentMoeLayer(gate, up, down, n_embd, n_ff, ty_gu, ty_down)
     offs, idx, w, pe = layer.upload_routes(routes)
     want = O.moe_ffn(ty_gu, ty_down, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, x, idx, pe, w, lim=lim,
-                     nthreads=8, act="f16")
+                     nthreads=8, act="f16s")
     wantx = O.moe_ffn(ty_gu, ty_down, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, x, idx, pe, w, lim=lim,
-                      nthreads=8, act="f16x")
+                      nthreads=8, act="f16sx")
     y0 = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
     s = G.Stream()
     dx, dy = G.DeviceBuffer.from_array(x), G.DeviceBuffer.from_array(y0)
@@ -123,11 +123,9 @@ def run_layer_sampled(n_tok, seed, n_sample, n_exp=288, k=8, n_embd=4096, n_ff=1
     tokens of the most loaded expert."""
     say(f"grouped (benchmark shapes): n_exp={n_exp} n_tok={n_tok} top{k} K={n_embd} n_ff={n_ff} seed={seed} "
         f"sampled tokens={n_sample}")
-    orng = O.Rng(2000 + seed)
-    gate = [orng.random_blocks(ty, n_ff * n_embd) for _ in range(n_exp)]
-    up = [orng.random_blocks(ty, n_ff * n_embd) for _ in range(n_exp)]
-    down = [orng.random_blocks(ty, n_embd * n_ff) for _ in range(n_exp)]
+    # the configuration's own generator: random IQ2_XXS blocks with d ~ |N(0, 0.02)|
     rng = np.random.default_rng(seed)
+    gate, up, down = map(list, zip(*[synth.iq2_xxs_expert(rng, n_embd, n_ff) for _ in range(n_exp)]))
     routes = [list(zip(e, w)) for e, w in synth.zipf_topk(rng, n_tok, n_exp, k)]
     x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
     layer = M.ResidentMoeLayer(gate, up, down, n_embd, n_ff, ty, ty)
@@ -150,9 +148,9 @@ def run_layer_sampled(n_tok, seed, n_sample, n_exp=288, k=8, n_embd=4096, n_ff=1
     xs = x[pick]
     kw = dict(nthreads=16)
     want = O.moe_ffn(ty, ty, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, xs, ptok, pe[sel], w[sel],
-                     act="f16", **kw)
+                     act="f16s", **kw)
     wantx = O.moe_ffn(ty, ty, gate, up, down, layer.rs_gu, layer.rs_down, n_embd, n_ff, xs, ptok, pe[sel], w[sel],
-                      act="f16x", **kw)
+                      act="f16sx", **kw)
     g = got[pick]
     err, errx, err_ref = rel_l2(g, want), rel_l2(g, wantx), rel_l2(want, wantx)
     say(f"  pairs={idx.size} unique experts={int(np.count_nonzero(counts))} max group={counts.max()} "

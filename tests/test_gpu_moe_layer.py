@@ -69,7 +69,7 @@ def test_moe_layer(t, ty_dn):
     for ti, r in enumerate(want_routes):
         for e, w in r:
             pt.append(ti); pe.append(e); pw.append(w)
-    act = "f16" if t > 4 else "q8_1"   # more than 4 tokens: grouped MFMA path, the GEMM semantics
+    act = "f16s" if t > 4 else "q8_1"   # more than 4 tokens: grouped MFMA path, the GEMM semantics
     routed = O.moe_ffn(T.IQ2_XXS, ty_dn, [e[0] for e in experts], [e[1] for e in experts],
                        [e[2] for e in experts], G.row_bytes(T.IQ2_XXS, n_embd), G.row_bytes(ty_dn, n_ff), n_embd,
                        n_ff, x, pt, pe, pw, lim=lim_e, nthreads=8, act=act)

@@ -315,3 +315,31 @@ def test_moe_ffn_f16_mode_bruteforce():
         D = half(O.dequantize(O.IQ2_XXS, down[e], n_embd * n_ff).reshape(n_embd, n_ff)) @ half(h[p])
         want[t] += np.float64(np.float32(w)) * D
     assert np.allclose(y, want, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("ty", [O.IQ2_XXS, O.Q8_0])
+def test_gemv_f16s_modes_scaled_half(ty):
+    # OR_ACT_F16S / F16SX: activation rows scaled by a power of two into [2^14, 2^15) before the half
+    # rounding. Pinned by (1) equality with F16 / F16X where every activation is a normal half
+    # (a power-of-two scale commutes with rounding there), (2) equivariance: scaling x by 2^k
+    # scales y by exactly 2^k for any k, far past the half range, (3) a brute-force numpy
+    # restatement for one row beyond the half range.
+    K, rows = 256, 17
+    rng = O.Rng(99 + ty)
+    W = rng.random_blocks(ty, rows * K)
+    rb = O.row_bytes(ty, K)
+    x = (np.random.default_rng(ty).standard_normal((2, K)) * 50).astype(np.float32)
+    for a, b in (("f16", "f16s"), ("f16x", "f16sx")):
+        assert np.array_equal(O.gemv(ty, W, rb, K, rows, x, B=2, act=a), O.gemv(ty, W, rb, K, rows, x, B=2, act=b))
+    for k in (-20, 7, 40, 100):
+        xs = (x.astype(np.float64) * 2.0 ** k).astype(np.float32)
+        for b in ("f16s", "f16sx"):
+            assert np.array_equal(O.gemv(ty, W, rb, K, rows, xs, B=2, act=b),
+                                  O.gemv(ty, W, rb, K, rows, x, B=2, act=b) * 2.0 ** k)
+    big = x[:1] * np.float32(1e9)
+    y = O.gemv(ty, W, rb, K, rows, big, act="f16sx")
+    m, e = np.frexp(np.abs(big).max())
+    sc = 2.0 ** (int(e) - 15)
+    xh = (big / sc).astype(np.float16).astype(np.float64) * sc
+    want = xh @ O.dequantize(ty, W, rows * K).reshape(rows, K).astype(np.float64).T
+    assert np.all(np.isfinite(y)) and np.allclose(y, want, rtol=1e-12, atol=0)
