@@ -209,20 +209,25 @@ def run_moe_per_token(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
                 frac_hbm_peak=round(wbytes / t / 1e9 / HBM_PEAK_GBPS, 4), calls_per_step=n_tok, routings_rotated=n_rout)
 
 
-def run_read_ceiling(L, s, sizes, steps, warmup, pool_bytes=768 << 20):
+def run_read_ceiling(L, s, sizes, steps, warmup, min_pool=768 << 20):
     """Plain HBM read (bench_kernels.hip bn_k_read) of each byte count, the start address rotated
-    over a 768 MB pool so no call is served from the last-level cache: the achievable ceiling the
-    streaming kernels are compared with at the same byte count."""
+    over a pool of at least 768 MB so no call is served from the last-level cache: the achievable
+    ceiling the streaming kernels are compared with at the same byte count."""
     import glmssd as G
+    sizes = [(n + 4095) // 4096 * 4096 for n in sizes]
+    pool_bytes = max(min_pool, max(sizes))
     pool = G.DeviceBuffer(pool_bytes)
     out = {}
     for n in sizes:
-        n = (n + 4095) // 4096 * 4096
         nb = max(1, min(64, pool_bytes // n))
-        bases = (C.c_void_p * nb)(*[pool.p.value + i * (pool_bytes // nb) // 4096 * 4096 for i in range(nb)])
+        step = (pool_bytes - n) // max(1, nb - 1) // 4096 * 4096 if nb > 1 else 0
+        offs = [i * step for i in range(nb)]
+        assert all(o + n <= pool_bytes for o in offs)   # every read stays inside the pool
+        bases = (C.c_void_p * nb)(*[pool.p.value + o for o in offs])
         ms = C.c_float()
         G.check(L.bn_read(C.cast(bases, C.c_void_p), nb, n, steps, warmup, s.raw(), C.byref(ms)))
-        out[str(n)] = {"bytes": n, "us": round(ms.value * 1e3, 2), "GB/s": round(n / (ms.value * 1e-3) / 1e9, 1)}
+        out[str(n)] = {"bytes": n, "us": round(ms.value * 1e3, 2), "GB/s": round(n / (ms.value * 1e-3) / 1e9, 1),
+                       "rotated_bases": nb}
     return out
 
 

@@ -31,84 +31,99 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));   // staging chunk (a native vector, so it stays in VGPRs)
 
 // Decode tables in LDS, built by every workgroup at start:
-//   grid (64 KB): for grid index g and unit scale s (0..15), the 8 (IQ2_XXS) or 4 (IQ3_XXS) grid
-//     values times 2s+1 as f16 at byte (g << 8) | (s << 4) -- the address is one v_perm of the
-//     unit's index byte and its scale nibble;
-//   signs (1 KB): for a 7-bit sign index i, 8 bytes, byte e = 0x80 when element e of ksigns(i)
-//     is negative, at byte 65536 + 8 i.
-// A B fragment is one 16-byte and one 8-byte LDS read, 4 v_perm (sign bytes -> f16 sign bits)
-// and 4 XORs. (Measured on gfx950 against one-table alternatives: the 24 bytes of LDS per 8
-// weights, not the VALU work, bound the decode; this layout reads the fewest bytes.)
-#define GS_GRP_TAB_BYTES (65536 + 1024)
-__shared__ int gs_grp_pre[GS_GRP_EXP_MAX + 1];
+//   signs (16 KB, at byte 0): for a 7-bit sign index i, the 8 elements' f16 sign bits as four
+//     words (bit 15 / bit 31 of word w: element 2w / 2w+1 of ksigns(i) negative), 16 bytes,
+//     replicated 8 times: lane j reads its copy at 128 i + 16 (j & 7), so the 8 lanes of an LDS
+//     phase never share a bank;
+//   grid (64 KB, at byte GS_GRP_GRID_OFF): for grid index g and unit scale s (0..15), the 8
+//     (IQ2_XXS) or 4 (IQ3_XXS) grid values times 2s+1 as f16 at 256 g + 16 s -- the address is one
+//     v_perm of the index byte and the scale nibble (grid * (2s+1) <= 43 * 31 = 1333 for IQ2_XXS,
+//     62 * 31 = 1922 for IQ3_XXS: exact in f16).
+// A B fragment (8 weights) is one 16-byte grid read, one 16-byte sign read and 4 XORs.
+#define GS_GRP_GRID_OFF 16384
+#define GS_GRP_TAB_BYTES (16384 + 65536)
+__shared__ int gs_grp_pre[GS_GRP_EXP_MAX + 1];     // tile prefix over experts in schedule order
+__shared__ int gs_grp_order[GS_GRP_EXP_MAX];       // schedule order: experts by pair count, largest first
+__shared__ int gs_grp_ep_tok[64];                   // epilogue operands of the current tile's token slots
+__shared__ float gs_grp_ep_w[64], gs_grp_ep_sc[64];
 
 template <int TY, int NTH>
 __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
-    for (int e = tid; e < 4096; e += NTH) {
-        const int g = e >> 4, sc = e & 15;
+    // thread -> (grid index g, 8 of the 16 scales): one table read per thread, issued up front
+    constexpr int PER = 4096 / NTH;   // entries per thread (8 with 512 threads)
+    static_assert(PER >= 1 && 16 % PER == 0, "threads per workgroup");
+    const int e0 = tid * PER, g = e0 >> 4;
+    const uint64_t grid = TY == GS_IQ2_XXS ? iq2xxs_grid[g] : (uint64_t)iq3xxs_grid[g];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int e = e0 + k, sc = e & 15;
         const float m = (float)(2 * sc + 1);
         uint32_t w[4];
         if (TY == GS_IQ2_XXS) {
-            const uint64_t grid = iq2xxs_grid[g];
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 w[i] = f2h(m * (float)((grid >> (16 * i)) & 0xff)) | (f2h(m * (float)((grid >> (16 * i + 8)) & 0xff)) << 16);
         } else {   // IQ3_XXS: 4 grid values per entry, the upper 8 bytes of the slot unused
-            const uint32_t grid = iq3xxs_grid[g];
 #pragma unroll
             for (int i = 0; i < 2; i++)
                 w[i] = f2h(m * (float)((grid >> (16 * i)) & 0xff)) | (f2h(m * (float)((grid >> (16 * i + 8)) & 0xff)) << 16);
             w[2] = w[3] = 0;
         }
-        *(uint4 *)(tab + (e << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4 *)(tab + GS_GRP_GRID_OFF + (e << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    for (int i = tid; i < 128; i += NTH) {
-        const uint32_t k = ksigns((uint32_t)i);
-        uint32_t lo = 0, hi = 0;
+    for (int e = tid; e < 128 * 8; e += NTH) {
+        const uint32_t k = ksigns((uint32_t)(e >> 3));
+        uint32_t w[4];
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            lo |= ((k >> b) & 1u) << (8 * b + 7);
-            hi |= ((k >> (b + 4)) & 1u) << (8 * b + 7);
-        }
-        *(uint2 *)(tab + 65536 + (i << 3)) = make_uint2(lo, hi);
+        for (int i = 0; i < 4; i++) w[i] = (((k >> (2 * i)) & 1u) << 15) | (((k >> (2 * i + 1)) & 1u) << 31);
+        *(uint4 *)(tab + (e << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
 // B fragment of group G (0..3) of one unit: 8 f16 integers grid * sign * (2s+1). Two phases, so
-// a decode step issues the table reads of all its fragments before it waits for any of them
-// (one fragment at a time, every read waited for in turn, config 5 took 6 % longer):
+// a decode step issues the table reads of all its fragments before it waits for any of them:
 //   IQ2_XXS: a0 = the unit's 4 grid-index bytes, a1 = signs | s << 28; one 16-byte grid read;
 //   IQ3_XXS: g0, g1 = its 8 index bytes, a1 as above; two 8-byte reads of 4-value entries
-//     (lib.rs:312-328; |v| <= 62 * 31 = 1922, exact in f16);
-// both: one 8-byte sign-byte read; finish turns sign byte e into bit 15 (e even) / bit 31 (e odd)
-// of half pair e/2 and applies it with XOR.
+//     (lib.rs:312-328);
+// both: one 16-byte sign-mask read (r16 = 16 (j & 7), the lane's replica); finish applies it
+// with XOR.
 struct FragRaw {
     uint4 g;
-    uint2 sb;
+    uint4 sm;
     uint2 g2;   // IQ3_XXS: the second 4-value entry
 };
 template <int G>
-__device__ __forceinline__ void iq2_frag_fetch(const uint8_t *tab, uint32_t a0, uint32_t a1, FragRaw &r) {
-    const uint32_t ga = __builtin_amdgcn_perm(a0, a1 & 0xF0000000u, 0x0c0c0403u + (G << 8));
-    r.g = *(const uint4 *)(tab + ga);
-    r.sb = *(const uint2 *)(tab + 65536 + (((a1 >> (7 * G)) & 127) << 3));
+__device__ __forceinline__ uint32_t sign_off(uint32_t a1, uint32_t r16) {
+    return (__builtin_amdgcn_ubfe(a1, 7 * G, 7) << 7) | r16;
 }
 template <int G>
-__device__ __forceinline__ void iq3_frag_fetch(const uint8_t *tab, uint32_t g0, uint32_t g1, uint32_t a1, FragRaw &r) {
+__device__ __forceinline__ void iq2_frag_fetch(const uint8_t *tab, uint32_t a0, uint32_t a1, uint32_t r16, FragRaw &r) {
+    const uint32_t ga = __builtin_amdgcn_perm(a0, a1 & 0xF0000000u, 0x0c0c0403u + (G << 8));
+    r.g = *(const uint4 *)(tab + GS_GRP_GRID_OFF + ga);
+    r.sm = *(const uint4 *)(tab + sign_off<G>(a1, r16));
+}
+template <int G>
+__device__ __forceinline__ void iq3_frag_fetch(const uint8_t *tab, uint32_t g0, uint32_t g1, uint32_t a1, uint32_t r16,
+                                               FragRaw &r) {
     const uint32_t gw = G < 2 ? g0 : g1;
     constexpr uint32_t b0 = (2 * G) & 3;
     const uint32_t hs = a1 & 0xF0000000u;
-    const uint2 lo = *(const uint2 *)(tab + __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + (b0 << 8)));
-    r.g2 = *(const uint2 *)(tab + __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + ((b0 + 1) << 8)));
+    const uint2 lo = *(const uint2 *)(tab + GS_GRP_GRID_OFF + __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + (b0 << 8)));
+    r.g2 = *(const uint2 *)(tab + GS_GRP_GRID_OFF + __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + ((b0 + 1) << 8)));
     r.g = make_uint4(lo.x, lo.y, 0u, 0u);
-    r.sb = *(const uint2 *)(tab + 65536 + (((a1 >> (7 * G)) & 127) << 3));
+    r.sm = *(const uint4 *)(tab + sign_off<G>(a1, r16));
+}
+// Load of a wave-uniform address in data no kernel of this launch writes (the CSR offsets and the
+// expert table), through the constant address space: a scalar load, waited on by its own counter
+// instead of the in-order vector-memory counter that the weight stream keeps busy.
+template <class T>
+__device__ __forceinline__ T ld_scalar(const T *p) {
+    return *(const __attribute__((address_space(4))) T *)(const __attribute__((address_space(4))) void *)p;
 }
 template <bool IQ3>
 __device__ __forceinline__ h8 frag_finish(const FragRaw &r) {
-    const uint4 m = make_uint4(__builtin_amdgcn_perm(r.sb.y, r.sb.x, 0x010c000cu), __builtin_amdgcn_perm(r.sb.y, r.sb.x, 0x030c020cu),
-                               __builtin_amdgcn_perm(r.sb.y, r.sb.x, 0x050c040cu), __builtin_amdgcn_perm(r.sb.y, r.sb.x, 0x070c060cu));
     const uint4 g = IQ3 ? make_uint4(r.g.x, r.g.y, r.g2.x, r.g2.y) : r.g;
-    return __builtin_bit_cast(h8, make_uint4(g.x ^ m.x, g.y ^ m.y, g.z ^ m.z, g.w ^ m.w));
+    return __builtin_bit_cast(h8, make_uint4(g.x ^ r.sm.x, g.y ^ r.sm.y, g.z ^ r.sm.z, g.w ^ r.sm.w));
 }
 
 #define GS_GRP_AV_LOAD(tt, cc) __builtin_bit_cast(h8, *(const uint4 *)(slab + (16 * (tt) + j) * 512 + ((((cc) ^ j)) << 4)))
@@ -121,17 +136,38 @@ __device__ __forceinline__ float grp_swiglu(float g, float u, float lim) {   // 
     return g / (1.f + expf(-g)) * u;
 }
 
-// Tile list: expert e owns ceil(m_e / MT) * nrb consecutive tiles (row block fastest, so the
-// workgroups that share a token chunk run side by side and share its activations in L2).
-__device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb) {
+// Tile list. Experts are scheduled by pair count, largest first (rank = experts with more pairs,
+// or as many and a lower id): the long tiles of hot experts start first and the short ones fill
+// in behind them. Expert e owns ceil(m_e / MT) * nrb consecutive tiles, the token chunks of one
+// row block adjacent (chunk fastest), so the chunks that read the same weights run side by side.
+// m_tmp: n_exp ints of scratch (the staging area, free during the prologue).
+template <int NTH>
+__device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb, int *m_tmp) {
     const int tid = threadIdx.x, lane = tid & 63;
+    const int n4 = (a.n_exp + 3) >> 2;   // m_tmp padded to whole int4 with -1 (sorts last)
+    for (int e = tid; e < 4 * n4; e += NTH) m_tmp[e] = e < a.n_exp ? a.offs[e + 1] - a.offs[e] : -1;
+    __syncthreads();
+    // rank by counting (every lane of a wave reads the same int4: one broadcast LDS read per 4 experts)
+    for (int e = tid; e < a.n_exp; e += NTH) {
+        const int m = m_tmp[e];
+        int rank = 0;
+#pragma unroll 8
+        for (int f4 = 0; f4 < n4; f4++) {
+            const int4 v = ((const int4 *)m_tmp)[f4];
+            const int f = 4 * f4;
+            rank += (v.x > m || (v.x == m && f < e)) + (v.y > m || (v.y == m && f + 1 < e)) +
+                    (v.z > m || (v.z == m && f + 2 < e)) + (v.w > m || (v.w == m && f + 3 < e));
+        }
+        gs_grp_order[rank] = e;
+    }
+    __syncthreads();
     if (tid < 64) {
         int carry = 0;
-        for (int e0 = 0; e0 < a.n_exp; e0 += 64) {
-            const int e = e0 + lane;
+        for (int r0 = 0; r0 < a.n_exp; r0 += 64) {
+            const int r = r0 + lane;
             int cnt = 0;
-            if (e < a.n_exp) {
-                const int m = a.offs[e + 1] - a.offs[e];
+            if (r < a.n_exp) {
+                const int m = m_tmp[gs_grp_order[r]];
                 cnt = m > 0 ? (m + MT - 1) / MT * nrb : 0;
             }
             int v = cnt;
@@ -140,7 +176,7 @@ __device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb
                 const int u = __shfl_up(v, o);
                 if (lane >= o) v += u;
             }
-            if (e < a.n_exp) gs_grp_pre[e + 1] = carry + v;
+            if (r < a.n_exp) gs_grp_pre[r + 1] = carry + v;
             carry += __shfl(v, 63);
         }
         if (lane == 0) gs_grp_pre[0] = 0;
@@ -174,16 +210,21 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     extern __shared__ __align__(16) uint8_t gs_grp_dyn[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4;
+    const uint32_t r16 = (uint32_t)(j & 7) << 4;   // the lane's sign-table replica
     const int K = a.K, rows = a.rows, nsb = K / 256;
     const int nrb = (rows + RB - 1) / RB;
     const uint32_t rs = (uint32_t)a.row_stride;
     uint8_t *const tab = gs_grp_dyn;
     uint8_t *const stage = gs_grp_dyn + GS_GRP_TAB_BYTES;
     grp_tables<TY, NTH>(tab, tid);
-    grp_prefix(a, MT, nrb);
+    grp_prefix<NTH>(a, MT, nrb, (int *)stage);
     __syncthreads();
     const int total = gs_grp_pre[a.n_exp];
-    int t = blockIdx.x;
+    // Workgroup w runs on XCD w % 8 (round-robin dispatch). With a grid that is a multiple of 8,
+    // round k of workgroup w takes tile k*G + (w % 8) * G/8 + w / 8, so consecutive tiles of the
+    // list (the chunks of one row block) run at the same time on one XCD and share its L2.
+    const int G8 = gridDim.x >> 3;
+    int t = (gridDim.x & 7) == 0 ? (int)(blockIdx.x & 7) * G8 + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
     if (t >= total) return;
 
     // staging chunks of this thread: chunk z = tid + NTH*k -> slot z >> 5, chunk column z & 31
@@ -201,20 +242,22 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         const uint8_t *wb[MATS];   // expert matrix bases (uniform)
     };
     auto describe = [&](int tt_, Desc &d) {
-        int lo = 0, hi = a.n_exp;   // largest e with pre[e] <= t
+        int lo = 0, hi = a.n_exp;   // largest rank r with pre[r] <= t
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
             if (gs_grp_pre[mid] <= tt_) lo = mid; else hi = mid;
         }
-        const int e = __builtin_amdgcn_readfirstlane(lo);
-        const int local = tt_ - gs_grp_pre[e];
-        const int chunk = local / nrb, rb = local - chunk * nrb;
-        const int o0 = a.offs[e], o1 = a.offs[e + 1];
+        const int r = __builtin_amdgcn_readfirstlane(lo);
+        const int e = __builtin_amdgcn_readfirstlane(gs_grp_order[r]);
+        const int local = tt_ - gs_grp_pre[r];
+        const int o0 = ld_scalar(a.offs + e), o1 = ld_scalar(a.offs + e + 1);
+        const int nch = (o1 - o0 + MT - 1) / MT;
+        const int rb = local / nch, chunk = local - rb * nch;
         d.p_beg = o0 + chunk * MT;
         d.n_here = min(MT, o1 - d.p_beg);
         d.row0 = rb * RB + wave * 16 * NR;
 #pragma unroll
-        for (int mt = 0; mt < MATS; mt++) d.wb[mt] = a.experts[3 * e + (KIND == 2 ? 2 : mt)];
+        for (int mt = 0; mt < MATS; mt++) d.wb[mt] = ld_scalar(a.experts + 3 * e + (KIND == 2 ? 2 : mt));
     };
     // per-lane weight offsets of a tile (row of sub-tile n, this lane's 16 bytes of each block)
     auto woffs = [&](const Desc &d, uint32_t (&wo)[NR]) {
@@ -231,17 +274,18 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         }
     };
 
+    // nxt repeats cur when there is no next tile (its loads are issued and dropped)
     Desc cur, nxt;
     describe(t, cur);
     const int tstep = gridDim.x;
     bool has_nxt = t + tstep < total;
-    if (has_nxt) describe(t + tstep, nxt);
+    describe(has_nxt ? t + tstep : t, nxt);
     uint32_t wo_cur[NR], wo_nxt[NR];
     woffs(cur, wo_cur);
-    if (has_nxt) woffs(nxt, wo_nxt);
+    woffs(nxt, wo_nxt);
     int ar_cur[NLD], ar_nxt[NLD];
     arows_raw(cur, ar_cur);
-    if (has_nxt) arows_raw(nxt, ar_nxt);
+    arows_raw(nxt, ar_nxt);
 
     struct WRegs {   // one position's raw weight words: 16 bytes (units 2q, 2q+1) + f16 d per row
         uint4 q[NR][MATS];
@@ -283,19 +327,23 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     }
     __syncthreads();
 
-    // epilogue operands of the current tile, requested early
-    int ep_tok[NT][4];
-    float ep_sc[NT][4], ep_w[NT][4];
+    // Epilogue operands of the current tile (per token slot: token id, combine weight, activation
+    // row scale): thread `tid` < MT loads slot tid's at tile entry and stores them to LDS at
+    // position nsb-2, so the epilogue at nsb-1 reads them from LDS after a barrier (three
+    // registers instead of NT x 12 per lane).
+    int ep_tok = 0;
+    float ep_w = 1.f, ep_sc = 1.f;
     auto ep_load = [&](const Desc &d) {
-#pragma unroll
-        for (int tt = 0; tt < NT; tt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = d.p_beg + min(16 * tt + 4 * q + i, d.n_here - 1);
-                ep_tok[tt][i] = a.idx[p];
-                ep_w[tt][i] = KIND == 2 ? a.w[p] : 1.f;
-                if (KIND == 2) ep_sc[tt][i] = a.ascale[p];
+        if (tid < MT) {
+            const int p = d.p_beg + min(tid, d.n_here - 1);
+            ep_tok = a.idx[p];
+            if (KIND == 2) {
+                ep_w = a.w[p];
+                ep_sc = a.ascale[p];
+            } else {
+                ep_sc = a.ascale[ep_tok];   // waits for the token id here, once per tile
             }
+        }
     };
     ep_load(cur);
 
@@ -312,30 +360,26 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         // ---- issue: activations of position +1, weights of position +2 -------------------
         const bool last_sb = b == nsb - 1;
         const bool have1 = !last_sb || has_nxt;
+        // Both requests are issued unconditionally (at the end of the tile list they re-read valid
+        // data of the current tile and are dropped), so every wait on them is an exact count.
         u4 stg[NLD];
-        if (have1) {   // one load site: select the tile element-wise (no array aliasing)
+        {
+            const bool a_nxt = last_sb;
             int ar[NLD];
 #pragma unroll
-            for (int k = 0; k < NLD; k++) ar[k] = last_sb ? ar_nxt[k] : ar_cur[k];
+            for (int k = 0; k < NLD; k++) ar[k] = a_nxt ? ar_nxt[k] : ar_cur[k];
             load_a(ar, last_sb ? 0 : b + 1, stg);
         }
         {
             const bool in_cur = b + 2 < nsb;
-            if (in_cur || has_nxt) {
-                Desc d;
-                uint32_t wo[NR];
+            const bool w_nxt = !in_cur;
+            Desc d;
+            uint32_t wo[NR];
 #pragma unroll
-                for (int mt = 0; mt < MATS; mt++) d.wb[mt] = in_cur ? cur.wb[mt] : nxt.wb[mt];
+            for (int mt = 0; mt < MATS; mt++) d.wb[mt] = w_nxt ? nxt.wb[mt] : cur.wb[mt];
 #pragma unroll
-                for (int n = 0; n < NR; n++) wo[n] = in_cur ? wo_cur[n] : wo_nxt[n];
-                load_w(d, wo, in_cur ? b + 2 : b + 2 - nsb, wl);
-            }
-        }
-        if (KIND == 1 && b == nsb / 2) {   // gate/up row scales by token id
-#pragma unroll
-            for (int tt = 0; tt < NT; tt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) ep_sc[tt][i] = a.ascale[ep_tok[tt][i]];
+            for (int n = 0; n < NR; n++) wo[n] = w_nxt ? wo_nxt[n] : wo_cur[n];
+            load_w(d, wo, in_cur ? b + 2 : b + 2 - nsb, wl);
         }
 
         // ---- contract position (cur, b) ------------------------------------------------------
@@ -356,8 +400,8 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         _Pragma("unroll") for (int n = 0; n < NR; n++)                                             \
         _Pragma("unroll") for (int mt = 0; mt < MATS; mt++) {                                      \
             if (IQ3) iq3_frag_fetch<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y, \
-                                       hu ? wu.sg[n][mt].y : wu.sg[n][mt].x, fr[n][mt]);          \
-            else iq2_frag_fetch<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y, fr[n][mt]); \
+                                       hu ? wu.sg[n][mt].y : wu.sg[n][mt].x, r16, fr[n][mt]);       \
+            else iq2_frag_fetch<G>(tab, hu ? wu.q[n][mt].z : wu.q[n][mt].x, hu ? wu.q[n][mt].w : wu.q[n][mt].y, r16, fr[n][mt]); \
         }                                                                                          \
         _Pragma("unroll") for (int n = 0; n < NR; n++)                                             \
         _Pragma("unroll") for (int mt = 0; mt < MATS; mt++) bf[n][mt] = frag_finish<IQ3>(fr[n][mt]);
@@ -383,7 +427,8 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 for (int mt = 0; mt < MATS; mt++) {
                     const float cd = h2f(wu.d[n][mt]) * XS;
 #pragma unroll
-                    for (int tt = 0; tt < NT; tt++) acc[tt][n][mt] += cd * sb[tt][n][mt];
+                    for (int tt = 0; tt < NT; tt++)
+                        if (tt == 0 || 16 * tt < n_here) acc[tt][n][mt] += cd * sb[tt][n][mt];
                 }
         }
 
@@ -394,7 +439,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int slot = 16 * tt + 4 * q + i;
-                    const float sc = ep_sc[tt][i], wt = ep_w[tt][i];
+                    const float sc = gs_grp_ep_sc[slot], wt = gs_grp_ep_w[slot];
                     if (slot < cur.n_here && (KIND == 1 || wt != 0.f)) {
                         const int p = cur.p_beg + slot;
 #pragma unroll
@@ -405,7 +450,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                                     a.out[(int64_t)p * rows + r] =
                                         grp_swiglu(acc[tt][n][0][i] * sc, acc[tt][n][1][i] * sc, a.lim);
                                 else
-                                    unsafeAtomicAdd(a.out + (int64_t)ep_tok[tt][i] * rows + r, wt * (acc[tt][n][0][i] * sc));
+                                    unsafeAtomicAdd(a.out + (int64_t)gs_grp_ep_tok[slot] * rows + r, wt * (acc[tt][n][0][i] * sc));
                             }
                         }
                     }
@@ -416,6 +461,11 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 for (int n = 0; n < NR; n++)
 #pragma unroll
                     for (int mt = 0; mt < MATS; mt++) acc[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+        if (b == nsb - 2 && tid < MT) {   // read by the epilogue of position nsb-1, after the barrier
+            gs_grp_ep_tok[tid] = ep_tok;
+            gs_grp_ep_w[tid] = ep_w;
+            gs_grp_ep_sc[tid] = ep_sc;
         }
         if (!have1) return false;
 
@@ -432,13 +482,15 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             for (int n = 0; n < NR; n++) wo_cur[n] = wo_nxt[n];
 #pragma unroll
             for (int k = 0; k < NLD; k++) ar_cur[k] = ar_nxt[k];
-            ep_load(cur);
             has_nxt = t + tstep < total;
-            if (has_nxt) {
-                describe(t + tstep, nxt);
-                woffs(nxt, wo_nxt);
-                arows_raw(nxt, ar_nxt);
-            }
+            describe(has_nxt ? t + tstep : t, nxt);
+            woffs(nxt, wo_nxt);
+            arows_raw(nxt, ar_nxt);
+            ep_load(cur);
+            // Once per tile, wait for every outstanding load (the weights of the new tile's first
+            // positions are among them): afterwards the values fetched here are known complete, so
+            // no later position has to wait for the whole load stream to reach them.
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
         } else {
             b++;
         }

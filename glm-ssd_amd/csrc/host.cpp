@@ -688,8 +688,8 @@ hipError_t grouped_launch(int kind, int ty, GroupedArgs &a, int n_pairs, hipStre
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
     const int threads = 64 * sh.wv;
-    // decode tables (65 KB) + two staged activation super-blocks
-    const size_t lds = 65536 + 1024 + 2 * (size_t)16 * sh.nt * 512;
+    // decode tables (80 KB, grouped.hip GS_GRP_TAB_BYTES) + two staged activation super-blocks
+    const size_t lds = 16384 + 65536 + 2 * (size_t)16 * sh.nt * 512;
     int per_cu = 1;
     {
         std::lock_guard<std::mutex> lk(g_mu);
