@@ -11,6 +11,7 @@ gs_blob_##NAME##_end:                    \
 
 BLOB(common, "build/common.hsaco")
 BLOB(grouped, "build/grouped.hsaco")
+BLOB(gemm, "build/gemm.hsaco")
 BLOB(t0, "build/t0.hsaco")
 BLOB(t1, "build/t1.hsaco")
 BLOB(t8, "build/t8.hsaco")

@@ -1,0 +1,239 @@
+// gfx950 quantized GEMM for token batches (gs_gemm: prefill projections, MoE expert groups run
+// one expert at a time, MTP verification) -- crates/cuda/kernels/gemm.cu:13-123 semantics:
+//
+//   Y[n][r] (+)= sum_k f16(deq(W[r][k])) * f16(X[n][k])     f32 accumulation
+//
+// Dequantized weights and activations are rounded to f16 exactly as the reference's tiles are
+// (round to nearest even); the products run on v_mfma_f32_16x16x32_f16.
+//
+// Tile: 128 weight rows x 64 tokens per workgroup of 4 waves; a wave owns 32 rows (two 16-row
+// MFMA column blocks) and all 64 tokens (four 16-token row blocks): 8 accumulators, each A
+// fragment (tokens) feeds 2 MFMAs and each B fragment (weights) 4. The K loop steps one
+// 256-element super-block at a time:
+//   * raw weight bytes of the tile's rows (one super-block each) are copied into LDS with 16-byte
+//     loads (one buffer resource per tile, so the tail of the last row reads zeros, never past
+//     the matrix), prefetched one step ahead through registers; each lane then decodes its own
+//     two 32-element units of each of its rows from LDS with the exact unit decoders (exact.h)
+//     and rounds them to f16;
+//   * X rows are converted to f16 into LDS (one step ahead), 512 bytes per token row, 16-byte
+//     chunk c of token i at chunk position c ^ (i & 15) so the 16 lanes reading one chunk column
+//     hit distinct banks;
+//   * the K order inside a super-block is permuted so a lane's B fragments come from whole units:
+//     lane quarter q (lane >> 4) owns units 2q and 2q+1, MFMA m (0..7) takes 8-element group m&3
+//     of unit 2q + (m>>2); the A fragments use the same permutation, so each dot product is
+//     unchanged.
+// Plain formats (F32, F16, BF16) skip the LDS copy: a lane reads its units straight from memory.
+// Workgroup order: the token blocks of one row block run back to back on one XCD (workgroup w
+// is dispatched to XCD w % 8), so the row block's weights come from that XCD's L2 after the first.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "kargs.h"
+#include "formats.h"
+
+typedef _Float16 gh8 __attribute__((ext_vector_type(8)));
+typedef float gf4 __attribute__((ext_vector_type(4)));
+
+#define GM_WV 4
+#define GM_NTH (64 * GM_WV)
+#define GM_RB 128   // weight rows per workgroup (GM_WV waves x 2 x 16)
+#define GM_TN 64    // tokens per workgroup (4 x 16)
+
+// 8 floats -> 8 halves (round to nearest even, as __floats2half2_rn)
+__device__ __forceinline__ gh8 to_h8(const float *v) {
+    return __builtin_bit_cast(gh8, make_uint4(f2h(v[0]) | (f2h(v[1]) << 16), f2h(v[2]) | (f2h(v[3]) << 16),
+                                              f2h(v[4]) | (f2h(v[5]) << 16), f2h(v[6]) | (f2h(v[7]) << 16)));
+}
+
+template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
+struct GemmFmt {
+    static constexpr bool PLAIN = QKB == 1;
+    // bytes of one 256-element super-block of a row, and its LDS slot (16-byte multiple)
+    static constexpr int SB = QKB == 1 ? 256 * BB : 256 / QKB * BB;
+    // LDS slot: the super-block is copied from the 4-byte boundary at or below its start (buffer
+    // loads at 2-byte alignment are avoided), so a slot holds up to 3 leading bytes more
+    static constexpr int SBP = (SB + 3 + 15) & ~15;
+    // exact decode of 32-element unit u (0..7) of a super-block starting at p
+    __device__ static __forceinline__ void unit(const uint8_t *p, int u, float (&v)[32]) {
+        if (QKB == 256) DEC(p, u, v);
+        else if (QKB == 32) DEC(p + u * BB, 0, v);
+        else DEC(p + 32 * u * BB, 0, v);
+    }
+};
+
+template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
+__device__ __forceinline__ void gemm_body(const GemmArgs &a) {
+    using F = GemmFmt<QKB, BB, DEC>;
+    constexpr int CPR = F::PLAIN ? 1 : F::SBP / 16;                 // raw 16-byte chunks per row
+    constexpr int NRAW = F::PLAIN ? 1 : (GM_RB * CPR + GM_NTH - 1) / GM_NTH;
+    constexpr int RAWB = F::PLAIN ? 16 : GM_RB * F::SBP;            // one raw buffer
+    constexpr int ASLAB = GM_TN * 512;                              // one f16 activation buffer
+    constexpr int NXA = GM_TN * 32 / GM_NTH;                        // 16-byte A chunks per thread (8)
+    extern __shared__ __align__(16) uint8_t gm_lds[];
+    uint8_t *const rawbuf = gm_lds;
+    uint8_t *const abuf = gm_lds + 2 * RAWB;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 15, q = lane >> 4;
+    // workgroup -> (row block, token block): row block r on XCD r % 8, its token blocks in a row
+    const int L = blockIdx.x, xcd = L & 7, k8 = L >> 3;
+    const int rblk = xcd + 8 * (k8 / a.n_tb), tblk = k8 % a.n_tb;
+    if (rblk >= a.n_rb) return;
+    const int z = blockIdx.y;
+    const uint8_t *W = a.W + (int64_t)z * a.w_bs;
+    const float *X = a.X + (int64_t)z * a.x_bs;
+    float *Y = a.Y + (int64_t)z * a.y_bs;
+    const int K = a.K, rows = a.rows, N = a.N, nsb = K / 256 + (K % 256 != 0);
+    const int r0 = rblk * GM_RB, n0 = tblk * GM_TN;
+    const int nrows = min(GM_RB, rows - r0), ntok = min(GM_TN, N - n0);
+    const int64_t rs = a.row_stride;
+
+    // raw copy: chunk z = tid + GM_NTH*i -> tile row z / CPR, chunk z % CPR, read from the row's
+    // super-block start rounded down to 4 bytes; one buffer resource per tile bounded at the tile's
+    // last valid byte
+    const int64_t row_bytes = (int64_t)(K / QKB) * BB;
+    // the resource starts at the 4-byte boundary at or below the tile's first row (d0 bytes
+    // before it) and ends at the 4-byte boundary at or above its last byte: every read is
+    // dword-aligned and the range check passes every dword that holds a byte of the tile
+    const uint8_t *tile = W + (int64_t)r0 * rs;
+    const uint32_t d0 = (uint32_t)((uintptr_t)tile & 3u);
+    const BufferAt wt(tile - d0, 0,
+                      F::PLAIN ? 0u : (uint32_t)((d0 + (int64_t)(nrows - 1) * rs + row_bytes + 3) & ~(int64_t)3));
+    uint32_t roff[NRAW];
+    int rdst[NRAW];
+#pragma unroll
+    for (int i = 0; i < NRAW; i++) {
+        const int zc = tid + GM_NTH * i, rr = min(zc / CPR, nrows - 1), c = zc % CPR;
+        roff[i] = d0 + (uint32_t)((int64_t)rr * rs) + 16u * c;
+        rdst[i] = zc < GM_RB * CPR ? (zc / CPR) * F::SBP + 16 * c : -1;
+    }
+    auto raw_load = [&](int b, uint4 (&rv)[NRAW]) {
+        if constexpr (!F::PLAIN) {
+#pragma unroll
+            for (int i = 0; i < NRAW; i++) rv[i] = wt.u128((roff[i] + (uint32_t)(F::SB * b)) & ~3u);
+        }
+    };
+    auto raw_store = [&](int buf, const uint4 (&rv)[NRAW]) {
+        if constexpr (!F::PLAIN) {
+#pragma unroll
+            for (int i = 0; i < NRAW; i++)
+                if (rdst[i] >= 0) *(uint4 *)(rawbuf + buf * RAWB + rdst[i]) = rv[i];
+        }
+    };
+    // activations: A chunk y = tid + GM_NTH*i -> token row y >> 5, 8-element chunk y & 31
+    auto x_load = [&](int b, float4 (&xv)[NXA][2]) {
+#pragma unroll
+        for (int i = 0; i < NXA; i++) {
+            const int y = tid + GM_NTH * i, t = y >> 5, c = y & 31;
+            const int kk = 256 * b + 8 * c;
+            if (t < ntok && kk < K) {
+                const float4 *p = (const float4 *)(X + (int64_t)(n0 + t) * a.x_stride + kk);
+                xv[i][0] = p[0];
+                xv[i][1] = p[1];
+            } else {
+                xv[i][0] = xv[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
+    auto x_store = [&](int buf, const float4 (&xv)[NXA][2]) {
+#pragma unroll
+        for (int i = 0; i < NXA; i++) {
+            const int y = tid + GM_NTH * i, t = y >> 5, c = y & 31;
+            const float f[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                                xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+            *(gh8 *)(abuf + buf * ASLAB + t * 512 + ((c ^ (t & 15)) << 4)) = to_h8(f);
+        }
+    };
+
+    gf4 acc[4][2];
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+        for (int n = 0; n < 2; n++) acc[tt][n] = gf4{0.f, 0.f, 0.f, 0.f};
+
+    {   // prologue: super-block 0
+        uint4 rv[NRAW];
+        float4 xv[NXA][2];
+        raw_load(0, rv);
+        x_load(0, xv);
+        raw_store(0, rv);
+        x_store(0, xv);
+    }
+    __syncthreads();
+
+    const int ntt = (ntok + 15) >> 4;   // token row blocks with any token (wave-uniform)
+    for (int b = 0; b < nsb; b++) {
+        const int buf = b & 1;
+        const bool more = b + 1 < nsb;
+        // next super-block in flight while this one is decoded and contracted (issued on the last
+        // step too, re-reading that step's data, so every wait on them is an exact count)
+        uint4 rv[NRAW];
+        float4 xv[NXA][2];
+        raw_load(more ? b + 1 : b, rv);
+        x_load(more ? b + 1 : b, xv);
+        // B fragments: units 2q, 2q+1 of this lane's two rows, rounded to f16
+        gh8 bf[2][2][4];
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            const int rr = min(wave * 32 + 16 * n + j, nrows - 1);
+#pragma unroll
+            for (int hu = 0; hu < 2; hu++) {
+                float v[32];
+                if (256 * b + 32 * (2 * q + hu) >= K) {   // past the row (K % 256 != 0): zero weights
+#pragma unroll
+                    for (int e = 0; e < 32; e++) v[e] = 0.f;
+                } else if constexpr (F::PLAIN) {
+                    F::unit(W + (int64_t)(r0 + rr) * rs + (int64_t)256 * b * BB, 2 * q + hu, v);
+                } else {
+                    const uint32_t lead = (uint32_t)(d0 + (int64_t)rr * rs + (int64_t)F::SB * b) & 3u;
+                    F::unit(rawbuf + buf * RAWB + rr * F::SBP + lead, 2 * q + hu, v);
+                }
+#pragma unroll
+                for (int g = 0; g < 4; g++) bf[n][hu][g] = to_h8(v + 8 * g);
+            }
+        }
+        // contraction: MFMA m takes group m & 3 of unit 2q + (m >> 2)
+        const uint8_t *slab = abuf + buf * ASLAB;
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const int cc = 8 * q + m;   // = 8q + 4 (m >> 2) + (m & 3)
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) {
+                if (tt < ntt) {
+                    const gh8 av = *(const gh8 *)(slab + (16 * tt + j) * 512 + ((cc ^ j) << 4));
+#pragma unroll
+                    for (int n = 0; n < 2; n++)
+                        acc[tt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[n][m >> 2][m & 3], acc[tt][n], 0, 0, 0);
+                }
+            }
+        }
+        if (more) {
+            raw_store(buf ^ 1, rv);
+            x_store(buf ^ 1, xv);
+        }
+        __syncthreads();
+    }
+
+    // lane holds tokens 16tt + 4q + i of row 32 wave + 16n + j
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 16 * tt + 4 * q + i;
+            if (t < ntok) {
+#pragma unroll
+                for (int n = 0; n < 2; n++) {
+                    const int rr = wave * 32 + 16 * n + j;
+                    if (rr < nrows) {
+                        float *dst = Y + (int64_t)(n0 + t) * a.y_stride + r0 + rr;
+                        *dst = a.accumulate ? *dst + acc[tt][n][i] : acc[tt][n][i];
+                    }
+                }
+            }
+        }
+}
+
+#define GS_GEMM_KERNEL(TY, QKB, BB, DEC)                                                          \
+    extern "C" __global__ void __launch_bounds__(GM_NTH) gs_k_gemm_##TY(GemmArgs a) {               \
+        gemm_body<QKB, BB, DEC>(a);                                                              \
+    }
+GS_TYPE_LIST(GS_GEMM_KERNEL)

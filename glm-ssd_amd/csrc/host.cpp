@@ -28,7 +28,7 @@
 #define GS_BLOB(NAME)                                 \
     extern "C" const unsigned char gs_blob_##NAME##_start[]; \
     extern "C" const unsigned char gs_blob_##NAME##_end[];
-#define GS_BLOB_LIST(X) X(common) X(grouped) X(t0) X(t1) X(t8) X(t10) X(t11) X(t12) X(t13) X(t14) X(t16) X(t18) X(t22) X(t23) X(t30)
+#define GS_BLOB_LIST(X) X(common) X(grouped) X(gemm) X(t0) X(t1) X(t8) X(t10) X(t11) X(t12) X(t13) X(t14) X(t16) X(t18) X(t22) X(t23) X(t30)
 GS_BLOB_LIST(GS_BLOB)
 
 namespace {
@@ -569,23 +569,47 @@ GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int6
 }
 
 // =============================================================================================
-// GEMM (gemm.cu:107-123): token batches of 8 through the streaming kernel
+// GEMM (gemm.cu:107-123): MFMA tiles of 128 weight rows x 64 tokens (gemm.hip)
 // =============================================================================================
 GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride,
                       float *Y, int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs,
                       int64_t y_bs, void *s) {
-    if (K % 32 != 0 || N < 1 || n_batch < 1 || x_stride % 4 != 0) return hipErrorInvalidValue;
+    if (K <= 0 || K % 32 != 0 || N < 1 || n_batch < 1 || x_stride % 4 != 0 || rows < 0) return hipErrorInvalidValue;
     int qk, bb;
     if (!geometry(ty, qk, bb) || K % ggml_block_elems(ty) != 0) return hipErrorInvalidValue;
-    for (int z = 0; z < n_batch; z++) {
-        for (int n0 = 0; n0 < N; n0 += 8) {
-            const int nb = std::min(8, N - n0);
-            int rc = gemv_impl(ty, (const uint8_t *)W + z * w_bs, row_stride, K, rows, X + z * x_bs + n0 * x_stride,
-                               x_stride, Y + z * y_bs + n0 * y_stride, y_stride, nb, accumulate, 1, 0, 0, 0, s);
-            if (rc) return rc;
-        }
-    }
-    return 0;
+    // X rows are read as float4 (the reference's contract: 16-byte aligned rows)
+    if (!aligned16(X) || (n_batch > 1 && x_bs % 4 != 0)) return hipErrorInvalidValue;
+    if (!check_w(W, row_stride) || (n_batch > 1 && (w_bs & 1))) return hipErrorInvalidValue;
+    if (rows == 0) return 0;
+    // bytes of one 256-element super-block of a row and its LDS slot (gemm.hip GemmFmt::SB, SBP:
+    // up to 3 leading bytes more, rounded to 16)
+    const int eb = ggml_block_elems(ty);
+    const int sb = eb == 1 ? 256 * (bb / qk) : 256 / eb * bb;
+    const int sbp = (sb + 3 + 15) & ~15;
+    const bool plain = eb == 1;
+    const size_t lds = 2 * (plain ? 16 : (size_t)128 * sbp) + 2 * (size_t)64 * 512;
+    GemmArgs a;
+    memset(&a, 0, sizeof(a));
+    a.W = (const uint8_t *)W;
+    a.X = X;
+    a.Y = Y;
+    a.row_stride = row_stride;
+    a.x_stride = x_stride;
+    a.y_stride = y_stride;
+    a.w_bs = w_bs;
+    a.x_bs = x_bs;
+    a.y_bs = y_bs;
+    a.K = K;
+    a.rows = rows;
+    a.N = N;
+    a.accumulate = accumulate;
+    a.n_rb = (rows + 127) / 128;
+    a.n_tb = (N + 63) / 64;
+    // row block r runs on XCD r % 8 (workgroup w -> XCD w % 8): 8 x ceil(n_rb / 8) x n_tb workgroups
+    const int64_t nwg = (int64_t)8 * ((a.n_rb + 7) / 8) * a.n_tb;
+    if (nwg > 0x7fffffff || n_batch > 65535) return hipErrorInvalidValue;
+    return launch("gs_k_gemm_" + std::to_string(ty), dim3((unsigned)nwg, n_batch, 1), dim3(256, 1, 1), lds,
+                  (hipStream_t)s, a);
 }
 
 // =============================================================================================

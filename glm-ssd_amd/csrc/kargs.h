@@ -113,3 +113,16 @@ struct RowsQArgs {
     int K;
     int nrows;
 };
+
+// Quantized GEMM (gemm.hip): Y[z][n][r] (+)= sum_k f16(deq(W[z][r][k])) * f16(X[z][n][k])
+struct GemmArgs {
+    const uint8_t *W;
+    const float *X;
+    float *Y;
+    int64_t row_stride;   // bytes between weight rows
+    int64_t x_stride;     // floats between X rows
+    int64_t y_stride;     // floats between Y rows
+    int64_t w_bs, x_bs, y_bs;   // per blockIdx.y (z) batch strides: bytes / floats / floats
+    int K, rows, N, accumulate;
+    int n_rb, n_tb;       // row blocks and token blocks of one problem
+};

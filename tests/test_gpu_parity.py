@@ -287,14 +287,82 @@ def test_elementwise_and_rows(stream):
     assert np.allclose(da.download(np.float32, 64 * width, stream).reshape(64, width), want, rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("ty", [T.IQ2_XXS, T.Q4_K])
-def test_gemm_matches_oracle(ty, stream):
-    K, rows, N = 1024, 160, 37
+# gs_gemm has the reference's multi-token GEMM semantics (gemm.cu:57-78): weights dequantized and
+# rounded to f16, activations rounded to f16, f32 accumulation -- the oracle's act="f16" computes
+# the same products exactly, in f64, so only the summation order differs (tight bound below). The
+# q8_1 GEMV of the same rows is within the north-star bound of it.
+GEMM_REL = 1e-5
+
+
+def _gemm_case(ty, K, rows, N, stream, seed, accumulate=False, x_stride=None, y_stride=None):
     rb = G.row_bytes(ty, K)
-    raw = O.Rng(31).random_blocks(ty, rows * K)
-    X = np.random.default_rng(2).standard_normal((N, K)).astype(np.float32)
-    want = O.gemv(ty, raw, rb, K, rows, X, B=N)
+    if ty == T.BF16:
+        v = np.random.default_rng(seed).standard_normal(rows * K).astype(np.float32)
+        raw = (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+    else:
+        raw = O.Rng(seed).random_blocks(ty, rows * K)
+        if ty in (T.F16, T.F32):   # finite values
+            v = np.random.default_rng(seed).standard_normal(rows * K)
+            raw = v.astype(np.float16 if ty == T.F16 else np.float32).view(np.uint8)
+    xs = K if x_stride is None else x_stride
+    ys = rows if y_stride is None else y_stride
+    X = np.random.default_rng(seed + 1).standard_normal((N, xs)).astype(np.float32)
+    want = O.gemv(ty, raw, rb, K, rows, X, B=N, x_stride=xs, act="f16", nthreads=8)
+    # prior contents on the scale of the product (accumulate: the f32 sum then keeps its bits)
+    y0 = (np.random.default_rng(seed + 2).standard_normal((N, ys)) * np.std(want)).astype(np.float32)
+    dw, dx, dy = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer.from_array(y0)
+    G.ops.gemm(ty, dw, rb, K, rows, dx, xs, dy, ys, N, accumulate, 1, 0, 0, 0, stream)
+    got = dy.download(np.float32, N * ys, stream).reshape(N, ys)
+    assert np.array_equal(got[:, rows:], y0[:, rows:])   # padding columns untouched
+    if accumulate:
+        got = got.astype(np.float64) - y0
+    return rel_l2(got[:, :rows], want)
+
+
+@pytest.mark.parametrize("ty", [T.IQ2_XXS, T.IQ3_XXS, T.Q4_K, T.Q6_K, T.Q8_0])
+@pytest.mark.parametrize("N", [9, 37, 512])
+def test_gemm_hot_types(ty, N, stream):
+    K, rows = (2048, 300) if N < 512 else (1024, 200)
+    e = _gemm_case(ty, K, rows, N, stream, seed=100 * ty + N)
+    say(f"gemm {G.TYPE_NAMES[ty]} N={N}: rel-L2 {e:.2e}")
+    assert e <= GEMM_REL
+
+
+@pytest.mark.parametrize("ty", [t for t in ALL])
+def test_gemm_every_type(ty, stream):
+    e = _gemm_case(ty, 512, 131, 70, stream, seed=7 * ty)
+    say(f"gemm {G.TYPE_NAMES[ty]}: rel-L2 {e:.2e}")
+    assert e <= GEMM_REL
+
+
+def test_gemm_accumulate_strides_and_partial_superblock(stream):
+    # Q8_0 with K = 800 (the last 256-element step is partial), strided X / Y, accumulate
+    assert _gemm_case(T.Q8_0, 800, 129, 65, stream, 11, accumulate=True, x_stride=804, y_stride=133) <= GEMM_REL
+    assert _gemm_case(T.F32, 96, 40, 3, stream, 12, x_stride=100) <= GEMM_REL
+
+
+def test_gemm_batched(stream):
+    # n_batch = 3 independent problems (per-head matrices), non-zero batch strides
+    ty, K, rows, N, nb = T.Q4_K, 512, 144, 20, 3
+    rb = G.row_bytes(ty, K)
+    raw = O.Rng(5).random_blocks(ty, nb * rows * K)
+    X = np.random.default_rng(6).standard_normal((nb, N, K)).astype(np.float32)
+    dw, dx, dy = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(nb * N * rows * 4)
+    G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, nb, rows * rb, N * K, N * rows, stream)
+    got = dy.download(np.float32, nb * N * rows, stream).reshape(nb, N, rows)
+    for z in range(nb):
+        want = O.gemv(ty, raw[z * rows * rb:(z + 1) * rows * rb], rb, K, rows, X[z], B=N, act="f16")
+        assert rel_l2(got[z], want) <= GEMM_REL
+
+
+def test_gemm_vs_gemv_semantics(stream):
+    # the f16 GEMM and the q8_1 GEMV of the same rows agree within the north-star bound
+    ty, K, rows, N = T.IQ2_XXS, 2048, 256, 8
+    rb = G.row_bytes(ty, K)
+    raw = O.Rng(9).random_blocks(ty, rows * K)
+    X = np.random.default_rng(10).standard_normal((N, K)).astype(np.float32)
     dw, dx, dy = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(N * rows * 4)
     G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, stream)
     got = dy.download(np.float32, N * rows, stream).reshape(N, rows)
+    want = O.gemv(ty, raw, rb, K, rows, X, B=N, act="f32")
     assert rel_l2(got, want) <= REL_L2
