@@ -58,6 +58,8 @@ def bench_lib():
                              C.c_int, P, C.POINTER(C.c_float)]
     L.bn_copy.argtypes = [P, P, C.c_size_t, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_read.argtypes = [P, C.c_int, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
+    L.bn_gemm.argtypes = [C.c_int, P, C.c_int, I64, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P,
+                          C.POINTER(C.c_float)]
     L.bn_moe_grouped.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, P, P, P, P, C.c_int, I64, C.c_int, C.c_int, I64, P, P,
                                  P, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     return L
@@ -250,6 +252,30 @@ def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 
     return dict(ms=ms.value, bytes=raw.nbytes, gbps=raw.nbytes / (ms.value * 1e-3) / 1e9, copies=n)
 
 
+def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 << 20):
+    """gs_gemm (f16 MFMA tiles) of N tokens through a rows x K matrix, weight copies rotated."""
+    import glmssd as G
+    rng = np.random.default_rng(seed)
+    raw = make(rng, rows, K)
+    n = max(2, -(-min_rot_bytes // raw.nbytes))
+    buf = G.DeviceBuffer(n * raw.nbytes)
+    buf.upload(raw, s)
+    for i in range(1, n):
+        G.check(G.lib().gs_memcpy_d2d(buf.ptr(i * raw.nbytes), buf.p, raw.nbytes, s.raw()))
+    s.sync()
+    ptrs = (C.c_void_p * n)(*[buf.p.value + i * raw.nbytes for i in range(n)])
+    x = G.DeviceBuffer.from_array(rng.standard_normal(N * K).astype(np.float32), s)
+    y = G.DeviceBuffer(N * rows * 4)
+    ms = C.c_float()
+    G.check(L.bn_gemm(ty, C.cast(ptrs, C.c_void_p), n, G.row_bytes(ty, K), K, rows, x.p, y.p, N, steps, warmup,
+                      s.raw(), C.byref(ms)))
+    t = ms.value * 1e-3
+    flops = 2.0 * N * rows * K
+    return {"us_per_call": round(ms.value * 1e3, 2), "TFLOPs": round(flops / t / 1e12, 1),
+            "frac_mfma_f16_peak": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "weight_GBps": round(raw.nbytes / t / 1e9, 1), "tokens": N, "rotated_copies": n}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -366,6 +392,14 @@ def main():
                 "GB/s": round(rb["gbps"], 1), "us_per_call": round(rb["ms"] * 1e3, 2),
                 "frac_hbm_peak": round(rb["gbps"] / HBM_PEAK_GBPS, 4), "weight_bytes": rb["bytes"], "vectors": B}
             log(f"config1 B={B}: {rb['ms'] * 1e3:.2f} us, {rb['gbps']:.1f} GB/s")
+        from glmssd import synth as S
+        iq = lambda rng, rows, K: S.random_blocks(rng, G.GgmlType.IQ2_XXS, rows * K, 0.02, [0])
+        for name, ty, rows, K, N, mk in [("gemm_q4_k_k4096_rows12288_N512", G.GgmlType.Q4_K, 12288, 4096, 512, S.q4_k_matrix),
+                                         ("gemm_q8_0_k4096_rows4096_N512", G.GgmlType.Q8_0, 4096, 4096, 512, S.q8_0_matrix),
+                                         ("gemm_iq2_xxs_k4096_rows1536_N64", G.GgmlType.IQ2_XXS, 1536, 4096, 64, iq)]:
+            r = run_gemm(L, s, ty, rows, K, N, mk, max(20, args.steps // 5), max(5, args.warmup // 5), 9)
+            secondary[name] = r
+            log(f"{name}: {r}")
         rc = run_read_ceiling(L, s, [17825792, 25952256, 38928384, 41287680, 1 << 30], args.steps, args.warmup)
         secondary["plain_read_ceiling"] = rc
         log(f"plain-read ceiling: {rc}")

@@ -180,3 +180,19 @@ BN_EXPORT int bn_read(const void *const *bases, int nb, size_t bytes, int steps,
     *ms /= steps;
     return 0;
 }
+
+// gs_gemm over rotating weight copies Ws[i % nw]: Y[N][rows] = X[N][K] . W^T; mean ms per call.
+BN_EXPORT int bn_gemm(int ty, const void *const *Ws, int nw, int64_t rs, int K, int rows, const float *X, float *Y,
+                      int N, int steps, int warmup, void *s, float *ms) {
+    Timer t;
+    CK(t.init());
+    for (int i = 0; i < warmup; i++) CK(gs_gemm(ty, Ws[i % nw], rs, K, rows, X, K, Y, rows, N, 0, 1, 0, 0, 0, s));
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    for (int i = 0; i < steps; i++) CK(gs_gemm(ty, Ws[i % nw], rs, K, rows, X, K, Y, rows, N, 0, 1, 0, 0, 0, s));
+    CK(gs_event_record(t.b, s));
+    CK(gs_event_sync(t.b));
+    CK(gs_event_elapsed_ms(ms, t.a, t.b));
+    *ms /= steps;
+    return 0;
+}

@@ -20,7 +20,6 @@
 #include "../../include/glmssd.h"
 #include "kargs.h"
 
-#define GS_BAR_SLOTS 64   // grid-barrier counter slots per code object (gridbar.h)
 
 #define GS_EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -52,7 +51,6 @@ struct DeviceCtx {
     size_t max_lds = 0;
     hipError_t init_err = hipSuccess;
     std::map<std::pair<std::string, int>, int> occ;  // (kernel, lds) -> blocks per CU
-    std::atomic<uint64_t> bar_seq{0};                // fused-FFN launches (grid-barrier slot rotation)
 };
 
 std::mutex g_mu;
@@ -493,77 +491,15 @@ GS_EXPORT int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_strid
     return 0;
 }
 
-// fused FFN kernels exist for these (gate/up, down) format pairs (kernels.hip GS_FFN_ALL)
-static bool ffn_pair(int ty_gu, int ty_dn) {
-    if (ty_gu == GS_IQ2_XXS && ty_dn == GS_IQ3_XXS) return true;
-    return ty_gu == ty_dn && (ty_gu == GS_Q8_0 || ty_gu == GS_Q4_K || ty_gu == GS_Q6_K || ty_gu == GS_IQ2_XXS ||
-                              ty_gu == GS_IQ3_XXS);
-}
-
 // Routed-expert FFN of one layer: exactly gs_moe_gateup followed by gs_moe_down (h is written
-// too). For one token whose down pass fits one launch this is a single fused launch (gate/up,
-// grid barrier, down); otherwise the two launches.
-// bound of the fused FFN's grid-barrier wait, in ticks of the 100 MHz clock (0.2 s)
-constexpr uint64_t kFfnWaitTicks = 20000000ull;
-std::atomic<uint64_t> g_ffn_wait_ticks{kFfnWaitTicks};
-
-GS_EXPORT int gs_moe_ffn_set_wait_limit(uint64_t ticks) {
-    g_ffn_wait_ticks.store(ticks ? ticks : kFfnWaitTicks);
-    return 0;
-}
-
-GS_EXPORT int gs_moe_ffn_status(int *expired) {
-    if (!expired) return hipErrorInvalidValue;
-    *expired = 0;
-    hipError_t e;
-    DeviceCtx *c = ctx(&e);
-    if (!c) return e;
-    if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-    for (hipModule_t m : c->mods) {   // every per-format code object holds its own flag
-        hipDeviceptr_t p;
-        size_t sz;
-        if (hipModuleGetGlobal(&p, &sz, m, "gs_ffn_timeout") != hipSuccess || sz != sizeof(unsigned)) continue;
-        unsigned v = 0;
-        if ((e = hipMemcpyDtoH(&v, p, sizeof v)) != hipSuccess) return e;
-        if (v) {
-            *expired = 1;
-            const unsigned zero = 0;
-            if ((e = hipMemcpyHtoD(p, (void *)&zero, sizeof zero)) != hipSuccess) return e;
-        }
-    }
-    (void)hipGetLastError();   // clear the lookup misses of modules without fused kernels
-    return 0;
-}
-
+// too), as two launches. (A one-launch variant with a grid-wide barrier between the two passes was
+// measured slower once the barrier carries the agent-scope release/acquire fences its cross-XCD
+// hand-over of h needs: 27 us against 18 us for config 2.)
 GS_EXPORT int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int64_t rs_gu, int n_embd, int n_ff,
                          int64_t rs_dn, const float *x, float *h, float *y, float lim, void *s) {
     int rc = moe_check(ty_gu, b, nt, n_embd, n_ff, rs_gu);
     if (rc) return rc;
     if ((rc = moe_check(ty_dn, b, nt, n_ff, n_embd, rs_dn))) return rc;
-    bool fuse = nt == 1 && ffn_pair(ty_gu, ty_dn) && b->n <= down_per_launch(nt, n_ff);
-    hipError_t e;
-    DeviceCtx *c = ctx(&e);
-    if (!c) return e;
-    FfnArgs fa;
-    StreamPlan P1, P2;
-    if (fuse) {
-        if ((rc = gateup_args(fa.gu, b, nt, rs_gu, n_embd, n_ff, x, h, lim))) return rc;
-        if ((rc = down_args(fa.dn, b, 0, b->n, nt, rs_dn, n_ff, n_embd, h, y))) return rc;
-        fuse = plan_stream(c, 1, ty_gu, fa.gu, P1) == hipSuccess && plan_stream(c, 2, ty_dn, fa.dn, P2) == hipSuccess &&
-               fa.gu.lpr == 64 && fa.dn.lpr == 64 && fa.dn.wlo;   // what the fused kernels fix
-    }
-    if (fuse) {
-        fa.wait_ticks = g_ffn_wait_ticks.load();
-        fa.slot = (int)(c->bar_seq.fetch_add(1) % GS_BAR_SLOTS);
-        const std::string name = "gs_k_ffn_" + std::to_string(ty_gu) + "_" + std::to_string(ty_dn) + "_" +
-                                 std::to_string(P1.um) + "_" + std::to_string(P2.um);
-        const size_t lds = std::max(P1.lds, P2.lds);
-        hipFunction_t f;
-        if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
-        // the barrier needs every workgroup resident at once: one per CU, within the occupancy limit
-        const int per_cu = blocks_per_cu(c, name, f, lds);
-        if (per_cu >= 1) return launch(name, dim3(c->cu_count, 1, 1), dim3(GS_WG, 1, 1), lds, (hipStream_t)s, fa);
-    }
     if ((rc = gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, lim, s))) return rc;
     return gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y, s);
 }

@@ -46,14 +46,6 @@ struct StreamArgs {
                                      // rows lie within 4 GiB above it (32-bit offsets)
 };
 
-// Fused MoE FFN (gate/up + SwiGLU, grid barrier, down + combine) for one token
-struct FfnArgs {
-    StreamArgs gu;         // kind 1: gate/up -> h
-    StreamArgs dn;         // kind 2: h -> y (accumulated)
-    uint64_t wait_ticks;   // bound of the grid-barrier wait (100 MHz clock ticks)
-    int slot;              // barrier counter slot of this launch (0 .. GS_BAR_SLOTS-1)
-};
-
 // Whole-tensor dequantization
 struct DequantArgs {
     const uint8_t *src;

@@ -5,7 +5,6 @@
 #include <stdint.h>
 #include "kargs.h"
 #include "formats.h"
-#include "gridbar.h"
 
 // =============================================================================================
 // q8_1 activation quantization of one 32-element unit, in registers.
@@ -744,95 +743,10 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     GS_STREAM_KERNEL_W(F, NAME, 2, 6) GS_STREAM_KERNEL_W(F, NAME, 2, 8)
 #define GS_STREAM_ALL(F, NAME) GS_STREAM_MV(F, NAME, 0) GS_STREAM_GU(F, NAME) GS_STREAM_MV(F, NAME, 2) GS_STREAM_W(F, NAME)
 
-// =============================================================================================
-// Fused routed-expert FFN for one decode token: gate/up + SwiGLU for every expert of the batch,
-// a grid-wide barrier, then down + weighted combine, in one launch (the same work as
-// gs_moe_gateup followed by gs_moe_down). The second launch's start-up (dispatch, argument
-// fetch, first-load latency) disappears, and the down weights are requested before the
-// barrier, so they stream in while the slowest workgroups finish gate/up.
-//
-// The grid must be co-resident (the host sizes it to the occupancy limit); the barrier and its
-// memory ordering are gridbar.h's.
-// =============================================================================================
-template <class F1, class F2, int UM1, int UM2>
-__device__ __forceinline__ void ffn_body(const FfnArgs &fa) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const unsigned gen0 = threadIdx.x == 0 ? bar_generation(fa.slot) : 0;
-    // a down format with other tables: staged with the gate/up ones (separate LDS arrays; the
-    // sign selectors are common), so the down units can be decoded before the barrier
-    constexpr bool SAME = is_same_t<F1, F2>::value;
-    typename F2::TabReg t2;
-    if (!SAME) F2::tab_load(threadIdx.x, t2);
-    {
-        StreamPass<F1, 1, 1, UM1, 64> G(fa.gu, smem);   // the host fuses only 64-lane gate/up plans
-        G.issue_x();
-        G.issue_tab();
-        G.bind();
-        constexpr int E = G.RING && GS_RING_EARLY < G.PF ? GS_RING_EARLY : G.PF;
-        G.load_batch(G.gid, 0, E);
-        G.stage_x();
-        if (!SAME) F2::tab_store(threadIdx.x, t2);
-        __syncthreads();
-        G.load_batch(G.gid, E, G.PF);
-        G.run_rows();
-    }
-    __syncthreads();   // orders every wave's h stores before thread 0's release
-    if (threadIdx.x == 0) {
-        bar_release();
-        bar_arrive(fa.slot);
-    }
-    StreamPass<F2, 2, 1, UM2, 64> D(fa.dn, smem);   // the host fuses only 64-lane down plans with wlo
-    D.issue_tab();
-    D.bind();
-    D.load_batch(D.gid);   // down weights in flight across the barrier
-    // IQ formats, one batch of rows per wave: the down units are decoded (table reads, signs)
-    // while the workgroup waits for the grid and for h, leaving only the dots for afterwards.
-    constexpr bool PRE = decltype(D)::PRE;
-    const bool pre = PRE && D.single_batch();
-    if (pre) D.predecode();
-    if (threadIdx.x == 0) bar_wait(fa.slot, gen0, fa.wait_ticks);
-    // the other waves order their h loads after thread 0's acquire through the workgroup barrier
-    // (a workgroup-scope acquire: it waits for no outstanding load, so the down weights keep
-    // streaming)
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    D.issue_x();           // h, complete in every expert
-    D.stage_x();
-    __syncthreads();
-    if constexpr (PRE) {
-        if (pre) D.template run_rows<true>();
-        else D.run_rows();
-    } else {
-        D.run_rows();
-    }
-}
-
-#define GS_FFN_KERNEL(F1, N1, F2, N2, UM1, UM2)                                                  \
-    extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE))) \
-        gs_k_ffn_##N1##_##N2##_##UM1##_##UM2(FfnArgs a) {                                        \
-        ffn_body<F1, F2, UM1, UM2>(a);                                                          \
-    }
-// (gate/up units per lane, down units per lane): the unit budgets the host picks for one token
-#define GS_FFN_ALL(F1, N1, F2, N2)                                                              \
-    GS_FFN_KERNEL(F1, N1, F2, N2, 2, 2) GS_FFN_KERNEL(F1, N1, F2, N2, 2, 4)                     \
-    GS_FFN_KERNEL(F1, N1, F2, N2, 2, 6) GS_FFN_KERNEL(F1, N1, F2, N2, 2, 8)                     \
-    GS_FFN_KERNEL(F1, N1, F2, N2, 4, 2) GS_FFN_KERNEL(F1, N1, F2, N2, 4, 4)                     \
-    GS_FFN_KERNEL(F1, N1, F2, N2, 4, 6) GS_FFN_KERNEL(F1, N1, F2, N2, 4, 8)                     \
-    GS_FFN_KERNEL(F1, N1, F2, N2, 8, 2) GS_FFN_KERNEL(F1, N1, F2, N2, 8, 4)                     \
-    GS_FFN_KERNEL(F1, N1, F2, N2, 8, 6) GS_FFN_KERNEL(F1, N1, F2, N2, 8, 8)
-
 // One code object per format keeps the build parallel: the Makefile compiles this file once
 // per GS_STREAM_TYPE (F-struct, type id) and once with GS_COMMON for the kernels below.
 #if defined(GS_STREAM_F)
 GS_STREAM_ALL(GS_STREAM_F, GS_STREAM_ID)
-// fused FFN for the formats with a fast decode; gate/up and down in the same format, plus the
-// IQ2_XXS gate/up with IQ3_XXS down experts of the target model
-#if GS_STREAM_ID == 8 || GS_STREAM_ID == 12 || GS_STREAM_ID == 14 || GS_STREAM_ID == 16 || GS_STREAM_ID == 18
-GS_FFN_ALL(GS_STREAM_F, GS_STREAM_ID, GS_STREAM_F, GS_STREAM_ID)
-#endif
-#if GS_STREAM_ID == 16
-GS_FFN_ALL(FIQ2_XXS, 16, FIQ3_XXS, 18)
-#endif
 #endif
 
 #if defined(GS_COMMON)

@@ -81,8 +81,6 @@ SIGNATURES = {
     "gs_moe_down": [C.c_int, C.POINTER(MoeBatch), C.c_int, _I64, C.c_int, C.c_int, _P, _P, _P],
     "gs_moe_ffn": [C.c_int, C.c_int, C.POINTER(MoeBatch), C.c_int, _I64, C.c_int, C.c_int, _I64, _P, _P, _P, C.c_float,
                    _P],
-    "gs_moe_ffn_status": [C.POINTER(C.c_int)],
-    "gs_moe_ffn_set_wait_limit": [C.c_uint64],
     "gs_swiglu": [_P, _P, _P, _I64, C.c_float, _P],
     "gs_axpy": [_P, _P, C.c_float, _I64, _P],
     "gs_gemm": [C.c_int, _P, _I64, C.c_int, C.c_int, _P, _I64, _P, _I64, C.c_int, C.c_int, C.c_int, _I64, _I64, _I64,
@@ -275,22 +273,10 @@ class ops:
 
     @staticmethod
     def moe_ffn(ty_gu, ty_dn, batch, nt, rs_gu, n_embd, n_ff, rs_dn, x, h, y, lim=0.0, s=None):
-        """gs_moe_ffn: moe_gateup then moe_down (one fused launch for one token)."""
+        """gs_moe_ffn: moe_gateup then moe_down."""
         check(lib().gs_moe_ffn(ty_gu, ty_dn, C.byref(batch), nt, rs_gu, n_embd, n_ff, rs_dn, _p(x), _p(h), _p(y), lim,
                                _raw(s)))
 
-    @staticmethod
-    def moe_ffn_status():
-        """gs_moe_ffn_status: True if a fused launch's barrier wait expired since the last call
-        (waits for the device; clears the flag)."""
-        e = C.c_int()
-        check(lib().gs_moe_ffn_status(C.byref(e)))
-        return bool(e.value)
-
-    @staticmethod
-    def moe_ffn_set_wait_limit(ticks):
-        """gs_moe_ffn_set_wait_limit: barrier wait bound in 100 MHz ticks (0: the 0.2 s default)."""
-        check(lib().gs_moe_ffn_set_wait_limit(int(ticks)))
 
     @staticmethod
     def gemm(ty, w, row_stride, k, rows, x, x_stride, y, y_stride, n, accumulate=False, n_batch=1, w_bs=0, x_bs=0,

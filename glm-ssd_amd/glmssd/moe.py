@@ -105,7 +105,7 @@ class MoeLayer:
     """One MoE FFN layer with every expert resident: the work of forward.rs:982-1136
     (`Engine::moe`) without the expert cache. forward(): router logits (F32 GEMV), host routing,
     shared expert SwiGLU FFN into `out`, routed experts into an accumulator (up to 4 tokens: one
-    fused gs_moe_ffn per token over its own experts, where the engine's decode branch batches up
+    gs_moe_ffn per token over its own experts, where the engine's decode branch batches up
     to 16 experts for 1-2 tokens; more tokens: the grouped MFMA kernel when
     every expert matrix is IQ2_XXS or IQ3_XXS, else per-expert gather / GEMM / SwiGLU / scatter-add as
     run_expert_rows), then out += accumulator.
@@ -178,7 +178,7 @@ class MoeLayer:
                 groups[e].append((ti, w))
         used = [e for e in range(ne) if groups[e]]
         if t <= self.PER_TOKEN_MAX:
-            # decode and MTP sizes: one fused one-token FFN per token over its own experts (on the
+            # decode and MTP sizes: one one-token FFN (gs_moe_ffn) per token over its own experts (on the
             # config-2 experts: 2 tokens 36 us against 52 us as one 2-token batch over the union of
             # their experts, 4 tokens 71 us against 116 us through the grouped GEMM)
             h = self._buf("h", self.MOE_MAX * self.n_ff * 4)

@@ -112,23 +112,10 @@ int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, 
 
 /* Additive (no counterpart in the reference): the whole routed-expert FFN of one layer, exactly
  * gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, lim) followed by
- * gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y); replaces the pair the decode path calls
- * per expert batch (crates/engine/src/forward.rs:1067-1107). For one token it is one launch
- * (gate/up, grid-wide barrier, down) when the format pair has a fused kernel (IQ2_XXS, IQ3_XXS,
- * Q4_K, Q6_K, Q8_0 each with itself; IQ2_XXS gate/up with IQ3_XXS down), else the two launches.
- * Fused launches must not overlap in time on one device (they share the barrier counters). */
+ * gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y) (two launches on s); replaces the pair the
+ * decode path calls per expert batch (crates/engine/src/forward.rs:1067-1107). */
 int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int64_t rs_gu, int n_embd, int n_ff, int64_t rs_dn,
                const float *x, float *h, float *y, float lim, void *s);
-
-/* Additive (no counterpart in the reference): health of the fused launches of gs_moe_ffn. Their
- * grid-wide barrier waits at most a bounded time (0.2 s by default); if a wait expires (a
- * workgroup never arrived: the grid was not co-resident, or the device was preempted) the kernel
- * still completes, sets a flag and its results are undefined. gs_moe_ffn_status waits for the
- * device to finish, then reports in *expired whether any fused launch on the current device
- * expired since the previous call, and clears the flag. gs_moe_ffn_set_wait_limit sets the bound
- * (ticks of the 100 MHz clock) for later launches from any thread; 0 restores the default. */
-int gs_moe_ffn_status(int *expired);
-int gs_moe_ffn_set_wait_limit(uint64_t ticks);
 
 /* ---- GEMM and MoE glue (crates/cuda/src/lib.rs:71-74,115-122; kernels/gemm.cu, ops.cu) ---- */
 /* SwiGLU with clamp: y = silu(min(g,L)) * clamp(u,-L,L); L <= 0: no clamp (lib.rs:76; ops.cu:101-115) */
