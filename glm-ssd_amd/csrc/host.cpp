@@ -199,19 +199,6 @@ hipError_t plan_stream(DeviceCtx *c, int kind, int ty, StreamArgs &a, StreamPlan
     return hipSuccess;
 }
 
-// workgroups of `f` that fit one CU with `lds` bytes of dynamic LDS (cached)
-int blocks_per_cu(DeviceCtx *c, const std::string &name, hipFunction_t f, size_t lds) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    auto key = std::make_pair(name, (int)lds);
-    auto it = c->occ.find(key);
-    if (it != c->occ.end()) return it->second;
-    int nb = 0;
-    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, GS_WG, lds) != hipSuccess || nb < 1) nb = 0;
-    (void)hipGetLastError();
-    c->occ[key] = nb;
-    return nb;
-}
-
 // Plan and launch one streaming kernel (kind 0 GEMV, 1 MoE gate/up, 2 MoE down).
 hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 1) {
     hipError_t e;
