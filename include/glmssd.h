@@ -164,6 +164,21 @@ int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_ex
                    const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K, int n_ff,
                    int64_t down_row_stride, const float *x, float *y, float lim, void *work, size_t work_bytes, void *s);
 
+/* No counterpart in the reference; for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): gs_moe_grouped with
+ * its workspace in a device array of the library (GS_MOE_GROUPED_SCRATCH_MAX bytes, one per GPU,
+ * held until the process ends) instead of a caller buffer. Allocates nothing: the first call on
+ * a device looks up that device's array (and, like any first gs_* call, loads the library's
+ * code objects), later calls only launch. Returns hipErrorInvalidValue when
+ * gs_moe_grouped_workspace(n_tok, n_pairs, K, n_ff) exceeds GS_MOE_GROUPED_SCRATCH_MAX (e.g.
+ * 512 tokens x top-8 at 4096 / 1536 needs about 42 MB). Every call on one GPU shares its array:
+ * calls that overlap in time on one GPU (other streams, other threads) race and must not be
+ * issued. */
+#define GS_MOE_GROUPED_SCRATCH_MAX (48u << 20)
+int gs_moe_grouped_noalloc(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs,
+                           const int *idx, const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K,
+                           int n_ff, int64_t down_row_stride, const float *x, float *y, float lim, void *s);
+
 #ifdef __cplusplus
 }
 #endif
