@@ -287,10 +287,11 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     arows_raw(cur, ar_cur);
     arows_raw(nxt, ar_nxt);
 
+    static_assert(NR * MATS <= 4, "one block-scale load per lane quarter");
     struct WRegs {   // one position's raw weight words: 16 bytes (units 2q, 2q+1) + f16 d per row
         uint4 q[NR][MATS];
         uint2 sg[NR][MATS];   // IQ3_XXS: the two units' sign/scale words
-        uint32_t d[NR][MATS];
+        uint32_t dq;          // f16 block scale of row sub-tile (n, mt) = (q / MATS, q % MATS), row j
     };
     auto load_w = [&](const Desc &d, const uint32_t (&wo)[NR], int b, WRegs &w) {
 #pragma unroll
@@ -300,8 +301,19 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 const uint8_t *p = d.wb[mt] + (wo[n] + BB * b);
                 w.q[n][mt] = ldg16(p);
                 if (IQ3) w.sg[n][mt] = ldg8(p + 64 - 8 * q);   // block + 66 + 8q
-                w.d[n][mt] = ldg2(p - 2 - 16 * q);
             }
+        // one 2-byte load per lane for all NR x MATS row sub-tiles' block scales (lane quarter q
+        // takes sub-tile q), instead of one load instruction per sub-tile
+        {
+            const int sq = q < NR * MATS ? q : 0, sn = sq / MATS, smt = sq % MATS;
+            const uint8_t *wbq = d.wb[0];
+#pragma unroll
+            for (int mt = 1; mt < MATS; mt++) wbq = smt == mt ? d.wb[mt] : wbq;
+            uint32_t won = wo[0];
+#pragma unroll
+            for (int n = 1; n < NR; n++) won = sn == n ? wo[n] : won;
+            w.dq = ldg2(wbq + (won + BB * b) - 2 - 16 * q);
+        }
     };
     auto load_a = [&](const int (&ar)[NLD], int b, u4 (&stg)[NLD]) {
 #pragma unroll
@@ -425,7 +437,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             for (int n = 0; n < NR; n++)
 #pragma unroll
                 for (int mt = 0; mt < MATS; mt++) {
-                    const float cd = h2f(wu.d[n][mt]) * XS;
+                    const float cd = h2f((uint32_t)__builtin_amdgcn_ds_bpermute((j + 16 * (n * MATS + mt)) << 2, (int)wu.dq)) * XS;
 #pragma unroll
                     for (int tt = 0; tt < NT; tt++)
                         if (tt == 0 || 16 * tt < n_here) acc[tt][n][mt] += cd * sb[tt][n][mt];
