@@ -113,15 +113,12 @@ def run_moe_decode(L, s, steps, warmup, n_expert=288, n_embd=4096, n_ff=1536, se
     rc = L.bn_moe_decode(ty, ty_dn, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p,
                          steps, warmup, s.raw(), C.byref(ms), C.byref(msg))
     G.check(rc)
-    msf = C.c_float()
-    G.check(L.bn_moe_ffn(ty, ty_dn, C.cast(batches, C.c_void_p), nb, 1, rbg, n_embd, n_ff, rbd, dx.p, dh.p, dy.p,
-                         steps, warmup, s.raw(), C.byref(msf)))
     step_bytes = 8 * (2 * mat + mat_dn)
     gu_bytes = 8 * 2 * mat
     keep = (gate, up, down, dx, dh, dy, batches)
     layer = dict(gate=gate, up=up, down=down, mat=mat, mat_dn=mat_dn, n_expert=n_expert, n_embd=n_embd, n_ff=n_ff,
                  rbg=rbg, rbd=rbd, ty_gu=int(ty), ty_dn=int(ty_dn))
-    return dict(ms_step=ms.value, ms_gateup=msg.value, ms_ffn=msf.value, step_bytes=step_bytes, gateup_bytes=gu_bytes,
+    return dict(ms_step=ms.value, ms_gateup=msg.value, step_bytes=step_bytes, gateup_bytes=gu_bytes,
                 flops=8 * 3 * 2 * n_ff * n_embd), keep, layer
 
 
@@ -276,6 +273,24 @@ def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 
             "weight_GBps": round(raw.nbytes / t / 1e9, 1), "tokens": N, "rotated_copies": n}
 
 
+GROUPED_KERNELS = ("gs_k_grouped_16_1_2_2_8", "gs_k_grouped_16_2_2_4_8")   # config 5's gate/up and down
+
+
+def config5_roofline(r):
+    """BASELINE's second metric: the 512-token grouped MoE step against the HBM and f16 MFMA peaks."""
+    if not r:
+        return None
+    tr = [traffic_bytes(k) for k in GROUPED_KERNELS]
+    return {"bound": "hbm", "achieved": r["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(r["GBps"] / HBM_PEAK_GBPS, 4),
+            "traffic": sum(tr) if all(t is not None for t in tr) else None,
+            "traffic_source": "profiles/stream_kernels_traffic.json (gate/up + down kernels, rocprofv3 FETCH_SIZE + "
+                              "WRITE_SIZE, calibrated on a 1 GiB device copy)",
+            "algorithmic_bytes_per_step": r["weight_bytes"], "us_per_step": r["us_per_step"],
+            "mfma": {"achieved": r["TFLOPs"], "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": r["frac_mfma_f16_peak"], "dtype": "f16 x f16 -> f32 (v_mfma_f32_16x16x32_f16)"}}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -372,7 +387,7 @@ def main():
                                            ty_dn=G.GgmlType.IQ3_XXS, label="target-model decode FFN")
         secondary["decode_ffn_iq2xxs_gateup_iq3xxs_down_nff2048"] = {
             "us_per_step": round(rr["ms_step"] * 1e3, 2), "GB/s": round(rr["step_bytes"] / rr["ms_step"] / 1e6, 1),
-            "us_fused_gs_moe_ffn": round(rr["ms_ffn"] * 1e3, 2), "weight_bytes": rr["step_bytes"],
+            "weight_bytes": rr["step_bytes"],
             "experts_resident": 96}
         log(f"target-model decode FFN: {secondary['decode_ffn_iq2xxs_gateup_iq3xxs_down_nff2048']}")
         # config 5's 512-token prefill on the target model's expert types and shapes
@@ -380,8 +395,6 @@ def main():
         secondary["prefill_512tok_grouped_iq2xxs_gateup_iq3xxs_down_nff2048"] = r
         log(f"target-model prefill: {r}")
         del keep2, layer2
-        secondary["config2_fused_gs_moe_ffn"] = {"us_per_step": round(res["ms_ffn"] * 1e3, 2),
-                                                 "GB/s": round(res["step_bytes"] / res["ms_ffn"] / 1e6, 1)}
         from glmssd import synth
         r1 = run_gemv(L, s, G.GgmlType.Q8_0, 4096, 4096, synth.q8_0_matrix, args.steps, args.warmup, 1)
         r3a = run_gemv(L, s, G.GgmlType.Q4_K, 12288, 4096, synth.q4_k_matrix, args.steps, args.warmup, 3)
@@ -400,7 +413,8 @@ def main():
             r = run_gemm(L, s, ty, rows, K, N, mk, max(20, args.steps // 5), max(5, args.warmup // 5), 9)
             secondary[name] = r
             log(f"{name}: {r}")
-        rc = run_read_ceiling(L, s, [17825792, 25952256, 38928384, 41287680, 1 << 30], args.steps, args.warmup)
+        rc = run_read_ceiling(L, s, [17825792, 25952256, 28311552, 38928384, 41287680, 1 << 30], args.steps,
+                              args.warmup)
         secondary["plain_read_ceiling"] = rc
         log(f"plain-read ceiling: {rc}")
         for name, r in [("config1_q8_0_gemv_4096x4096", r1), ("config3_q4_k_gemv_k4096_rows12288", r3a),
@@ -408,6 +422,9 @@ def main():
             secondary[name] = {"GB/s": round(r["gbps"], 1), "us_per_call": round(r["ms"] * 1e3, 2),
                                "frac_hbm_peak": round(r["gbps"] / HBM_PEAK_GBPS, 4), "weight_bytes": r["bytes"],
                                "rotated_copies": r["copies"]}
+            # against a plain read of the same byte count (launch, ramp-up and drain included in both)
+            near = min(rc.values(), key=lambda v: abs(v["bytes"] - r["bytes"]))
+            secondary[name]["frac_of_plain_read_at_same_bytes"] = round(r["gbps"] / near["GB/s"], 3)
             log(f"{name}: {r['ms'] * 1e3:.2f} us, {r['gbps']:.1f} GB/s")
     if args.calib:
         src, dst = G.DeviceBuffer(1 << 30), G.DeviceBuffer(1 << 30)
@@ -433,6 +450,8 @@ def main():
         "config": {"workload": "config 2: routed-expert FFN, 1 decode token, 8 of 288 resident IQ2_XXS experts "
                                "(hidden 4096, intermediate 1536), gate/up+SwiGLU then down+weighted combine",
                    "weight_bytes_per_step": res["step_bytes"], "frac_hbm_peak": round(value / HBM_PEAK_GBPS, 4),
+                   "frac_of_plain_read_at_same_bytes": (round(value / secondary["plain_read_ceiling"]["38928384"]["GB/s"], 3)
+                                                        if "plain_read_ceiling" in secondary else None),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "gs_moe_gateup (gs_k_stream_16_1_1_4_w)",
                      "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -442,6 +461,7 @@ def main():
                      "algorithmic_bytes_per_launch": res["gateup_bytes"],
                      "avg_launch_us": round(res["ms_gateup"] * 1e3, 3)},
         "cpu_baseline": cpu,
+        "roofline_config5": config5_roofline(secondary.get("config5_prefill_512tok_grouped")),
         "secondary": secondary,
     }
     print(json.dumps(out), flush=True)
