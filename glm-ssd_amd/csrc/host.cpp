@@ -661,10 +661,11 @@ GS_EXPORT int gs_moe_grouped_workspace(int n_tok, int n_pairs, int K, int n_ff, 
     return 0;
 }
 
-GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs,
-                             const int *idx, const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K,
-                             int n_ff, int64_t down_row_stride, const float *x, float *y, float lim, void *work,
-                             size_t work_bytes, void *s) {
+namespace {
+// Both grouped entry points: pair p reads x[idx[p]] and adds into y[out_idx[p]].
+int grouped_ffn(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs, const int *idx,
+                const int *out_idx, const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K, int n_ff,
+                int64_t down_row_stride, const float *x, float *y, float lim, void *work, size_t work_bytes, void *s) {
     auto grp_type = [](int t) { return t == GS_IQ2_XXS || t == GS_IQ3_XXS; };
     if (!grp_type(ty_gu) || !grp_type(ty_down)) return hipErrorInvalidValue;
     if (n_exp < 1 || n_exp > GS_GRP_EXP_MAX || n_pairs < 0 || n_tok < 1) return hipErrorInvalidValue;
@@ -675,7 +676,7 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
     if (gu_row_stride < (int64_t)K / 256 * sb_bytes(ty_gu) || down_row_stride < (int64_t)n_ff / 256 * sb_bytes(ty_down))
         return hipErrorInvalidValue;
     if (n_pairs == 0) return 0;
-    if (!idx || !w || !aligned16(x) || ((uintptr_t)work & 255)) return hipErrorInvalidValue;
+    if (!idx || !out_idx || !w || !aligned16(x) || ((uintptr_t)work & 255)) return hipErrorInvalidValue;
     const GroupedWork L = grouped_layout(n_tok, n_pairs, K, n_ff);
     if (!work || work_bytes < L.total) return hipErrorInvalidValue;
     uint8_t *wb = (uint8_t *)work;
@@ -703,10 +704,28 @@ GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts
     a.act = h16;
     a.ascale = hs;
     a.out = y;
+    a.idx = out_idx;   // the down pass reads h per pair; idx only addresses its output rows
     a.row_stride = down_row_stride;
     a.K = n_ff;
     a.rows = K;
     return grouped_launch(2, ty_down, a, n_pairs, st);
+}
+}  // namespace
+
+GS_EXPORT int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs,
+                             const int *idx, const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K,
+                             int n_ff, int64_t down_row_stride, const float *x, float *y, float lim, void *work,
+                             size_t work_bytes, void *s) {
+    return grouped_ffn(ty_gu, ty_down, experts, n_exp, offs, idx, idx, w, n_pairs, n_tok, gu_row_stride, K, n_ff,
+                       down_row_stride, x, y, lim, work, work_bytes, s);
+}
+
+GS_EXPORT int gs_moe_grouped_scatter(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs,
+                                     const int *idx, const int *out_idx, const float *w, int n_pairs, int n_tok,
+                                     int64_t gu_row_stride, int K, int n_ff, int64_t down_row_stride, const float *x,
+                                     float *y, float lim, void *work, size_t work_bytes, void *s) {
+    return grouped_ffn(ty_gu, ty_down, experts, n_exp, offs, idx, out_idx, w, n_pairs, n_tok, gu_row_stride, K, n_ff,
+                       down_row_stride, x, y, lim, work, work_bytes, s);
 }
 
 

@@ -92,6 +92,8 @@ SIGNATURES = {
     "gs_moe_grouped_workspace": [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_size_t)],
     "gs_moe_grouped": [C.c_int, C.c_int, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int, _I64, C.c_int, C.c_int, _I64,
                        _P, _P, C.c_float, _P, C.c_size_t, _P],
+    "gs_moe_grouped_scatter": [C.c_int, C.c_int, _P, C.c_int, _P, _P, _P, _P, C.c_int, C.c_int, _I64, C.c_int,
+                               C.c_int, _I64, _P, _P, C.c_float, _P, C.c_size_t, _P],
     "gs_moe_grouped_noalloc": [C.c_int, C.c_int, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int, _I64, C.c_int, C.c_int,
                                _I64, _P, _P, C.c_float, _P],
 }
@@ -298,6 +300,14 @@ class ops:
         check(lib().gs_moe_grouped(ty_gu, ty_down, _p(experts), n_exp, _p(offs), _p(idx), _p(w), n_pairs, n_tok,
                                    gu_row_stride, k, n_ff, down_row_stride, _p(x), _p(y), lim, _p(work), work_bytes,
                                    _raw(s)))
+
+    @staticmethod
+    def moe_grouped_scatter(ty_gu, ty_down, experts, n_exp, offs, idx, out_idx, w, n_pairs, n_tok, gu_row_stride,
+                            k, n_ff, down_row_stride, x, y, lim, work, work_bytes, s=None):
+        """gs_moe_grouped_scatter: pair p adds into y[out_idx[p]] (the deterministic slot combine)."""
+        check(lib().gs_moe_grouped_scatter(ty_gu, ty_down, _p(experts), n_exp, _p(offs), _p(idx), _p(out_idx),
+                                           _p(w), n_pairs, n_tok, gu_row_stride, k, n_ff, down_row_stride, _p(x),
+                                           _p(y), lim, _p(work), work_bytes, _raw(s)))
 
     @staticmethod
     def moe_grouped_noalloc(ty_gu, ty_down, experts, n_exp, offs, idx, w, n_pairs, n_tok, gu_row_stride, k, n_ff,

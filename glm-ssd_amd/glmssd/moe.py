@@ -2,6 +2,7 @@
 multi-token MoE pass (crates/engine/src/forward.rs:1017-1036, :1335-1349), in the CSR form that
 gs_moe_grouped takes, and a resident-layer helper that owns the device arrays."""
 import ctypes as C
+import os
 
 import numpy as np
 
@@ -38,6 +39,19 @@ def group_pairs(routes, n_exp):
     return (offs, np.asarray(idx, dtype=np.int32), np.asarray(w, dtype=np.float32), np.asarray(pe, dtype=np.int32))
 
 
+def slot_index(routes, idx, pair_exp):
+    """Deterministic-combine slot of each pair (forward.rs:1039-1048): (rank of the pair's expert in
+    its token's route) * n_tok + token. Every (rank, token) slot is hit by exactly one pair."""
+    t = len(routes)
+    rank = [{int(e): k for k, (e, _) in enumerate(r)} for r in routes]
+    return np.asarray([rank[ti][int(e)] * t + ti for ti, e in zip(idx.tolist(), pair_exp.tolist())], dtype=np.int32)
+
+
+def deterministic_default():
+    """GLMSSD_DETERMINISTIC=1 selects the ordered combine, as the engine reads it (forward.rs:551)."""
+    return os.environ.get("GLMSSD_DETERMINISTIC") == "1"
+
+
 class ResidentMoeLayer:
     """Every routed expert of one MoE layer resident in device memory, plus the GsExpertPtrs
     table gs_moe_grouped reads."""
@@ -55,21 +69,41 @@ class ResidentMoeLayer:
         self.table = DeviceBuffer.from_array(np.frombuffer(bytes(tab), dtype=np.uint8))
         self.work = None
 
-    def upload_routes(self, routes, s=None):
+    def upload_routes(self, routes, s=None, slots=False):
+        """Pairs of `routes` to the device; with `slots`, also each pair's deterministic-combine slot."""
         offs, idx, w, pe = group_pairs(routes, self.n_exp)
         self.n_pairs = int(idx.size)
         self.d_offs = DeviceBuffer.from_array(offs, s)
         self.d_idx = DeviceBuffer.from_array(idx if idx.size else np.zeros(1, np.int32), s)
         self.d_w = DeviceBuffer.from_array(w if w.size else np.zeros(1, np.float32), s)
+        self.d_slot = None
+        if slots:
+            sl = slot_index(routes, idx, pe)
+            self.d_slot = DeviceBuffer.from_array(sl if sl.size else np.zeros(1, np.int32), s)
         return offs, idx, w, pe
 
-    def forward(self, x_dev, y_dev, n_tok, lim=0.0, s=None):
+    def _work(self, n_tok):
         need = ops.moe_grouped_workspace(n_tok, self.n_pairs, self.n_embd, self.n_ff)
         if self.work is None or self.work.nbytes < need:
             self.work = DeviceBuffer(need)
+        return self.work
+
+    def forward(self, x_dev, y_dev, n_tok, lim=0.0, s=None):
+        """y[token] += every routed expert's weighted FFN output (f32 atomics: run-to-run order varies)"""
+        wk = self._work(n_tok)
         ops.moe_grouped(self.ty_gu, self.ty_down, self.table, self.n_exp, self.d_offs, self.d_idx, self.d_w,
                         self.n_pairs, n_tok, self.rs_gu, self.n_embd, self.n_ff, self.rs_down, x_dev, y_dev, lim,
-                        self.work, self.work.nbytes, s)
+                        wk, wk.nbytes, s)
+
+    def forward_slots(self, x_dev, slots_dev, n_tok, lim=0.0, s=None):
+        """slots[rank * n_tok + token] += the pair's weighted FFN output (needs upload_routes(slots=True);
+        `slots` zeroed, [k * n_tok][n_embd]): one addition per element, so the result is reproducible."""
+        if self.d_slot is None:
+            raise ValueError("upload_routes(..., slots=True) first")
+        wk = self._work(n_tok)
+        ops.moe_grouped_scatter(self.ty_gu, self.ty_down, self.table, self.n_exp, self.d_offs, self.d_idx,
+                                self.d_slot, self.d_w, self.n_pairs, n_tok, self.rs_gu, self.n_embd, self.n_ff,
+                                self.rs_down, x_dev, slots_dev, lim, wk, wk.nbytes, s)
 
 
 def route(logits, bias, k, weights_norm=True, weights_scale=1.0):
@@ -111,14 +145,20 @@ class MoeLayer:
     run_expert_rows), then out += accumulator.
 
     experts: list of (gate, up, down) host byte arrays; gate/up [n_ff rows x n_embd], down
-    [n_embd rows x n_ff]."""
+    [n_embd rows x n_ff].
+
+    deterministic (default: GLMSSD_DETERMINISTIC=1 in the environment, forward.rs:551): the
+    engine's ordered combine. One-token FFNs take each token's experts in id order (forward.rs:
+    1071-1081); multi-token paths write every (route rank, token) pair into its own slot and sum
+    the slots in rank order (forward.rs:1119-1127), so the output is bit-reproducible."""
     MOE_MAX, PER_TOKEN_MAX = 16, 4
 
     def __init__(self, router, bias, shared, experts, n_embd, n_ff, ty_gu, ty_down, k=8, weights_norm=True,
                  weights_scale=1.0, clamp_exp=0.0, clamp_shexp=0.0, router_ty=T.F32, shared_ty=(T.Q6_K,) * 3,
-                 n_ff_shexp=None, s=None):
+                 n_ff_shexp=None, s=None, deterministic=None):
         from . import MoeBatch   # noqa: F401  (layout shared with the C ABI)
         self.n_embd, self.n_ff, self.k = n_embd, n_ff, k
+        self.deterministic = deterministic_default() if deterministic is None else bool(deterministic)
         self.n_exp = len(experts)
         self.bias = np.asarray(bias, dtype=np.float32)
         self.norm, self.scale, self.lim, self.lim_sh = weights_norm, weights_scale, clamp_exp, clamp_shexp
@@ -183,6 +223,8 @@ class MoeLayer:
             # their experts, 4 tokens 71 us against 116 us through the grouped GEMM)
             h = self._buf("h", self.MOE_MAX * self.n_ff * 4)
             for ti, r in enumerate(routes):
+                if self.deterministic:
+                    r = sorted(r, key=lambda ew: ew[0])
                 for b0 in range(0, len(r), self.MOE_MAX):
                     chunk = r[b0:b0 + self.MOE_MAX]
                     b = MoeBatch()
@@ -194,12 +236,23 @@ class MoeLayer:
                     ops.moe_ffn(self.ty_gu, self.ty_down, b, 1, self.gate[0].row_bytes, n, self.n_ff,
                                 self.down[0].row_bytes, _at(xn, ti * n * 4), h, acc.ptr(ti * n * 4), self.lim, s)
         elif self.grouped is not None:
-            self.grouped.upload_routes(routes, s)
-            self.grouped.forward(xn, acc, t, self.lim, s)
+            self.grouped.upload_routes(routes, s, slots=self.deterministic)
+            if self.deterministic:
+                slots = self._buf("slots", self.k * t * n * 4)
+                slots.zero(s)
+                self.grouped.forward_slots(xn, slots, t, self.lim, s)
+                self._sum_slots(acc, slots, t, s)
+            else:
+                self.grouped.forward(xn, acc, t, self.lim, s)
         else:
             # run_expert_rows (forward.rs:1399-1413) per used expert
-            offs, idx, w, _ = group_pairs(routes, ne)
+            offs, idx, w, pe = group_pairs(routes, ne)
             d_idx, d_w = DeviceBuffer.from_array(idx, s), DeviceBuffer.from_array(w, s)
+            to, slots = d_idx, None
+            if self.deterministic:
+                to = DeviceBuffer.from_array(slot_index(routes, idx, pe), s)
+                slots = self._buf("slots", self.k * t * n * 4)
+                slots.zero(s)
             m_max = max(len(groups[e]) for e in used)
             xg = self._buf("xg", m_max * n * 4)
             eg, eu = self._buf("eg", m_max * self.n_ff * 4), self._buf("eu", m_max * self.n_ff * 4)
@@ -211,6 +264,14 @@ class MoeLayer:
                 self._mm(self.up[e], xg, eu, m, s)
                 ops.swiglu(eg, eu, eg, m * self.n_ff, self.lim, s)
                 self._mm(self.down[e], eg, ey, m, s)
-                ops.scatter_add_rows(acc, d_idx.ptr(4 * o), d_w.ptr(4 * o), ey, m, n, s)
+                ops.scatter_add_rows(acc if slots is None else slots, to.ptr(4 * o), d_w.ptr(4 * o), ey, m, n, s)
+            if slots is not None:
+                self._sum_slots(acc, slots, t, s)
         ops.axpy(out, acc, 1.0, t * n, s)
         return routes
+
+    def _sum_slots(self, acc, slots, t, s):
+        """acc += slots[rank] for rank 0..k-1 in order (forward.rs:1122-1127)"""
+        n = self.n_embd
+        for r in range(self.k):
+            ops.axpy(acc, slots.ptr(4 * r * t * n), 1.0, t * n, s)

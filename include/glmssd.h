@@ -150,7 +150,8 @@ int gs_quant_q8_1(const float *x, void *q, int64_t n, void *s);
  * x and h enter the contractions as f16 (after a power-of-two row scale that keeps each row in
  * the f16 normal range), accumulation is f32; the weights are exact (the reference rounds the
  * dequantized weights to f16). The experts' outputs are combined into y with f32 atomics, so the
- * summation order (and the last bits of y) can differ between runs.
+ * summation order (and the last bits of y) can differ between runs (gs_moe_grouped_scatter below
+ * gives the reference's bit-reproducible mode).
  * Supported: ty_gu, ty_down each IQ2_XXS or IQ3_XXS, K and n_ff multiples of 256 and >= 512,
  * n_exp <= 1024, x 16-byte aligned. `work` (256-byte aligned, >= gs_moe_grouped_workspace bytes) is caller-owned scratch.
  * All of offs/idx/w/experts are device arrays; the call launches without a host sync. */
@@ -163,6 +164,18 @@ int gs_moe_grouped_workspace(int n_tok, int n_pairs, int K, int n_ff, size_t *by
 int gs_moe_grouped(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs, const int *idx,
                    const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K, int n_ff,
                    int64_t down_row_stride, const float *x, float *y, float lim, void *work, size_t work_bytes, void *s);
+
+/* gs_moe_grouped with the output row of each pair given separately: pair p reads x[idx[p]] and
+ * adds w[p] * FFN_e(x[idx[p]]) into y[out_idx[p]][:]. The reference's deterministic combine
+ * (GLMSSD_DETERMINISTIC, crates/engine/src/forward.rs:276-278, :1039-1048, :1119-1127) scatters
+ * every (route rank r, token t) pair into its own slot r * n_tok + t and sums the slots in rank
+ * order with gs_axpy; with distinct out_idx into a zeroed y each element receives exactly one
+ * addition, so the result is bit-reproducible. Arguments and limits otherwise as gs_moe_grouped
+ * (out_idx a device array of n_pairs entries; y holds as many rows as out_idx addresses). */
+int gs_moe_grouped_scatter(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs,
+                           const int *idx, const int *out_idx, const float *w, int n_pairs, int n_tok,
+                           int64_t gu_row_stride, int K, int n_ff, int64_t down_row_stride, const float *x, float *y,
+                           float lim, void *work, size_t work_bytes, void *s);
 
 /* No counterpart in the reference; for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): gs_moe_grouped with

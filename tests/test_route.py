@@ -48,3 +48,19 @@ def test_ties_keep_id_order():
     r = route(np.zeros((1, 5), np.float32), np.zeros(5, np.float32), 3)[0]
     assert [e for e, _ in r] == [0, 1, 2]
     np.testing.assert_allclose([w for _, w in r], [1 / 3] * 3, rtol=1e-6)
+
+
+def test_slot_index_is_rank_times_tokens_plus_token():
+    """forward.rs:1039-1048: slot = (rank of the expert in the token's route) * t + token; the
+    slots of all pairs are exactly 0 .. k*t-1 (each (rank, token) once)."""
+    from glmssd.moe import group_pairs, slot_index
+    rng = np.random.default_rng(5)
+    t, ne, k = 7, 12, 4
+    routes = [[(int(e), float(rng.random())) for e in rng.permutation(ne)[:k]] for _ in range(t)]
+    offs, idx, w, pe = group_pairs(routes, ne)
+    sl = slot_index(routes, idx, pe)
+    assert sorted(sl.tolist()) == list(range(k * t))
+    for p in range(idx.size):
+        ti, e = int(idx[p]), int(pe[p])
+        assert routes[ti][sl[p] // t][0] == e and sl[p] % t == ti
+        assert routes[ti][sl[p] // t][1] == w[p]
