@@ -39,9 +39,11 @@ typedef float gf4 __attribute__((ext_vector_type(4)));
 #define GM_TN 64    // tokens per workgroup (4 x 16)
 
 // 8 floats -> 8 halves (round to nearest even, as __floats2half2_rn)
+// (a vector conversion: v_cvt_pk_f16_f32, two values per instruction, round to nearest even)
+typedef float gf8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ gh8 to_h8(const float *v) {
-    return __builtin_bit_cast(gh8, make_uint4(f2h(v[0]) | (f2h(v[1]) << 16), f2h(v[2]) | (f2h(v[3]) << 16),
-                                              f2h(v[4]) | (f2h(v[5]) << 16), f2h(v[6]) | (f2h(v[7]) << 16)));
+    const gf8 f = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+    return __builtin_convertvector(f, gh8);
 }
 
 template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
@@ -49,9 +51,13 @@ struct GemmFmt {
     static constexpr bool PLAIN = QKB == 1;
     // bytes of one 256-element super-block of a row, and its LDS slot (16-byte multiple)
     static constexpr int SB = QKB == 1 ? 256 * BB : 256 / QKB * BB;
-    // LDS slot: the super-block is copied from the 4-byte boundary at or below its start (buffer
-    // loads at 2-byte alignment are avoided), so a slot holds up to 3 leading bytes more
-    static constexpr int SBP = (SB + 3 + 15) & ~15;
+    // LDS slot: the super-block realigned to the slot start (the copy reads from the 4-byte
+    // boundary at or below the block and shifts the bytes into place), so every decoder sees a
+    // 4-byte aligned block and its byte reads merge into dword reads. An odd number of dwords:
+    // the 16 rows a wave decodes side by side then start in 16 different banks (a multiple of 16
+    // bytes put rows 4 apart in one bank, and the lane quarters' units 32 bytes apart on top of
+    // them: 16-way conflicts on every read)
+    static constexpr int SBP = 4 * (((SB + 3) / 4) | 1);
     // exact decode of 32-element unit u (0..7) of a super-block starting at p
     __device__ static __forceinline__ void unit(const uint8_t *p, int u, float (&v)[32]) {
         if (QKB == 256) DEC(p, u, v);
@@ -63,7 +69,7 @@ struct GemmFmt {
 template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
 __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     using F = GemmFmt<QKB, BB, DEC>;
-    constexpr int CPR = F::PLAIN ? 1 : F::SBP / 16;                 // raw 16-byte chunks per row
+    constexpr int CPR = F::PLAIN ? 1 : (F::SBP + 15) / 16;          // raw 16-byte chunks per row
     constexpr int NRAW = F::PLAIN ? 1 : (GM_RB * CPR + GM_NTH - 1) / GM_NTH;
     constexpr int RAWB = F::PLAIN ? 16 : GM_RB * F::SBP;            // one raw buffer
     constexpr int ASLAB = GM_TN * 512;                              // one f16 activation buffer
@@ -99,51 +105,66 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     const BufferAt wt(tile - d0, 0,
                       F::PLAIN ? 0u : (uint32_t)((d0 + (int64_t)(nrows - 1) * rs + row_bytes + 3) & ~(int64_t)3));
     uint32_t roff[NRAW];
-    int rdst[NRAW];
+    int rdst[NRAW], rcap[NRAW];
 #pragma unroll
     for (int i = 0; i < NRAW; i++) {
         const int zc = tid + GM_NTH * i, rr = min(zc / CPR, nrows - 1), c = zc % CPR;
         roff[i] = d0 + (uint32_t)((int64_t)rr * rs) + 16u * c;
         rdst[i] = zc < GM_RB * CPR ? (zc / CPR) * F::SBP + 16 * c : -1;
+        rcap[i] = F::SBP - 16 * c;   // bytes of the slot from this chunk on
     }
-    auto raw_load = [&](int b, uint4 (&rv)[NRAW]) {
+    // chunk i of super-block b: 20 bytes from the dword boundary at or below its first byte
+    auto raw_load = [&](int b, uint4 (&rv)[NRAW], uint32_t (&rx)[NRAW]) {
         if constexpr (!F::PLAIN) {
 #pragma unroll
-            for (int i = 0; i < NRAW; i++) rv[i] = wt.u128((roff[i] + (uint32_t)(F::SB * b)) & ~3u);
+            for (int i = 0; i < NRAW; i++) {
+                const uint32_t o = (roff[i] + (uint32_t)(F::SB * b)) & ~3u;
+                rv[i] = wt.u128(o);
+                rx[i] = wt.u32(o + 16);
+            }
         }
     };
-    auto raw_store = [&](int buf, const uint4 (&rv)[NRAW]) {
+    // the chunk shifted by the block's misalignment (v_alignbyte), as dword stores (slots are
+    // 4-byte aligned), none past the slot
+    auto raw_store = [&](int buf, int b, const uint4 (&rv)[NRAW], const uint32_t (&rx)[NRAW]) {
         if constexpr (!F::PLAIN) {
 #pragma unroll
             for (int i = 0; i < NRAW; i++)
-                if (rdst[i] >= 0) *(uint4 *)(rawbuf + buf * RAWB + rdst[i]) = rv[i];
+                if (rdst[i] >= 0) {
+                    const uint32_t lead = (roff[i] + (uint32_t)(F::SB * b)) & 3u;
+                    uint32_t *d = (uint32_t *)(rawbuf + buf * RAWB + rdst[i]);
+                    const int room = rcap[i];
+                    d[0] = __builtin_amdgcn_alignbyte(rv[i].y, rv[i].x, lead);
+                    if (room > 4) d[1] = __builtin_amdgcn_alignbyte(rv[i].z, rv[i].y, lead);
+                    if (room > 8) d[2] = __builtin_amdgcn_alignbyte(rv[i].w, rv[i].z, lead);
+                    if (room > 12) d[3] = __builtin_amdgcn_alignbyte(rx[i], rv[i].w, lead);
+                }
         }
     };
     // activations: A chunk y = tid + GM_NTH*i -> token row y >> 5, 8-element chunk y & 31
+    // unconditional loads (a clamped address past the tokens or the row; zeroed at the store), so
+    // the compiler's waits for them stay exact counts instead of draining at a branch
     auto x_load = [&](int b, float4 (&xv)[NXA][2]) {
 #pragma unroll
         for (int i = 0; i < NXA; i++) {
             const int y = tid + GM_NTH * i, t = y >> 5, c = y & 31;
-            const int kk = 256 * b + 8 * c;
-            if (t < ntok && kk < K) {
-                const float4 *p = (const float4 *)(X + (int64_t)(n0 + t) * a.x_stride + kk);
-                xv[i][0] = p[0];
-                xv[i][1] = p[1];
-            } else {
-                xv[i][0] = xv[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            const int kk = min(256 * b + 8 * c, K - 8);
+            const float4 *p = (const float4 *)(X + (int64_t)(n0 + min(t, ntok - 1)) * a.x_stride + kk);
+            xv[i][0] = p[0];
+            xv[i][1] = p[1];
         }
     };
-    auto x_store = [&](int buf, const float4 (&xv)[NXA][2]) {
+    auto x_store = [&](int buf, int b, const float4 (&xv)[NXA][2]) {
 #pragma unroll
         for (int i = 0; i < NXA; i++) {
             const int y = tid + GM_NTH * i, t = y >> 5, c = y & 31;
-            const float f[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
-                                xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+            const bool ok = t < ntok && 256 * b + 8 * c < K;
+            const float f[8] = {ok ? xv[i][0].x : 0.f, ok ? xv[i][0].y : 0.f, ok ? xv[i][0].z : 0.f,
+                                ok ? xv[i][0].w : 0.f, ok ? xv[i][1].x : 0.f, ok ? xv[i][1].y : 0.f,
+                                ok ? xv[i][1].z : 0.f, ok ? xv[i][1].w : 0.f};
             *(gh8 *)(abuf + buf * ASLAB + t * 512 + ((c ^ (t & 15)) << 4)) = to_h8(f);
         }
     };
-
     gf4 acc[4][2];
 #pragma unroll
     for (int tt = 0; tt < 4; tt++)
@@ -152,11 +173,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
 
     {   // prologue: super-block 0
         uint4 rv[NRAW];
+        uint32_t rx[NRAW];
         float4 xv[NXA][2];
-        raw_load(0, rv);
+        raw_load(0, rv, rx);
         x_load(0, xv);
-        raw_store(0, rv);
-        x_store(0, xv);
+        raw_store(0, 0, rv, rx);
+        x_store(0, 0, xv);
     }
     __syncthreads();
 
@@ -167,8 +189,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         // next super-block in flight while this one is decoded and contracted (issued on the last
         // step too, re-reading that step's data, so every wait on them is an exact count)
         uint4 rv[NRAW];
+        uint32_t rx[NRAW];
         float4 xv[NXA][2];
-        raw_load(more ? b + 1 : b, rv);
+        raw_load(more ? b + 1 : b, rv, rx);
         x_load(more ? b + 1 : b, xv);
         // B fragments: units 2q, 2q+1 of this lane's two rows, rounded to f16
         gh8 bf[2][2][4];
@@ -184,8 +207,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
                 } else if constexpr (F::PLAIN) {
                     F::unit(W + (int64_t)(r0 + rr) * rs + (int64_t)256 * b * BB, 2 * q + hu, v);
                 } else {
-                    const uint32_t lead = (uint32_t)(d0 + (int64_t)rr * rs + (int64_t)F::SB * b) & 3u;
-                    F::unit(rawbuf + buf * RAWB + rr * F::SBP + lead, 2 * q + hu, v);
+                    F::unit((const uint8_t *)__builtin_assume_aligned(rawbuf + buf * RAWB + rr * F::SBP, 4), 2 * q + hu, v);
                 }
 #pragma unroll
                 for (int g = 0; g < 4; g++) bf[n][hu][g] = to_h8(v + 8 * g);
@@ -207,8 +229,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
             }
         }
         if (more) {
-            raw_store(buf ^ 1, rv);
-            x_store(buf ^ 1, xv);
+            raw_store(buf ^ 1, b + 1, rv, rx);
+            x_store(buf ^ 1, b + 1, xv);
         }
         __syncthreads();
     }

@@ -505,10 +505,10 @@ GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows
     if (!check_w(W, row_stride) || (n_batch > 1 && (w_bs & 1))) return hipErrorInvalidValue;
     if (rows == 0) return 0;
     // bytes of one 256-element super-block of a row and its LDS slot (gemm.hip GemmFmt::SB, SBP:
-    // up to 3 leading bytes more, rounded to 16)
+    // rounded up to an odd number of dwords)
     const int eb = ggml_block_elems(ty);
     const int sb = eb == 1 ? 256 * (bb / qk) : 256 / eb * bb;
-    const int sbp = (sb + 3 + 15) & ~15;
+    const int sbp = 4 * (((sb + 3) / 4) | 1);
     const bool plain = eb == 1;
     const size_t lds = 2 * (plain ? 16 : (size_t)128 * sbp) + 2 * (size_t)64 * 512;
     GemmArgs a;
