@@ -33,10 +33,14 @@
 typedef _Float16 gh8 __attribute__((ext_vector_type(8)));
 typedef float gf4 __attribute__((ext_vector_type(4)));
 
-#define GM_WV 4
+#define GM_NR 1     // 16-row MFMA column blocks per wave
+#define GM_RB 128   // weight rows per workgroup (GM_WV waves x GM_NR x 16)
+#define GM_WV (GM_RB / (16 * GM_NR))
 #define GM_NTH (64 * GM_WV)
-#define GM_RB 128   // weight rows per workgroup (GM_WV waves x 2 x 16)
+static_assert(GM_NTH == GS_GEMM_THREADS, "host launch width");
 #define GM_TN 64    // tokens per workgroup (4 x 16)
+
+template <bool B> struct BoolC { static constexpr bool value = B; };
 
 // 8 floats -> 8 halves (round to nearest even, as __floats2half2_rn)
 // (a vector conversion: v_cvt_pk_f16_f32, two values per instruction, round to nearest even)
@@ -155,21 +159,28 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         }
     };
     auto x_store = [&](int buf, int b, const float4 (&xv)[NXA][2]) {
+        auto put = [&](auto masked) {
 #pragma unroll
-        for (int i = 0; i < NXA; i++) {
-            const int y = tid + GM_NTH * i, t = y >> 5, c = y & 31;
-            const bool ok = t < ntok && 256 * b + 8 * c < K;
-            const float f[8] = {ok ? xv[i][0].x : 0.f, ok ? xv[i][0].y : 0.f, ok ? xv[i][0].z : 0.f,
-                                ok ? xv[i][0].w : 0.f, ok ? xv[i][1].x : 0.f, ok ? xv[i][1].y : 0.f,
-                                ok ? xv[i][1].z : 0.f, ok ? xv[i][1].w : 0.f};
-            *(gh8 *)(abuf + buf * ASLAB + t * 512 + ((c ^ (t & 15)) << 4)) = to_h8(f);
-        }
+            for (int i = 0; i < NXA; i++) {
+                const int y = tid + GM_NTH * i, t = y >> 5, c = y & 31;
+                const bool ok = !decltype(masked)::value || (t < ntok && 256 * b + 8 * c < K);
+                const float f[8] = {ok ? xv[i][0].x : 0.f, ok ? xv[i][0].y : 0.f, ok ? xv[i][0].z : 0.f,
+                                    ok ? xv[i][0].w : 0.f, ok ? xv[i][1].x : 0.f, ok ? xv[i][1].y : 0.f,
+                                    ok ? xv[i][1].z : 0.f, ok ? xv[i][1].w : 0.f};
+                *(gh8 *)(abuf + buf * ASLAB + t * 512 + ((c ^ (t & 15)) << 4)) = to_h8(f);
+            }
+        };
+        // masking only where the tile has missing tokens or the row ends inside the step (a
+        // workgroup-uniform branch)
+        if (ntok < GM_TN || 256 * (b + 1) > K) put(BoolC<true>{});
+        else put(BoolC<false>{});
     };
-    gf4 acc[4][2];
+
+    gf4 acc[4][GM_NR];
 #pragma unroll
     for (int tt = 0; tt < 4; tt++)
 #pragma unroll
-        for (int n = 0; n < 2; n++) acc[tt][n] = gf4{0.f, 0.f, 0.f, 0.f};
+        for (int n = 0; n < GM_NR; n++) acc[tt][n] = gf4{0.f, 0.f, 0.f, 0.f};
 
     {   // prologue: super-block 0
         uint4 rv[NRAW];
@@ -194,10 +205,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         raw_load(more ? b + 1 : b, rv, rx);
         x_load(more ? b + 1 : b, xv);
         // B fragments: units 2q, 2q+1 of this lane's two rows, rounded to f16
-        gh8 bf[2][2][4];
+        gh8 bf[GM_NR][2][4];
 #pragma unroll
-        for (int n = 0; n < 2; n++) {
-            const int rr = min(wave * 32 + 16 * n + j, nrows - 1);
+        for (int n = 0; n < GM_NR; n++) {
+            const int rr = min(wave * 16 * GM_NR + 16 * n + j, nrows - 1);
 #pragma unroll
             for (int hu = 0; hu < 2; hu++) {
                 float v[32];
@@ -223,7 +234,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
                 if (tt < ntt) {
                     const gh8 av = *(const gh8 *)(slab + (16 * tt + j) * 512 + ((cc ^ j) << 4));
 #pragma unroll
-                    for (int n = 0; n < 2; n++)
+                    for (int n = 0; n < GM_NR; n++)
                         acc[tt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[n][m >> 2][m & 3], acc[tt][n], 0, 0, 0);
                 }
             }
@@ -243,8 +254,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
             const int t = 16 * tt + 4 * q + i;
             if (t < ntok) {
 #pragma unroll
-                for (int n = 0; n < 2; n++) {
-                    const int rr = wave * 32 + 16 * n + j;
+                for (int n = 0; n < GM_NR; n++) {
+                    const int rr = wave * 16 * GM_NR + 16 * n + j;
                     if (rr < nrows) {
                         float *dst = Y + (int64_t)(n0 + t) * a.y_stride + r0 + rr;
                         *dst = a.accumulate ? *dst + acc[tt][n][i] : acc[tt][n][i];

@@ -531,7 +531,7 @@ GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows
     // row block r runs on XCD r % 8 (workgroup w -> XCD w % 8): 8 x ceil(n_rb / 8) x n_tb workgroups
     const int64_t nwg = (int64_t)8 * ((a.n_rb + 7) / 8) * a.n_tb;
     if (nwg > 0x7fffffff || n_batch > 65535) return hipErrorInvalidValue;
-    return launch("gs_k_gemm_" + std::to_string(ty), dim3((unsigned)nwg, n_batch, 1), dim3(256, 1, 1), lds,
+    return launch("gs_k_gemm_" + std::to_string(ty), dim3((unsigned)nwg, n_batch, 1), dim3(GS_GEMM_THREADS, 1, 1), lds,
                   (hipStream_t)s, a);
 }
 

@@ -107,6 +107,8 @@ struct RowsQArgs {
 };
 
 // Quantized GEMM (gemm.hip): Y[z][n][r] (+)= sum_k f16(deq(W[z][r][k])) * f16(X[z][n][k])
+// threads per gs_k_gemm_* workgroup (gemm.hip: 8 waves, 16 weight rows each)
+#define GS_GEMM_THREADS 512
 struct GemmArgs {
     const uint8_t *W;
     const float *X;
