@@ -70,7 +70,7 @@ struct GemmFmt {
     }
 };
 
-template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
+template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32]), int GM_NBUF>
 __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     using F = GemmFmt<QKB, BB, DEC>;
     constexpr int CPR = F::PLAIN ? 1 : (F::SBP + 15) / 16;          // raw 16-byte chunks per row
@@ -80,7 +80,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     constexpr int NXA = GM_TN * 32 / GM_NTH;                        // 16-byte A chunks per thread (8)
     extern __shared__ __align__(16) uint8_t gm_lds[];
     uint8_t *const rawbuf = gm_lds;
-    uint8_t *const abuf = gm_lds + 2 * RAWB;
+    uint8_t *const abuf = gm_lds + GM_NBUF * RAWB;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4;
@@ -182,7 +182,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
 #pragma unroll
         for (int n = 0; n < GM_NR; n++) acc[tt][n] = gf4{0.f, 0.f, 0.f, 0.f};
 
-    {   // prologue: super-block 0
+    if (GM_NBUF == 2) {   // prologue: super-block 0
         uint4 rv[NRAW];
         uint32_t rx[NRAW];
         float4 xv[NXA][2];
@@ -190,20 +190,30 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         x_load(0, xv);
         raw_store(0, 0, rv, rx);
         x_store(0, 0, xv);
+        __syncthreads();
     }
-    __syncthreads();
 
     const int ntt = (ntok + 15) >> 4;   // token row blocks with any token (wave-uniform)
     for (int b = 0; b < nsb; b++) {
-        const int buf = b & 1;
-        const bool more = b + 1 < nsb;
-        // next super-block in flight while this one is decoded and contracted (issued on the last
-        // step too, re-reading that step's data, so every wait on them is an exact count)
+        const int buf = GM_NBUF == 2 ? b & 1 : 0;
+        const bool more = GM_NBUF == 2 && b + 1 < nsb;
         uint4 rv[NRAW];
         uint32_t rx[NRAW];
         float4 xv[NXA][2];
-        raw_load(more ? b + 1 : b, rv, rx);
-        x_load(more ? b + 1 : b, xv);
+        if (GM_NBUF == 1) {
+            // one buffer: the other workgroup on the CU computes while this one loads
+            if (b > 0) __syncthreads();   // every wave is done with step b-1
+            raw_load(b, rv, rx);
+            x_load(b, xv);
+            raw_store(0, b, rv, rx);
+            x_store(0, b, xv);
+            __syncthreads();
+        } else {
+            // next super-block in flight while this one is decoded and contracted (issued on the
+            // last step too, re-reading that step's data, so every wait on them is an exact count)
+            raw_load(more ? b + 1 : b, rv, rx);
+            x_load(more ? b + 1 : b, xv);
+        }
         // B fragments: units 2q, 2q+1 of this lane's two rows, rounded to f16
         gh8 bf[GM_NR][2][4];
 #pragma unroll
@@ -243,7 +253,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
             raw_store(buf ^ 1, b + 1, rv, rx);
             x_store(buf ^ 1, b + 1, xv);
         }
-        __syncthreads();
+        if (GM_NBUF == 2) __syncthreads();
     }
 
     // lane holds tokens 16tt + 4q + i of row 32 wave + 16n + j
@@ -266,7 +276,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
 }
 
 #define GS_GEMM_KERNEL(TY, QKB, BB, DEC)                                                          \
-    extern "C" __global__ void __launch_bounds__(GM_NTH) gs_k_gemm_##TY(GemmArgs a) {               \
-        gemm_body<QKB, BB, DEC>(a);                                                              \
+    extern "C" __global__ void __launch_bounds__(GM_NTH, 3 - gs_gemm_nbuf(TY)) gs_k_gemm_##TY(GemmArgs a) {    \
+        gemm_body<QKB, BB, DEC, gs_gemm_nbuf(TY)>(a);                                            \
     }
 GS_TYPE_LIST(GS_GEMM_KERNEL)

@@ -510,7 +510,7 @@ GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows
     const int sb = eb == 1 ? 256 * (bb / qk) : 256 / eb * bb;
     const int sbp = 4 * (((sb + 3) / 4) | 1);
     const bool plain = eb == 1;
-    const size_t lds = 2 * (plain ? 16 : (size_t)128 * sbp) + 2 * (size_t)64 * 512;
+    const size_t lds = gs_gemm_nbuf(ty) * ((plain ? 16 : (size_t)128 * sbp) + (size_t)64 * 512);
     GemmArgs a;
     memset(&a, 0, sizeof(a));
     a.W = (const uint8_t *)W;
