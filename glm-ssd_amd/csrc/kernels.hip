@@ -23,7 +23,9 @@ __device__ __forceinline__ Q81 quant_unit(const float (&v)[32]) {
     for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
     Q81 r;
     r.d = amax / 127.0f;
-    const float id = r.d != 0.f ? 1.0f / r.d : 0.f;
+    // 1/d overflows for d < 2^-128 (a block of tiny subnormals): q = 0 (its f16 d is 0 anyway)
+    float id = r.d != 0.f ? 1.0f / r.d : 0.f;
+    id = id <= 3.40282347e38f ? id : 0.f;
     r.slo = r.shi = 0;
 #pragma unroll
     for (int w = 0; w < 8; w++) {
@@ -508,7 +510,8 @@ struct StreamPass {
             ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0x4E>(__builtin_bit_cast(float, ab))));   // [2,3,0,1]
             amax = __builtin_bit_cast(float, ab);
             const float d = q8_div127(amax);
-            const float id = d != 0.f ? 1.0f / d : 0.f;
+            float id = d != 0.f ? 1.0f / d : 0.f;
+            id = id <= 3.40282347e38f ? id : 0.f;   // d < 2^-128: q = 0, as quant_unit
             uint32_t w[2];
 #pragma unroll
             for (int h = 0; h < 2; h++) {

@@ -29,6 +29,7 @@
  */
 #include "oracle.h"
 #include "ggml_tables.h"
+#include <float.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -363,6 +364,9 @@ void or_quantize_q8_1(const float *x, int64_t n, uint8_t *out) {
         }
         float d = amax / 127.0f;
         float id = d != 0.0f ? 1.0f / d : 0.0f;
+        /* 1/d overflows for d < 2^-128 (a block of tiny subnormals): q = 0, as the stored f16 d is
+           0 for such a block anyway (the int conversion of an infinite product is undefined) */
+        if (!(id <= FLT_MAX)) id = 0.0f;
         int sum = 0;
         for (int j = 0; j < 32; j++) {
             float v = xb[j] * id;

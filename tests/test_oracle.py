@@ -184,7 +184,9 @@ def _q8_1_numpy(x):
     xb = x.reshape(-1, 32).astype(np.float32)
     amax = np.abs(xb).max(axis=1)
     d = (amax / np.float32(127)).astype(np.float32)
-    idv = np.where(d != 0, np.float32(1) / np.where(d != 0, d, np.float32(1)), np.float32(0)).astype(np.float32)
+    with np.errstate(over="ignore"):
+        idv = np.where(d != 0, np.float32(1) / np.where(d != 0, d, np.float32(1)), np.float32(0)).astype(np.float32)
+    idv = np.where(np.isfinite(idv), idv, np.float32(0)).astype(np.float32)   # d < 2^-128: q = 0
     v = (xb * idv[:, None]).astype(np.float32).astype(np.float64)
     q = (np.sign(v) * np.floor(np.abs(v) + 0.5)).astype(np.int64)
     s = (q.sum(axis=1).astype(np.float32) * d).astype(np.float32)
@@ -197,13 +199,17 @@ def test_q8_1_invariants_and_rederivation():
     x[:32] = 0.0                       # zero block
     x[32:64] = 0.5                     # constant block
     x[64:96] = np.linspace(-3, 3, 32)  # symmetric ramp (ties)
+    x[96:128] = np.float32(1e-40) * (np.arange(32) - 16)   # subnormals: 1/d overflows, q = 0
     q8 = O.quantize_q8_1(x).reshape(-1, 36)
     d = q8[:, 0:2].copy().view(np.float16).reshape(-1)
     s = q8[:, 2:4].copy().view(np.float16).reshape(-1)
     q = q8[:, 4:].view(np.int8).astype(np.int64)
     assert np.abs(q).max() <= 127
-    nz = np.abs(x.reshape(-1, 32)).max(axis=1) > 0
+    amax = np.abs(x.reshape(-1, 32)).max(axis=1)
+    tiny = (amax / np.float32(127)).astype(np.float32) < np.float32(2.0 ** -128)   # 1/d overflows
+    nz = (amax > 0) & ~tiny
     assert np.all(np.abs(q[nz]).max(axis=1) == 127)
+    assert tiny[3] and np.all(q[tiny] == 0) and np.all(d[tiny] == 0)
     assert np.all(q[0] == 0) and d[0] == 0 and s[0] == 0
     dw, sw, qw = _q8_1_numpy(x)
     assert np.array_equal(q, qw) and np.array_equal(d.view(np.uint16), dw.view(np.uint16))
