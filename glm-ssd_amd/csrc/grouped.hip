@@ -44,8 +44,13 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));   // staging chunk (a n
 #define GS_GRP_TAB_BYTES (16384 + 65536)
 __shared__ int gs_grp_pre[GS_GRP_EXP_MAX + 1];     // tile prefix over experts in schedule order
 __shared__ int gs_grp_order[GS_GRP_EXP_MAX];       // schedule order: experts by pair count, largest first
-__shared__ int gs_grp_ep_tok[64];                   // epilogue operands of the current tile's token slots
-__shared__ float gs_grp_ep_w[64], gs_grp_ep_sc[64];
+// epilogue operands of a tile's token slots, by tile parity (waves drift up to one position apart)
+__shared__ int gs_grp_ep_tok[2][64];
+__shared__ float gs_grp_ep_w[2][64], gs_grp_ep_sc[2][64];
+// fills of the four activation slots (slot s has been stored by cnt[s] waves so far) and, per tile
+// parity, the sequence number of the tile whose epilogue operands are in gs_grp_ep_*
+__shared__ uint32_t gs_grp_cnt[4];
+__shared__ uint32_t gs_grp_ep_seq[2];
 
 template <int TY, int NTH>
 __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
@@ -324,19 +329,25 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         }
     };
 
-    // prologue: weights of positions 0 and 1, activations of position 0. Three weight register
-    // sets rotate by role (the loop body is instantiated three times), so a set loaded for position
-    // p + 2 is not touched until position p + 2: no register copies, no early waits.
+    // prologue: weights and activations of positions 0 and 1 (nsb >= 2: both in the first tile).
+    // Three weight register sets rotate by role (the loop body is instantiated three times), so a
+    // set loaded for position p + 2 is not touched until position p + 2: no register copies.
     WRegs W0, W1, W2;
     {
-        u4 stg0[NLD];
+        u4 stg0[NLD], stg1[NLD];
         load_a(ar_cur, 0, stg0);
+        load_a(ar_cur, 1, stg1);
         load_w(cur, wo_cur, 0, W0);
         load_w(cur, wo_cur, 1, W1);
 #pragma unroll
         for (int k = 0; k < NLD; k++)
-            if (NCH % NTH == 0 || tid + NTH * k < NCH) *(u4 *)(stage + dst[k]) = stg0[k];
+            if (NCH % NTH == 0 || tid + NTH * k < NCH) {
+                *(u4 *)(stage + dst[k]) = stg0[k];
+                *(u4 *)(stage + SLAB + dst[k]) = stg1[k];
+            }
     }
+    if (tid < 4) gs_grp_cnt[tid] = tid < 2 ? NTH / 64 : 0u;   // slots 0, 1: positions 0, 1, stored by every wave
+    if (tid < 2) gs_grp_ep_seq[tid] = 0xffffffffu;
     __syncthreads();
 
     // Epilogue operands of the current tile (per token slot: token id, combine weight, activation
@@ -367,20 +378,49 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 #pragma unroll
             for (int mt = 0; mt < MATS; mt++) acc[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
 
-    int b = 0, buf = 0;
+    // Positions run through four activation slots without a workgroup barrier: each wave stores
+    // its share of position P + 2 at the end of position P and then counts the fill; position Q is
+    // read from slot Q % 4 once every wave has stored its share (the slot's count reaches
+    // 8 (Q / 4 + 1)). A wave reading Q thus knows every wave has finished Q - 2, so waves drift at
+    // most two positions apart, and the slot a wave overwrites at the end of P (last read at
+    // P - 2) is no longer read by anyone. The epilogue operands of tile T are published with T's
+    // sequence number (per tile parity) and awaited before the epilogue. Every wait is bounded:
+    // it gives up after 2^16 polls (no configuration comes near; it keeps a lost fill from
+    // hanging the GPU).
+    int b = 0, buf = 0, tpar = 0;
+    uint32_t pos = 0, tseq = 0;
+    auto wait_count = [&](const uint32_t *c, uint32_t want) __attribute__((always_inline)) {
+        for (int spin = 0; spin < (1 << 16); spin++) {
+            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile("" ::: "memory");   // no LDS read moves above the wait
+    };
+    auto wait_seq = [&](const uint32_t *c, uint32_t want) __attribute__((always_inline)) {
+        for (int spin = 0; spin < (1 << 16); spin++) {
+            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == want) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile("" ::: "memory");
+    };
+    auto wait_slot = [&]() __attribute__((always_inline)) {
+        if (pos > 1) wait_count(&gs_grp_cnt[buf], (uint32_t)(NTH / 64) * (pos / 4u + 1u));
+    };
     auto step = [&](WRegs &wu, WRegs &wl) __attribute__((always_inline)) -> bool {
+        wait_slot();
         // ---- issue: activations of position +1, weights of position +2 -------------------
         const bool last_sb = b == nsb - 1;
         const bool have1 = !last_sb || has_nxt;
+        const bool have2 = b + 2 < nsb || has_nxt;   // position +2 exists (nsb >= 2)
         // Both requests are issued unconditionally (at the end of the tile list they re-read valid
         // data of the current tile and are dropped), so every wait on them is an exact count.
         u4 stg[NLD];
         {
-            const bool a_nxt = last_sb;
+            const bool a_nxt = b + 2 >= nsb;
             int ar[NLD];
 #pragma unroll
             for (int k = 0; k < NLD; k++) ar[k] = a_nxt ? ar_nxt[k] : ar_cur[k];
-            load_a(ar, last_sb ? 0 : b + 1, stg);
+            load_a(ar, a_nxt ? b + 2 - nsb : b + 2, stg);
         }
         {
             const bool in_cur = b + 2 < nsb;
@@ -446,12 +486,13 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 
         // ---- tile epilogue: lane holds tokens 16t + 4q + i (i < 4) of row row0 + 16n + j ----
         if (last_sb) {
+            wait_seq(&gs_grp_ep_seq[tpar], tseq);
 #pragma unroll
             for (int tt = 0; tt < NT; tt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int slot = 16 * tt + 4 * q + i;
-                    const float sc = gs_grp_ep_sc[slot], wt = gs_grp_ep_w[slot];
+                    const float sc = gs_grp_ep_sc[tpar][slot], wt = gs_grp_ep_w[tpar][slot];
                     if (slot < cur.n_here && (KIND == 1 || wt != 0.f)) {
                         const int p = cur.p_beg + slot;
 #pragma unroll
@@ -462,7 +503,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                                     a.out[(int64_t)p * rows + r] =
                                         grp_swiglu(acc[tt][n][0][i] * sc, acc[tt][n][1][i] * sc, a.lim);
                                 else
-                                    unsafeAtomicAdd(a.out + (int64_t)gs_grp_ep_tok[slot] * rows + r, wt * (acc[tt][n][0][i] * sc));
+                                    unsafeAtomicAdd(a.out + (int64_t)gs_grp_ep_tok[tpar][slot] * rows + r, wt * (acc[tt][n][0][i] * sc));
                             }
                         }
                     }
@@ -475,20 +516,30 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                     for (int mt = 0; mt < MATS; mt++) acc[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
         }
         if (b == nsb - 2 && tid < MT) {   // read by the epilogue of position nsb-1, after the barrier
-            gs_grp_ep_tok[tid] = ep_tok;
-            gs_grp_ep_w[tid] = ep_w;
-            gs_grp_ep_sc[tid] = ep_sc;
+            gs_grp_ep_tok[tpar][tid] = ep_tok;
+            gs_grp_ep_w[tpar][tid] = ep_w;
+            gs_grp_ep_sc[tpar][tid] = ep_sc;
+            asm volatile("" ::: "memory");   // published after wave 0's stores (LDS keeps a wave's order)
+            if (tid == 0) __hip_atomic_store(&gs_grp_ep_seq[tpar], tseq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         if (!have1) return false;
 
-        // ---- advance: stage position +1, rotate the weight registers -------------------------
+        // ---- advance: stage position +2, rotate the weight registers -------------------------
+        if (have2) {
+            const int sbuf = (buf + 2) & 3;
 #pragma unroll
-        for (int k = 0; k < NLD; k++)
-            if (NCH % NTH == 0 || tid + NTH * k < NCH) *(u4 *)(stage + (buf ^ 1) * SLAB + dst[k]) = stg[k];
-        buf ^= 1;
+            for (int k = 0; k < NLD; k++)
+                if (NCH % NTH == 0 || tid + NTH * k < NCH) *(u4 *)(stage + sbuf * SLAB + dst[k]) = stg[k];
+            asm volatile("" ::: "memory");   // the fill is counted after this wave's stores (LDS keeps a wave's order)
+            if (lane == 0) __hip_atomic_fetch_add(&gs_grp_cnt[sbuf], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        buf = (buf + 1) & 3;
+        pos++;
         if (last_sb) {   // enter the next tile; fetch the one after it
             b = 0;
             t += tstep;
+            tpar ^= 1;
+            tseq++;
             cur = nxt;
 #pragma unroll
             for (int n = 0; n < NR; n++) wo_cur[n] = wo_nxt[n];
@@ -506,7 +557,6 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         } else {
             b++;
         }
-        __syncthreads();
         return true;
     };
     for (;;) {
@@ -528,7 +578,6 @@ GS_GRP_KERNEL(1, 1, 1, 8)
 GS_GRP_KERNEL(1, 1, 2, 8)
 GS_GRP_KERNEL(1, 2, 1, 8)
 GS_GRP_KERNEL(1, 2, 2, 8)
-GS_GRP_KERNEL(1, 4, 1, 8)
 GS_GRP_KERNEL(1, 1, 1, 16)
 GS_GRP_KERNEL(2, 1, 1, 8)
 GS_GRP_KERNEL(2, 1, 2, 8)
@@ -536,8 +585,6 @@ GS_GRP_KERNEL(2, 1, 4, 8)
 GS_GRP_KERNEL(2, 2, 1, 8)
 GS_GRP_KERNEL(2, 2, 2, 8)
 GS_GRP_KERNEL(2, 2, 4, 8)
-GS_GRP_KERNEL(2, 4, 1, 8)
-GS_GRP_KERNEL(2, 4, 2, 8)
 GS_GRP_KERNEL(2, 1, 1, 16)
 GS_GRP_KERNEL(2, 1, 2, 16)
 GS_GRP_KERNEL(2, 2, 1, 16)

@@ -609,9 +609,9 @@ hipError_t grouped_launch(int kind, int ty, GroupedArgs &a, int n_pairs, hipStre
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
-    static const std::vector<GrpShape> all1 = {{1, 1, 8}, {1, 2, 8}, {2, 1, 8}, {2, 2, 8}, {4, 1, 8}, {1, 1, 16}};
+    static const std::vector<GrpShape> all1 = {{1, 1, 8}, {1, 2, 8}, {2, 1, 8}, {2, 2, 8}, {1, 1, 16}};
     static const std::vector<GrpShape> all2 = {{1, 1, 8}, {1, 2, 8}, {1, 4, 8}, {2, 1, 8}, {2, 2, 8}, {2, 4, 8},
-                                               {4, 1, 8}, {4, 2, 8}, {1, 1, 16}, {1, 2, 16}, {2, 1, 16}};
+                                               {1, 1, 16}, {1, 2, 16}, {2, 1, 16}};
     // preference order (largest useful tile first), per token-chunk size
     static const std::vector<GrpShape> pref1 = {{2, 2, 8}, {2, 1, 8}, {1, 2, 8}, {1, 1, 16}, {1, 1, 8}};
     static const std::vector<GrpShape> pref2 = {{2, 4, 8}, {2, 2, 8}, {1, 4, 8}, {1, 2, 8}, {2, 1, 8}, {1, 1, 8}};
@@ -635,8 +635,8 @@ hipError_t grouped_launch(int kind, int ty, GroupedArgs &a, int n_pairs, hipStre
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
     const int threads = 64 * sh.wv;
-    // decode tables (80 KB, grouped.hip GS_GRP_TAB_BYTES) + two staged activation super-blocks
-    const size_t lds = 16384 + 65536 + 2 * (size_t)16 * sh.nt * 512;
+    // decode tables (80 KB, grouped.hip GS_GRP_TAB_BYTES) + four staged activation super-blocks
+    const size_t lds = 16384 + 65536 + 4 * (size_t)16 * sh.nt * 512;
     int per_cu = 1;
     {
         std::lock_guard<std::mutex> lk(g_mu);
