@@ -6,16 +6,15 @@
 // Dequantized weights and activations are rounded to f16 exactly as the reference's tiles are
 // (round to nearest even); the products run on v_mfma_f32_16x16x32_f16.
 //
-// Tile: 128 weight rows x 64 tokens per workgroup of 4 waves; a wave owns 32 rows (two 16-row
-// MFMA column blocks) and all 64 tokens (four 16-token row blocks): 8 accumulators, each A
-// fragment (tokens) feeds 2 MFMAs and each B fragment (weights) 4. The K loop steps one
-// 256-element super-block at a time:
+// Tile: 128 weight rows x 64 tokens per workgroup of 8 waves; a wave owns 16 rows (one MFMA
+// column block) and all 64 tokens (four 16-token row blocks): 4 accumulators, each B fragment
+// (weights) feeds 4 MFMAs. The K loop steps one 256-element super-block at a time:
 //   * raw weight bytes of the tile's rows (one super-block each) are copied into LDS with 16-byte
 //     loads (one buffer resource per tile, so the tail of the last row reads zeros, never past
-//     the matrix), prefetched one step ahead through registers; each lane then decodes its own
-//     two 32-element units of each of its rows from LDS with the exact unit decoders (exact.h)
-//     and rounds them to f16;
-//   * X rows are converted to f16 into LDS (one step ahead), 512 bytes per token row, 16-byte
+//     the matrix) and shifted to a 4-byte aligned slot; each lane then decodes its own two
+//     32-element units of its row from LDS with the exact unit decoders (exact.h) and rounds them
+//     to f16;
+//   * X rows are converted to f16 into LDS, 512 bytes per token row, 16-byte
 //     chunk c of token i at chunk position c ^ (i & 15) so the 16 lanes reading one chunk column
 //     hit distinct banks;
 //   * the K order inside a super-block is permuted so a lane's B fragments come from whole units:
@@ -42,6 +41,10 @@ static_assert(GM_NTH == GS_GEMM_THREADS, "host launch width");
 
 template <bool B> struct BoolC { static constexpr bool value = B; };
 
+// fills of the two LDS buffers of the double-buffered steps: buffer s has been stored by
+// gm_fill[s] waves so far
+__shared__ uint32_t gm_fill[2];
+
 // 8 floats -> 8 halves (round to nearest even, as __floats2half2_rn)
 // (a vector conversion: v_cvt_pk_f16_f32, two values per instruction, round to nearest even)
 typedef float gf8 __attribute__((ext_vector_type(8)));
@@ -53,7 +56,7 @@ __device__ __forceinline__ gh8 to_h8(const float *v) {
 template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
 struct GemmFmt {
     static constexpr bool PLAIN = QKB == 1;
-    // bytes of one 256-element super-block of a row, and its LDS slot (16-byte multiple)
+    // bytes of one 256-element super-block of a row
     static constexpr int SB = QKB == 1 ? 256 * BB : 256 / QKB * BB;
     // LDS slot: the super-block realigned to the slot start (the copy reads from the 4-byte
     // boundary at or below the block and shifts the bytes into place), so every decoder sees a
@@ -190,8 +193,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         x_load(0, xv);
         raw_store(0, 0, rv, rx);
         x_store(0, 0, xv);
+        if (tid < 2) gm_fill[tid] = tid == 0 ? GM_WV : 0u;   // buffer 0: step 0, stored by every wave
         __syncthreads();
     }
+    // Double-buffered steps without a workgroup barrier: step b is read from buffer b & 1 once
+    // every wave has stored its share of it (the buffer's fill count reaches GM_WV (b / 2 + 1));
+    // each wave stores step b + 1 at the end of step b and then counts the fill. A wave reading
+    // step b thus knows every wave has finished computing step b - 1, the last reader of the
+    // buffer it overwrites next. The wait is bounded (2^16 polls; it keeps a lost fill from
+    // hanging the GPU).
+    auto wait_fill = [&](int b) __attribute__((always_inline)) {
+        const uint32_t want = (uint32_t)GM_WV * (uint32_t)(b / 2 + 1);
+        for (int spin = 0; spin < (1 << 16); spin++) {
+            if (__hip_atomic_load(&gm_fill[b & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile("" ::: "memory");   // no LDS read moves above the wait
+    };
 
     const int ntt = (ntok + 15) >> 4;   // token row blocks with any token (wave-uniform)
     for (int b = 0; b < nsb; b++) {
@@ -213,6 +231,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
             // last step too, re-reading that step's data, so every wait on them is an exact count)
             raw_load(more ? b + 1 : b, rv, rx);
             x_load(more ? b + 1 : b, xv);
+            if (b > 0) wait_fill(b);
         }
         // B fragments: units 2q, 2q+1 of this lane's two rows, rounded to f16
         gh8 bf[GM_NR][2][4];
@@ -252,8 +271,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         if (more) {
             raw_store(buf ^ 1, b + 1, rv, rx);
             x_store(buf ^ 1, b + 1, xv);
+            asm volatile("" ::: "memory");   // counted after this wave's stores (LDS keeps a wave's order)
+            if (lane == 0) __hip_atomic_fetch_add(&gm_fill[buf ^ 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        if (GM_NBUF == 2) __syncthreads();
     }
 
     // lane holds tokens 16tt + 4q + i of row 32 wave + 16n + j
