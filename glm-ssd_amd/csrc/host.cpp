@@ -344,6 +344,19 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
     if (B < 1 || B > 8 || rows < 0 || n_batch < 1) return hipErrorInvalidValue;
     if (!check_w(W, row_stride) || (n_batch > 1 && (w_bs & 1))) return hipErrorInvalidValue;
     if (rows == 0) return 0;
+    // more than 4 vectors whose units do not fit 8-vector registers (K > 2048): groups of 4 vectors
+    // over the whole K instead of K slices of 8 vectors (8 x 4096 Q8_0: 14 us against 28 us). Both
+    // groups of an 8-vector call run in one launch (blockIdx.y), reading the same weights at the
+    // same time.
+    if (B > 4 && n_batch == 1 && K > 64 * 32) {
+        if (B == 8)
+            return gemv_impl(ty, W, row_stride, K, rows, x, x_stride, y, y_stride, 4, accumulate, 2, 0, 4 * x_stride,
+                             4 * y_stride, s);
+        int e = gemv_impl(ty, W, row_stride, K, rows, x, x_stride, y, y_stride, 4, accumulate, 1, 0, 0, 0, s);
+        if (e) return e;
+        return gemv_impl(ty, W, row_stride, K, rows, x + 4 * x_stride, x_stride, y + 4 * y_stride, y_stride, B - 4,
+                         accumulate, 1, 0, 0, 0, s);
+    }
     // split K so one lane's q8_1 activation units fit in registers: K <= 64 lanes x (8/NV) units x 32
     const int NVt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
     const int kmax_units = 64 * (8 / NVt);

@@ -196,6 +196,16 @@ def test_gemv_long_rows_split(ty, stream):
     assert _gemv_case(ty, 64, 12288, 4, stream, 12) <= REL_L2
 
 
+@pytest.mark.parametrize("ty", [T.Q8_0, T.Q4_K, T.IQ2_XXS])
+def test_gemv_5_to_8_vectors_token_groups(ty, stream):
+    # more than 4 vectors with K > 2048 run as groups of 4 vectors over the whole K (B = 8: both
+    # groups in one launch; B = 5..7: a group of 4 and one of B - 4), with strides and accumulate
+    for B in (5, 7, 8):
+        assert _gemv_case(ty, 130, 4096, B, stream, 50 + B) <= REL_L2
+    assert _gemv_case(ty, 130, 4096, 8, stream, 61, accumulate=True, x_stride=4096 + 4) <= REL_L2
+    assert _gemv_case(ty, 130, 4096, 6, stream, 62, accumulate=True) <= REL_L2
+
+
 def test_gemv_batched(stream):
     ty, K, rows, nb = T.Q4_K, 512, 96, 5
     rb = G.row_bytes(ty, K)
