@@ -311,8 +311,8 @@ __device__ __forceinline__ void signed_dot8x4(const uint2 (&g_)[4], const uint2 
     }
 }
 
-// A unit decoded ahead of its activations (the fused FFN's down pass does this while it waits at
-// the grid barrier): grid bytes with the signs applied, 2s+1 and the block scale. dot_pre is then
+// A unit decoded ahead of its activations (the one-token down pass does this while its activation
+// staging is in flight): grid bytes with the signs applied, 2s+1 and the block scale. dot_pre is then
 // the integer dot and scaling of signed_dot8x4<NV, false>, operation for operation (same result).
 struct PreUnit {
     uint2 g[4];
