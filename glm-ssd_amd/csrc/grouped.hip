@@ -42,8 +42,7 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));   // staging chunk (a n
 // A B fragment (8 weights) is one 16-byte grid read, one 16-byte sign read and 4 XORs.
 #define GS_GRP_GRID_OFF 16384
 #define GS_GRP_TAB_BYTES (16384 + 65536)
-__shared__ int gs_grp_pre[GS_GRP_EXP_MAX + 1];     // tile prefix over experts in schedule order
-__shared__ int gs_grp_order[GS_GRP_EXP_MAX];       // schedule order: experts by pair count, largest first
+__shared__ int gs_grp_pre[GS_GRP_EXP_MAX + 1];     // tile prefix over the experts
 // epilogue operands of a tile's token slots, by tile parity (waves drift up to one position apart)
 __shared__ int gs_grp_ep_tok[2][64];
 __shared__ float gs_grp_ep_w[2][64], gs_grp_ep_sc[2][64];
@@ -141,30 +140,16 @@ __device__ __forceinline__ float grp_swiglu(float g, float u, float lim) {   // 
     return g / (1.f + expf(-g)) * u;
 }
 
-// Tile list. Experts are scheduled by pair count, largest first (rank = experts with more pairs,
-// or as many and a lower id): the long tiles of hot experts start first and the short ones fill
-// in behind them. Expert e owns ceil(m_e / MT) * nrb consecutive tiles, the token chunks of one
-// row block adjacent (chunk fastest), so the chunks that read the same weights run side by side.
+// Tile list, experts in id order. Expert e owns ceil(m_e / MT) * nrb consecutive tiles, the token
+// chunks of one row block adjacent (chunk fastest), so the chunks that read the same weights run
+// side by side. (Scheduling experts by pair count, largest first, made no difference at 512
+// tokens: every tile streams the same K, so tiles cost about the same; the count ranking itself,
+// done by every workgroup, took 10 us of a 4-token call.)
 // m_tmp: n_exp ints of scratch (the staging area, free during the prologue).
 template <int NTH>
 __device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb, int *m_tmp) {
     const int tid = threadIdx.x, lane = tid & 63;
-    const int n4 = (a.n_exp + 3) >> 2;   // m_tmp padded to whole int4 with -1 (sorts last)
-    for (int e = tid; e < 4 * n4; e += NTH) m_tmp[e] = e < a.n_exp ? a.offs[e + 1] - a.offs[e] : -1;
-    __syncthreads();
-    // rank by counting (every lane of a wave reads the same int4: one broadcast LDS read per 4 experts)
-    for (int e = tid; e < a.n_exp; e += NTH) {
-        const int m = m_tmp[e];
-        int rank = 0;
-#pragma unroll 8
-        for (int f4 = 0; f4 < n4; f4++) {
-            const int4 v = ((const int4 *)m_tmp)[f4];
-            const int f = 4 * f4;
-            rank += (v.x > m || (v.x == m && f < e)) + (v.y > m || (v.y == m && f + 1 < e)) +
-                    (v.z > m || (v.z == m && f + 2 < e)) + (v.w > m || (v.w == m && f + 3 < e));
-        }
-        gs_grp_order[rank] = e;
-    }
+    for (int e = tid; e < a.n_exp; e += NTH) m_tmp[e] = a.offs[e + 1] - a.offs[e];
     __syncthreads();
     if (tid < 64) {
         int carry = 0;
@@ -172,7 +157,7 @@ __device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb
             const int r = r0 + lane;
             int cnt = 0;
             if (r < a.n_exp) {
-                const int m = m_tmp[gs_grp_order[r]];
+                const int m = m_tmp[r];
                 cnt = m > 0 ? (m + MT - 1) / MT * nrb : 0;
             }
             int v = cnt;
@@ -247,14 +232,13 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         const uint8_t *wb[MATS];   // expert matrix bases (uniform)
     };
     auto describe = [&](int tt_, Desc &d) {
-        int lo = 0, hi = a.n_exp;   // largest rank r with pre[r] <= t
+        int lo = 0, hi = a.n_exp;   // largest expert e with pre[e] <= t (the owner of tile t)
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
             if (gs_grp_pre[mid] <= tt_) lo = mid; else hi = mid;
         }
-        const int r = __builtin_amdgcn_readfirstlane(lo);
-        const int e = __builtin_amdgcn_readfirstlane(gs_grp_order[r]);
-        const int local = tt_ - gs_grp_pre[r];
+        const int e = __builtin_amdgcn_readfirstlane(lo);
+        const int local = tt_ - gs_grp_pre[e];
         const int o0 = ld_scalar(a.offs + e), o1 = ld_scalar(a.offs + e + 1);
         const int nch = (o1 - o0 + MT - 1) / MT;
         const int rb = local / nch, chunk = local - rb * nch;
