@@ -62,7 +62,7 @@ BN_EXPORT int bn_moe_decode(int ty_gu, int ty_dn, const GsMoeBatch *batches, int
     return 0;
 }
 
-// Decode step through gs_moe_ffn (the fused gate/up + down launch) over batch (i % nb); mean ms.
+// Decode step through gs_moe_ffn (gate/up then down in one call) over batch (i % nb); mean ms.
 BN_EXPORT int bn_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *batches, int nb, int nt, int64_t rs_gu, int n_embd,
                          int n_ff, int64_t rs_dn, const float *x, float *h, float *y, int steps, int warmup, void *s,
                          float *ms_step) {
