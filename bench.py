@@ -56,6 +56,8 @@ def bench_lib():
                           C.POINTER(C.c_float)]
     L.bn_moe_ffn.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, I64, C.c_int, C.c_int, I64, P, P, P, C.c_int,
                              C.c_int, P, C.POINTER(C.c_float)]
+    L.bn_moe_ffn_tokens.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, I64, C.c_int, C.c_int, I64, P, P, P,
+                                    C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_copy.argtypes = [P, P, C.c_size_t, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_read.argtypes = [P, C.c_int, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_gemm.argtypes = [C.c_int, P, C.c_int, I64, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P,
@@ -203,9 +205,19 @@ def run_moe_per_token(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
                          s.raw(), C.byref(ms)))
     t = ms.value * n_tok * 1e-3
     wbytes = float(np.mean(uniq)) * (2 * mat + mat_dn)
-    return dict(us_per_step=round(t * 1e6, 2), unique_experts=round(float(np.mean(uniq)), 1),
-                weight_bytes=int(wbytes), GBps=round(wbytes / t / 1e9, 1),
-                frac_hbm_peak=round(wbytes / t / 1e9 / HBM_PEAK_GBPS, 4), calls_per_step=n_tok, routings_rotated=n_rout)
+    # the same steps as one gs_moe_ffn_tokens call each (token t in blockIdx.y slice t)
+    xs = G.DeviceBuffer.from_array(rng.standard_normal((n_tok, n_embd)).astype(np.float32), s)
+    hs = G.DeviceBuffer(n_tok * k * n_ff * 4)
+    ys = G.DeviceBuffer(n_tok * n_embd * 4)
+    ys.zero(s)
+    G.check(L.bn_moe_ffn_tokens(layer["ty_gu"], layer["ty_dn"], C.cast(batches, C.c_void_p), n_rout, n_tok,
+                                layer["rbg"], n_embd, n_ff, layer["rbd"], xs.p, hs.p, ys.p, steps, warmup, s.raw(),
+                                C.byref(ms)))
+    t1 = ms.value * 1e-3
+    return dict(us_per_step=round(t * 1e6, 2), us_per_step_one_call=round(t1 * 1e6, 2),
+                unique_experts=round(float(np.mean(uniq)), 1), weight_bytes=int(wbytes), GBps=round(wbytes / t / 1e9, 1),
+                GBps_one_call=round(wbytes / t1 / 1e9, 1), frac_hbm_peak=round(wbytes / t / 1e9 / HBM_PEAK_GBPS, 4),
+                calls_per_step=n_tok, routings_rotated=n_rout)
 
 
 def run_read_ceiling(L, s, sizes, steps, warmup, min_pool=768 << 20):

@@ -81,6 +81,28 @@ BN_EXPORT int bn_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *batches, int nb
     return 0;
 }
 
+// Token-sliced routed-expert FFN: step i is one gs_moe_ffn_tokens call over the n_tok batches at
+// batches[(i % nr) * n_tok]; mean ms per step.
+BN_EXPORT int bn_moe_ffn_tokens(int ty_gu, int ty_dn, const GsMoeBatch *batches, int nr, int n_tok, int64_t rs_gu,
+                                int n_embd, int n_ff, int64_t rs_dn, const float *x, float *h, float *y, int steps,
+                                int warmup, void *s, float *ms_step) {
+    Timer t;
+    CK(t.init());
+    for (int i = 0; i < warmup; i++)
+        CK(gs_moe_ffn_tokens(ty_gu, ty_dn, &batches[(i % nr) * n_tok], n_tok, rs_gu, n_embd, n_ff, rs_dn, x, h, y,
+                             0.0f, s));
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    for (int i = 0; i < steps; i++)
+        CK(gs_moe_ffn_tokens(ty_gu, ty_dn, &batches[((warmup + i) % nr) * n_tok], n_tok, rs_gu, n_embd, n_ff, rs_dn, x,
+                             h, y, 0.0f, s));
+    CK(gs_event_record(t.b, s));
+    CK(gs_event_sync(t.b));
+    CK(gs_event_elapsed_ms(ms_step, t.a, t.b));
+    *ms_step /= steps;
+    return 0;
+}
+
 // GEMV over rotating weight copies Ws[i % nw] (defeats the last-level cache); mean ms per call.
 BN_EXPORT int bn_gemv(int ty, const void *const *Ws, int nw, int64_t rs, int K, int rows, const float *x, float *y,
                       int B, int steps, int warmup, void *s, float *ms) {

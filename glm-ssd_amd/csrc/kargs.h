@@ -30,7 +30,7 @@ struct StreamArgs {
     int64_t row_stride;              // bytes between rows
     int64_t x_stride;                // floats between activation vectors
     int64_t y_stride;                // floats between output vectors
-    int64_t w_bs, x_bs, y_bs;        // GEMV batch strides (bytes / floats / floats) per blockIdx.y
+    int64_t w_bs, x_bs, y_bs;        // per blockIdx.y slice: GEMV batch (bytes / floats / floats); MoE token (x, y)
     int K;                           // row length (elements)
     int rows;                        // rows per matrix
     int nvec;                        // activation vectors (B or tokens)

@@ -281,6 +281,7 @@ struct StreamPass {
     const float *x;
     float *y;
     int K, nu, nv, rows, lpr, lane, tot, ngroups, gid, nrow, ge, nxv, nxu;
+    int sy;   // GATEUP/DOWN: first pointer-table entry of this blockIdx.y slice (one token each)
     float rnu;   // 1/nu
     int64_t rs;
     const uint8_t *wg, *wu, *wb0;   // GATEUP gate / up, GEMV matrix (wave-uniform)
@@ -306,11 +307,12 @@ struct StreamPass {
         const uint8_t *wb = a.w0[0];
         x = a.x;
         y = a.y;
-        if (KIND == 0) {
-            wb += (int64_t)blockIdx.y * a.w_bs;
-            x += (int64_t)blockIdx.y * a.x_bs;
-            y += (int64_t)blockIdx.y * a.y_bs;
-        }
+        // blockIdx.y slices: GEMV batches (own matrix); GATEUP/DOWN tokens, slice y owning table
+        // entries [y * nseg, (y + 1) * nseg) and its own activations and outputs
+        if (KIND == 0) wb += (int64_t)blockIdx.y * a.w_bs;
+        x += (int64_t)blockIdx.y * a.x_bs;
+        y += (int64_t)blockIdx.y * a.y_bs;
+        sy = KIND != 0 ? (int)blockIdx.y * a.nseg : 0;
         K = a.K, nu = a.nu, nv = a.nvec, rows = a.rows;
         lpr = LP ? LP : a.lpr, lane = tid & (lpr - 1);
         tot = KIND == 2 ? a.nseg * nu : nu;          // units along the (concatenated) row
@@ -348,7 +350,7 @@ struct StreamPass {
         // combine weights likewise (lane i <- expert i), requested before the weight loads so the
         // activation setup does not wait for them
 #pragma unroll
-        for (int t = 0; t < NV; t++) wtl[t] = KIND == 2 && L64 < GS_SEG_MAX && t < nv ? a.wt[t][L64] : 0.f;
+        for (int t = 0; t < NV; t++) wtl[t] = KIND == 2 && L64 + sy < GS_SEG_MAX && t < nv ? a.wt[t][L64 + sy] : 0.f;
         wg = wu = nullptr;
         wb0 = wb;
         // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
@@ -380,15 +382,16 @@ struct StreamPass {
             return (uint64_t)lo | ((uint64_t)hi << 32);
         };
         if (KIND == 1) {
-            wg = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw0 >> 32), ge) << 32) |
-                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw0, ge));
-            wu = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw1 >> 32), ge) << 32) |
-                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw1, ge));
+            const int se = ge + sy;
+            wg = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw0 >> 32), se) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw0, se));
+            wu = (const uint8_t *)(((uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw1 >> 32), se) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw1, se));
         }
         if (KIND == 2) {
 #pragma unroll
             for (int j = 0; j < UX; j++) {
-                ubase[j] = (const uint8_t *)lane_u64(tw0, uspan[j]);
+                ubase[j] = (const uint8_t *)lane_u64(tw0, uspan[j] + sy);
                 if (LP == 64) uoff[j] += (uint32_t)(ubase[j] - a.wlo);
             }
         }

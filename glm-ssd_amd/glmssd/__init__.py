@@ -81,6 +81,8 @@ SIGNATURES = {
     "gs_moe_down": [C.c_int, C.POINTER(MoeBatch), C.c_int, _I64, C.c_int, C.c_int, _P, _P, _P],
     "gs_moe_ffn": [C.c_int, C.c_int, C.POINTER(MoeBatch), C.c_int, _I64, C.c_int, C.c_int, _I64, _P, _P, _P, C.c_float,
                    _P],
+    "gs_moe_ffn_tokens": [C.c_int, C.c_int, C.POINTER(MoeBatch), C.c_int, _I64, C.c_int, C.c_int, _I64, _P, _P, _P,
+                          C.c_float, _P],
     "gs_swiglu": [_P, _P, _P, _I64, C.c_float, _P],
     "gs_axpy": [_P, _P, C.c_float, _I64, _P],
     "gs_gemm": [C.c_int, _P, _I64, C.c_int, C.c_int, _P, _I64, _P, _I64, C.c_int, C.c_int, C.c_int, _I64, _I64, _I64,
@@ -280,6 +282,14 @@ class ops:
         """gs_moe_ffn: moe_gateup then moe_down."""
         check(lib().gs_moe_ffn(ty_gu, ty_dn, C.byref(batch), nt, rs_gu, n_embd, n_ff, rs_dn, _p(x), _p(h), _p(y), lim,
                                _raw(s)))
+
+    @staticmethod
+    def moe_ffn_tokens(ty_gu, ty_dn, batches, rs_gu, n_embd, n_ff, rs_dn, x, h, y, lim=0.0, s=None):
+        """gs_moe_ffn_tokens: moe_ffn of token t over batches[t] (one token each, equal expert counts),
+        x and y [n_tok][n_embd], h [n_tok][n][n_ff], in one gate/up and one down launch."""
+        arr = (MoeBatch * len(batches))(*batches)
+        check(lib().gs_moe_ffn_tokens(ty_gu, ty_dn, arr, len(batches), rs_gu, n_embd, n_ff, rs_dn, _p(x), _p(h), _p(y),
+                                      lim, _raw(s)))
 
 
     @staticmethod

@@ -138,11 +138,11 @@ class Mat:
 class MoeLayer:
     """One MoE FFN layer with every expert resident: the work of forward.rs:982-1136
     (`Engine::moe`) without the expert cache. forward(): router logits (F32 GEMV), host routing,
-    shared expert SwiGLU FFN into `out`, routed experts into an accumulator (up to 4 tokens: one
-    gs_moe_ffn per token over its own experts, where the engine's decode branch batches up
-    to 16 experts for 1-2 tokens; more tokens: the grouped MFMA kernel when
-    every expert matrix is IQ2_XXS or IQ3_XXS, else per-expert gather / GEMM / SwiGLU / scatter-add as
-    run_expert_rows), then out += accumulator.
+    shared expert SwiGLU FFN into `out`, routed experts into an accumulator (up to 16 tokens: a
+    one-token FFN per token over its own experts, in gs_moe_ffn_tokens calls of up to 32 (token,
+    expert) pairs, where the engine's decode branch batches up to 16 experts for 1-2 tokens; more
+    tokens: the grouped MFMA kernel when every expert matrix is IQ2_XXS or IQ3_XXS, else per-expert
+    gather / GEMM / SwiGLU / scatter-add as run_expert_rows), then out += accumulator.
 
     experts: list of (gate, up, down) host byte arrays; gate/up [n_ff rows x n_embd], down
     [n_embd rows x n_ff].
@@ -151,7 +151,7 @@ class MoeLayer:
     engine's ordered combine. One-token FFNs take each token's experts in id order (forward.rs:
     1071-1081); multi-token paths write every (route rank, token) pair into its own slot and sum
     the slots in rank order (forward.rs:1119-1127), so the output is bit-reproducible."""
-    MOE_MAX, PER_TOKEN_MAX = 16, 4
+    MOE_MAX, PER_TOKEN_MAX = 16, 16
 
     def __init__(self, router, bias, shared, experts, n_embd, n_ff, ty_gu, ty_down, k=8, weights_norm=True,
                  weights_scale=1.0, clamp_exp=0.0, clamp_shexp=0.0, router_ty=T.F32, shared_ty=(T.Q6_K,) * 3,
@@ -218,13 +218,31 @@ class MoeLayer:
                 groups[e].append((ti, w))
         used = [e for e in range(ne) if groups[e]]
         if t <= self.PER_TOKEN_MAX:
-            # decode and MTP sizes: one one-token FFN (gs_moe_ffn) per token over its own experts (on the
-            # config-2 experts: 2 tokens 36 us against 52 us as one 2-token batch over the union of
-            # their experts, 4 tokens 71 us against 116 us through the grouped GEMM)
+            # decode, MTP and short-batch sizes: a one-token FFN per token over its own experts, the
+            # tokens in gs_moe_ffn_tokens calls of up to 32 (token, expert) pairs when their expert
+            # counts are equal. On the config-2 experts (top-8 of 288, Zipf routing) 2/4/8/16 tokens
+            # take 23/40/88/167 us this way against 70/109/134/202 us through the grouped GEMM.
+            routes_d = [sorted(r, key=lambda ew: ew[0]) if self.deterministic else r for r in routes]
+            kk = len(routes_d[0])
+            if t > 1 and all(len(r) == kk for r in routes_d) and 0 < kk <= self.MOE_MAX:
+                per = max(1, 32 // kk)
+                h = self._buf("h", min(t, per) * kk * self.n_ff * 4)
+                for t0 in range(0, t, per):
+                    bs = []
+                    for r in routes_d[t0:t0 + per]:
+                        b = MoeBatch()
+                        b.n = kk
+                        for i, (e, w) in enumerate(r):
+                            b.gate[i], b.up[i], b.down[i] = (self.gate[e].ptr().value, self.up[e].ptr().value,
+                                                             self.down[e].ptr().value)
+                            b.w[0][i] = w
+                        bs.append(b)
+                    ops.moe_ffn_tokens(self.ty_gu, self.ty_down, bs, self.gate[0].row_bytes, n, self.n_ff,
+                                       self.down[0].row_bytes, _at(xn, t0 * n * 4), h, acc.ptr(t0 * n * 4),
+                                       self.lim, s)
+                routes_d = []
             h = self._buf("h", self.MOE_MAX * self.n_ff * 4)
-            for ti, r in enumerate(routes):
-                if self.deterministic:
-                    r = sorted(r, key=lambda ew: ew[0])
+            for ti, r in enumerate(routes_d):
                 for b0 in range(0, len(r), self.MOE_MAX):
                     chunk = r[b0:b0 + self.MOE_MAX]
                     b = MoeBatch()

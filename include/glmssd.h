@@ -117,6 +117,14 @@ int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, 
 int gs_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *b, int nt, int64_t rs_gu, int n_embd, int n_ff, int64_t rs_dn,
                const float *x, float *h, float *y, float lim, void *s);
 
+/* Additive (no counterpart in the reference): the routed-expert FFN of n_tok tokens, token t over
+ * its own one-token batch b[t] (every b[t].n equal, n_tok * n <= 32): exactly
+ * gs_moe_ffn(ty_gu, ty_dn, &b[t], 1, ..., x + t*n_embd, h + t*n*n_ff, y + t*n_embd, lim) for each
+ * t, as one gate/up and one down launch; replaces the per-token loop of the engine's MTP verify
+ * step through the MoE layer (crates/engine/src/forward.rs:1067-1107). */
+int gs_moe_ffn_tokens(int ty_gu, int ty_dn, const GsMoeBatch *b, int n_tok, int64_t rs_gu, int n_embd, int n_ff,
+                      int64_t rs_dn, const float *x, float *h, float *y, float lim, void *s);
+
 /* ---- GEMM and MoE glue (crates/cuda/src/lib.rs:71-74,115-122; kernels/gemm.cu, ops.cu) ---- */
 /* SwiGLU with clamp: y = silu(min(g,L)) * clamp(u,-L,L); L <= 0: no clamp (lib.rs:76; ops.cu:101-115) */
 int gs_swiglu(const float *g, const float *u, float *y, int64_t n, float lim, void *s);

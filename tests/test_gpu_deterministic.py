@@ -45,7 +45,7 @@ def _layer(nrng, ty_gu, ty_dn, n_embd, n_ff, ne, k, det, s):
     return mk(det), mk(not det), experts
 
 
-@pytest.mark.parametrize("t,ty_gu,ty_dn", [(3, T.IQ2_XXS, T.IQ3_XXS), (24, T.IQ2_XXS, T.IQ3_XXS),
+@pytest.mark.parametrize("t,ty_gu,ty_dn", [(3, T.IQ2_XXS, T.IQ3_XXS), (9, T.IQ2_XXS, T.IQ3_XXS), (24, T.IQ2_XXS, T.IQ3_XXS),
                                            (24, T.Q4_K, T.Q6_K)])
 def test_deterministic_layer(t, ty_gu, ty_dn):
     n_embd, n_ff, ne, k = 1024, 512, 16, 8

@@ -88,3 +88,74 @@ def test_moe_ffn(ty_gu, ty_dn, nt, n, n_embd, n_ff, lim, stream):
             f"y {np.array_equal(y, y2)}")
         assert e <= REL_L2
         assert np.array_equal(h, h2) and np.array_equal(y, y2)
+
+
+# (gate/up type, down type, tokens, experts per token, pool of experts, n_embd, n_ff, clamp): the
+# tokens draw their experts from a shared pool, so they overlap as MTP verify tokens do
+TOKEN_CASES = [(T.IQ2_XXS, T.IQ2_XXS, 4, 8, 12, 4096, 1536, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 3, 8, 10, 4096, 2048, 0.0),
+               (T.Q4_K, T.Q4_K, 2, 5, 6, 2048, 1024, 7.0), (T.Q6_K, T.Q6_K, 4, 4, 8, 2048, 512, 3.0),
+               (T.IQ2_XXS, T.IQ2_XXS, 2, 16, 20, 8192, 512, 0.0), (T.IQ3_XXS, T.IQ3_XXS, 32, 1, 3, 1024, 512, 0.0)]
+
+
+@pytest.mark.parametrize("ty_gu,ty_dn,n_tok,n,pool,n_embd,n_ff,lim", TOKEN_CASES)
+def test_moe_ffn_tokens(ty_gu, ty_dn, n_tok, n, pool, n_embd, n_ff, lim, stream):
+    """gs_moe_ffn_tokens is bit for bit gs_moe_ffn per token (h and y), and within the matmul
+    tolerance of the oracle."""
+    say(f"moe_ffn_tokens {G.TYPE_NAMES[ty_gu]}/{G.TYPE_NAMES[ty_dn]} n_tok={n_tok} n={n} pool={pool} "
+        f"{n_embd}x{n_ff} lim={lim}")
+    rng = O.Rng(991 + 17 * ty_gu + ty_dn + n_tok)
+    gate = [rng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(pool)]
+    up = [rng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(pool)]
+    down = [rng.random_blocks(ty_dn, n_embd * n_ff) for _ in range(pool)]
+    nrng = np.random.default_rng(n_embd + n_tok)
+    x = nrng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    experts = [nrng.choice(pool, n, replace=False) for _ in range(n_tok)]
+    w = nrng.random((n_tok, n)).astype(np.float32)
+    rbg, rbd = G.row_bytes(ty_gu, n_embd), G.row_bytes(ty_dn, n_ff)
+    bufs = [G.DeviceBuffer.from_array(a) for a in gate + up + down]
+    batches = []
+    for t in range(n_tok):
+        b = G.MoeBatch()
+        b.n = n
+        for i, e in enumerate(experts[t]):
+            b.gate[i], b.up[i], b.down[i] = bufs[e].p.value, bufs[pool + e].p.value, bufs[2 * pool + e].p.value
+            b.w[0][i] = w[t, i]
+        batches.append(b)
+    dx = G.DeviceBuffer.from_array(x)
+    y0 = nrng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    dh1 = G.DeviceBuffer(n_tok * n * n_ff * 4)
+    dy1 = G.DeviceBuffer.from_array(y0)
+    for t in range(n_tok):
+        G.ops.moe_ffn(ty_gu, ty_dn, batches[t], 1, rbg, n_embd, n_ff, rbd, dx.p.value + t * n_embd * 4,
+                      dh1.p.value + t * n * n_ff * 4, dy1.p.value + t * n_embd * 4, lim, stream)
+    y1 = dy1.download(np.float32, n_tok * n_embd, stream)
+    h1 = dh1.download(np.float32, n_tok * n * n_ff, stream)
+    if n_tok * n <= 12:
+        pt = [t for t in range(n_tok) for _ in range(n)]
+        pe = [int(e) for t in range(n_tok) for e in experts[t]]
+        pw = [float(w[t, i]) for t in range(n_tok) for i in range(n)]
+        want = O.moe_ffn(ty_gu, ty_dn, gate, up, down, rbg, rbd, n_embd, n_ff, x, pt, pe, pw, lim=lim, nthreads=8)
+        e = rel_l2(y1.reshape(n_tok, n_embd).astype(np.float64) - y0, want)
+        say(f"  per-token calls: y rel-L2 vs oracle {e:.2e}")
+        assert e <= REL_L2
+    for rep in range(2):
+        dh = G.DeviceBuffer(n_tok * n * n_ff * 4)
+        dy = G.DeviceBuffer.from_array(y0)
+        G.ops.moe_ffn_tokens(ty_gu, ty_dn, batches, rbg, n_embd, n_ff, rbd, dx, dh, dy, lim, stream)
+        y = dy.download(np.float32, n_tok * n_embd, stream)
+        h = dh.download(np.float32, n_tok * n * n_ff, stream)
+        say(f"  call {rep}: identical to per-token calls: h {np.array_equal(h, h1)} y {np.array_equal(y, y1)}")
+        assert np.array_equal(h, h1) and np.array_equal(y, y1)
+
+
+def test_moe_ffn_tokens_rejects(stream):
+    """Unequal expert counts, and more than 32 (token, expert) pairs, are rejected before any launch."""
+    b1, b2 = G.MoeBatch(), G.MoeBatch()
+    b1.n, b2.n = 4, 3
+    with pytest.raises(RuntimeError):
+        G.ops.moe_ffn_tokens(T.IQ2_XXS, T.IQ2_XXS, [b1, b2], 66, 256, 512, 66, 0, 0, 0, 0.0, stream)
+    bs = [G.MoeBatch() for _ in range(5)]
+    for b in bs:
+        b.n = 8
+    with pytest.raises(RuntimeError):
+        G.ops.moe_ffn_tokens(T.IQ2_XXS, T.IQ2_XXS, bs, 66, 256, 512, 66, 0, 0, 0, 0.0, stream)

@@ -35,17 +35,20 @@ def _swiglu(g, u, lim):
     return g * expit(g) * u   # logistic without exp overflow for large negative g
 
 
-@pytest.mark.parametrize("t,ty_dn", [(1, T.IQ3_XXS), (2, T.IQ3_XXS), (4, T.IQ3_XXS), (5, T.IQ3_XXS), (5, T.IQ2_XXS)])
+# 1-16 tokens: one-token FFNs (gs_moe_ffn, gs_moe_ffn_tokens); 20: the grouped MFMA kernel
+@pytest.mark.parametrize("t,ty_dn", [(1, T.IQ3_XXS), (2, T.IQ3_XXS), (4, T.IQ3_XXS), (5, T.IQ3_XXS), (5, T.IQ2_XXS),
+                                     (16, T.IQ2_XXS), (20, T.IQ3_XXS), (20, T.IQ2_XXS)])
 def test_moe_layer(t, ty_dn):
     n_embd, n_ff, n_sh, ne, k = 2048, 512, 1024, 32, 8
     lim_e, lim_s = 7.0, 0.0
     nrng = np.random.default_rng(t * 10 + ty_dn)
-    # weight scales of a trained layer's order (|N(0,0.01)| Q6_K, |N(0,0.02)| IQ), so activations
-    # stay finite through the unclamped shared expert
+    # small weight scales (|N(0,1e-4)| Q6_K super-block d, |N(0,0.02)| IQ), so the unclamped shared
+    # expert's activations stay within f16 range where its matmuls run as GEMMs (t > 8)
     router = (nrng.standard_normal((ne, n_embd)) * 0.05).astype(np.float32)
     bias = (nrng.standard_normal(ne) * 0.1).astype(np.float32)
-    shared = [synth.q6_k_matrix(nrng, n_sh, n_embd), synth.q6_k_matrix(nrng, n_sh, n_embd),
-              synth.q6_k_matrix(nrng, n_embd, n_sh)]
+    shared = [synth.random_blocks(nrng, T.Q6_K, n_sh * n_embd, 1e-4, [208]),
+              synth.random_blocks(nrng, T.Q6_K, n_sh * n_embd, 1e-4, [208]),
+              synth.random_blocks(nrng, T.Q6_K, n_embd * n_sh, 1e-4, [208])]
     experts = [(synth.random_blocks(nrng, T.IQ2_XXS, n_ff * n_embd, 0.02, [0]),
                 synth.random_blocks(nrng, T.IQ2_XXS, n_ff * n_embd, 0.02, [0]),
                 synth.random_blocks(nrng, ty_dn, n_embd * n_ff, 0.02, [0])) for _ in range(ne)]
@@ -62,15 +65,16 @@ def test_moe_layer(t, ty_dn):
     want_routes = route(logits.astype(np.float32), bias, k, True, 2.5)
     assert [[e for e, _ in r] for r in routes] == [[e for e, _ in r] for r in want_routes]
     rb_sh = G.row_bytes(T.Q6_K, n_embd)
-    g = O.gemv(T.Q6_K, shared[0], rb_sh, n_embd, n_sh, x, B=t)
-    u = O.gemv(T.Q6_K, shared[1], rb_sh, n_embd, n_sh, x, B=t)
+    sact = "f16" if t > 8 else "q8_1"   # the shared expert's matmuls: GEMV up to 8 vectors, else GEMM
+    g = O.gemv(T.Q6_K, shared[0], rb_sh, n_embd, n_sh, x, B=t, act=sact)
+    u = O.gemv(T.Q6_K, shared[1], rb_sh, n_embd, n_sh, x, B=t, act=sact)
     h = _swiglu(g, u, lim_s).astype(np.float32)
-    sh = O.gemv(T.Q6_K, shared[2], G.row_bytes(T.Q6_K, n_sh), n_sh, n_embd, h, B=t)
+    sh = O.gemv(T.Q6_K, shared[2], G.row_bytes(T.Q6_K, n_sh), n_sh, n_embd, h, B=t, act=sact)
     pt, pe, pw = [], [], []
     for ti, r in enumerate(want_routes):
         for e, w in r:
             pt.append(ti); pe.append(e); pw.append(w)
-    act = "f16s" if t > 4 else "q8_1"   # more than 4 tokens: grouped MFMA path, the GEMM semantics
+    act = "f16s" if t > MoeLayer.PER_TOKEN_MAX else "q8_1"   # grouped MFMA path: the GEMM semantics
     routed = O.moe_ffn(T.IQ2_XXS, ty_dn, [e[0] for e in experts], [e[1] for e in experts],
                        [e[2] for e in experts], G.row_bytes(T.IQ2_XXS, n_embd), G.row_bytes(ty_dn, n_ff), n_embd,
                        n_ff, x, pt, pe, pw, lim=lim_e, nthreads=8, act=act)
