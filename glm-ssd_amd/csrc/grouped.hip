@@ -42,14 +42,20 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));   // staging chunk (a n
 // A B fragment (8 weights) is one 16-byte grid read, one 16-byte sign read and 4 XORs.
 #define GS_GRP_GRID_OFF 16384
 #define GS_GRP_TAB_BYTES (16384 + 65536)
-__shared__ int gs_grp_pre[GS_GRP_EXP_MAX + 1];     // tile prefix over the experts
-// epilogue operands of a tile's token slots, by tile parity (waves drift up to one position apart)
-__shared__ int gs_grp_ep_tok[2][64];
-__shared__ float gs_grp_ep_w[2][64], gs_grp_ep_sc[2][64];
-// fills of the four activation slots (slot s has been stored by cnt[s] waves so far) and, per tile
-// parity, the sequence number of the tile whose epilogue operands are in gs_grp_ep_*
-__shared__ uint32_t gs_grp_cnt[4];
-__shared__ uint32_t gs_grp_ep_seq[2];
+// Workgroup bookkeeping, in the dynamic LDS after the tables and the activation slots (the kernels
+// declare no static LDS, so the dynamic LDS starts at address 0 and every table address is a
+// compile-time offset from 0: no base-address add per lookup).
+struct GrpMeta {
+    int pre[GS_GRP_EXP_MAX + 1];   // tile prefix over the experts
+    // epilogue operands of a tile's token slots, by tile parity (waves drift up to one position apart)
+    int ep_tok[2][64];
+    float ep_w[2][64], ep_sc[2][64];
+    // fills of the four activation slots (slot s has been stored by cnt[s] waves so far) and, per
+    // tile parity, the sequence number of the tile whose epilogue operands are in ep_*
+    uint32_t cnt[4];
+    uint32_t ep_seq[2];
+};
+static_assert(sizeof(GrpMeta) <= GS_GRP_META_BYTES, "bookkeeping fits its LDS share");
 
 template <int TY, int NTH>
 __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
@@ -147,7 +153,7 @@ __device__ __forceinline__ float grp_swiglu(float g, float u, float lim) {   // 
 // done by every workgroup, took 10 us of a 4-token call.)
 // m_tmp: n_exp ints of scratch (the staging area, free during the prologue).
 template <int NTH>
-__device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb, int *m_tmp) {
+__device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb, int *m_tmp, int *pre) {
     const int tid = threadIdx.x, lane = tid & 63;
     for (int e = tid; e < a.n_exp; e += NTH) m_tmp[e] = a.offs[e + 1] - a.offs[e];
     __syncthreads();
@@ -166,10 +172,10 @@ __device__ __forceinline__ void grp_prefix(const GroupedArgs &a, int MT, int nrb
                 const int u = __shfl_up(v, o);
                 if (lane >= o) v += u;
             }
-            if (r < a.n_exp) gs_grp_pre[r + 1] = carry + v;
+            if (r < a.n_exp) pre[r + 1] = carry + v;
             carry += __shfl(v, 63);
         }
-        if (lane == 0) gs_grp_pre[0] = 0;
+        if (lane == 0) pre[0] = 0;
     }
 }
 
@@ -197,7 +203,11 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     constexpr int SLAB = MT * 512;                   // bytes of one staged super-block
     constexpr int NCH = SLAB / 16;                   // 16-byte chunks per staged super-block
     constexpr int NLD = (NCH + NTH - 1) / NTH;       // per thread (the last one may be partial)
-    extern __shared__ __align__(16) uint8_t gs_grp_dyn[];
+    // The launch's dynamic LDS is the kernel's only LDS, so it starts at LDS address 0; spelling
+    // that address as a constant (rather than through an extern __shared__ symbol, whose address
+    // is left to the linker) lets every table address fold into the load's offset field.
+    uint8_t *const gs_grp_dyn =
+        (uint8_t *)__builtin_bit_cast(__attribute__((address_space(3))) uint8_t *, (uint32_t)0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4;
     const uint32_t r16 = (uint32_t)(j & 7) << 4;   // the lane's sign-table replica
@@ -207,9 +217,10 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     uint8_t *const tab = gs_grp_dyn;
     uint8_t *const stage = gs_grp_dyn + GS_GRP_TAB_BYTES;
     grp_tables<TY, NTH>(tab, tid);
-    grp_prefix<NTH>(a, MT, nrb, (int *)stage);
+    GrpMeta &M = *(GrpMeta *)(gs_grp_dyn + GS_GRP_TAB_BYTES + 4 * SLAB);
+    grp_prefix<NTH>(a, MT, nrb, (int *)stage, M.pre);
     __syncthreads();
-    const int total = gs_grp_pre[a.n_exp];
+    const int total = M.pre[a.n_exp];
     // Workgroup w runs on XCD w % 8 (round-robin dispatch). With a grid that is a multiple of 8,
     // round k of workgroup w takes tile k*G + (w % 8) * G/8 + w / 8, so consecutive tiles of the
     // list (the chunks of one row block) run at the same time on one XCD and share its L2.
@@ -235,10 +246,10 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         int lo = 0, hi = a.n_exp;   // largest expert e with pre[e] <= t (the owner of tile t)
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
-            if (gs_grp_pre[mid] <= tt_) lo = mid; else hi = mid;
+            if (M.pre[mid] <= tt_) lo = mid; else hi = mid;
         }
         const int e = __builtin_amdgcn_readfirstlane(lo);
-        const int local = tt_ - gs_grp_pre[e];
+        const int local = tt_ - M.pre[e];
         const int o0 = ld_scalar(a.offs + e), o1 = ld_scalar(a.offs + e + 1);
         const int nch = (o1 - o0 + MT - 1) / MT;
         const int rb = local / nch, chunk = local - rb * nch;
@@ -330,8 +341,8 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                 *(u4 *)(stage + SLAB + dst[k]) = stg1[k];
             }
     }
-    if (tid < 4) gs_grp_cnt[tid] = tid < 2 ? NTH / 64 : 0u;   // slots 0, 1: positions 0, 1, stored by every wave
-    if (tid < 2) gs_grp_ep_seq[tid] = 0xffffffffu;
+    if (tid < 4) M.cnt[tid] = tid < 2 ? NTH / 64 : 0u;   // slots 0, 1: positions 0, 1, stored by every wave
+    if (tid < 2) M.ep_seq[tid] = 0xffffffffu;
     __syncthreads();
 
     // Epilogue operands of the current tile (per token slot: token id, combine weight, activation
@@ -388,7 +399,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         asm volatile("" ::: "memory");
     };
     auto wait_slot = [&]() __attribute__((always_inline)) {
-        if (pos > 1) wait_count(&gs_grp_cnt[buf], (uint32_t)(NTH / 64) * (pos / 4u + 1u));
+        if (pos > 1) wait_count(&M.cnt[buf], (uint32_t)(NTH / 64) * (pos / 4u + 1u));
     };
     auto step = [&](WRegs &wu, WRegs &wl) __attribute__((always_inline)) -> bool {
         wait_slot();
@@ -470,13 +481,13 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 
         // ---- tile epilogue: lane holds tokens 16t + 4q + i (i < 4) of row row0 + 16n + j ----
         if (last_sb) {
-            wait_seq(&gs_grp_ep_seq[tpar], tseq);
+            wait_seq(&M.ep_seq[tpar], tseq);
 #pragma unroll
             for (int tt = 0; tt < NT; tt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int slot = 16 * tt + 4 * q + i;
-                    const float sc = gs_grp_ep_sc[tpar][slot], wt = gs_grp_ep_w[tpar][slot];
+                    const float sc = M.ep_sc[tpar][slot], wt = M.ep_w[tpar][slot];
                     if (slot < cur.n_here && (KIND == 1 || wt != 0.f)) {
                         const int p = cur.p_beg + slot;
 #pragma unroll
@@ -487,7 +498,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                                     a.out[(int64_t)p * rows + r] =
                                         grp_swiglu(acc[tt][n][0][i] * sc, acc[tt][n][1][i] * sc, a.lim);
                                 else
-                                    unsafeAtomicAdd(a.out + (int64_t)gs_grp_ep_tok[tpar][slot] * rows + r, wt * (acc[tt][n][0][i] * sc));
+                                    unsafeAtomicAdd(a.out + (int64_t)M.ep_tok[tpar][slot] * rows + r, wt * (acc[tt][n][0][i] * sc));
                             }
                         }
                     }
@@ -500,11 +511,11 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
                     for (int mt = 0; mt < MATS; mt++) acc[tt][n][mt] = f4{0.f, 0.f, 0.f, 0.f};
         }
         if (b == nsb - 2 && tid < MT) {   // read by the epilogue of position nsb-1, after the barrier
-            gs_grp_ep_tok[tpar][tid] = ep_tok;
-            gs_grp_ep_w[tpar][tid] = ep_w;
-            gs_grp_ep_sc[tpar][tid] = ep_sc;
+            M.ep_tok[tpar][tid] = ep_tok;
+            M.ep_w[tpar][tid] = ep_w;
+            M.ep_sc[tpar][tid] = ep_sc;
             asm volatile("" ::: "memory");   // published after wave 0's stores (LDS keeps a wave's order)
-            if (tid == 0) __hip_atomic_store(&gs_grp_ep_seq[tpar], tseq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (tid == 0) __hip_atomic_store(&M.ep_seq[tpar], tseq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         if (!have1) return false;
 
@@ -515,7 +526,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             for (int k = 0; k < NLD; k++)
                 if (NCH % NTH == 0 || tid + NTH * k < NCH) *(u4 *)(stage + sbuf * SLAB + dst[k]) = stg[k];
             asm volatile("" ::: "memory");   // the fill is counted after this wave's stores (LDS keeps a wave's order)
-            if (lane == 0) __hip_atomic_fetch_add(&gs_grp_cnt[sbuf], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) __hip_atomic_fetch_add(&M.cnt[sbuf], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         buf = (buf + 1) & 3;
         pos++;

@@ -703,8 +703,9 @@ hipError_t grouped_launch(int kind, int ty, GroupedArgs &a, int n_pairs, hipStre
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
     const int threads = 64 * sh.wv;
-    // decode tables (80 KB, grouped.hip GS_GRP_TAB_BYTES) + four staged activation super-blocks
-    const size_t lds = 16384 + 65536 + 4 * (size_t)16 * sh.nt * 512;
+    // decode tables (80 KB, grouped.hip GS_GRP_TAB_BYTES) + four staged activation super-blocks +
+    // the workgroup's bookkeeping
+    const size_t lds = 16384 + 65536 + 4 * (size_t)16 * sh.nt * 512 + GS_GRP_META_BYTES;
     int per_cu = 1;
     {
         std::lock_guard<std::mutex> lk(g_mu);

@@ -81,6 +81,7 @@ struct RowsArgs {
 
 // Grouped MoE GEMM (grouped.hip): pairs sorted by expert, offs = CSR offsets per expert.
 #define GS_GRP_EXP_MAX 1024   // experts per layer the device-side tile list holds
+#define GS_GRP_META_BYTES 6144   // grouped kernels' per-workgroup bookkeeping in LDS (tile prefix, epilogue operands, fill counters)
 struct GroupedArgs {
     const uint8_t *const *experts;   // [n_exp][3] device pointers: gate, up, down
     const int *offs;                 // [n_exp + 1] pair offsets
