@@ -173,9 +173,10 @@ def run_moe_grouped(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
 
 
 def run_moe_per_token(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
-    """Config 4 the way the MoE layer runs up to 4 tokens: one fused gs_moe_ffn call per token over
-    its own top-k experts (Zipf(1.1) routings as run_moe_grouped draws them, n_rout rotated).
-    Timed per call by bn_moe_ffn; a step is n_tok calls."""
+    """Config 4 as one-token FFNs, each token over its own top-k experts (Zipf(1.1) routings as
+    run_moe_grouped draws them, n_rout rotated), timed two ways: n_tok gs_moe_ffn calls per step
+    (bn_moe_ffn, us_per_step) and one gs_moe_ffn_tokens call per step, the MoE layer's path
+    (bn_moe_ffn_tokens, us_per_step_one_call)."""
     import glmssd as G
     from glmssd import synth
     n_exp, mat, mat_dn = layer["n_expert"], layer["mat"], layer["mat_dn"]
