@@ -350,7 +350,7 @@ struct StreamPass {
         // combine weights likewise (lane i <- expert i), requested before the weight loads so the
         // activation setup does not wait for them
 #pragma unroll
-        for (int t = 0; t < NV; t++) wtl[t] = KIND == 2 && L64 + sy < GS_SEG_MAX && t < nv ? a.wt[t][L64 + sy] : 0.f;
+        for (int t = 0; t < NV; t++) wtl[t] = KIND == 2 && L64 < GS_SEG_MAX && t < nv ? a.wt[t][L64] : 0.f;
         wg = wu = nullptr;
         wb0 = wb;
         // per-unit geometry; padding units re-read the lane's first unit (their activation is 0)
@@ -575,7 +575,7 @@ struct StreamPass {
             for (int t = 0; t < NV; t++) {
                 const int v = KIND == 2 ? uspan[j] * nv + t : t;
                 const float w = KIND == 2 ? __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                                uspan[j] << 2, __builtin_bit_cast(int, wtl[t])))
+                                                (uspan[j] + sy) << 2, __builtin_bit_cast(int, wtl[t])))
                                           : 1.f;   // routing weight folded into D
                 xr[j][t] = load_xu<F, XNEG>(xq, xm, K, nu, v, up, w, uval[j] && t < nv);
             }
