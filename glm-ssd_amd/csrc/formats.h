@@ -189,32 +189,52 @@ struct FQ4_K : UnitGeom<256, 144>, NoTable {
     }
 };
 
+// Q6_K (lib.rs:243-262). A super-block's 32-element unit of quarter q in half h takes the low
+// (q < 2) or high (q >= 2) nibbles of the 32 ql bytes at 64h + 32(q & 1) and 2-bit fields 2q of
+// the 32 qh bytes at 128 + 32h, so quarters q and q + 2 of a half read the same 64 bytes. The
+// streaming kernels number a super-block's units in pair order -- v = 0..7 is quarter
+// qp + 2(v & 1) of half v >> 2 with qp = (v >> 1) & 1 -- so the two units of a lane's pair (v even,
+// v + 1) share their bytes and load them once (load2: 9 registers per unit instead of 18) and
+// the activation unit of v is the natural unit nat(v) (xunit).
 struct FQ6_K : UnitGeom<256, 210>, NoTable {
-    static constexpr int TYPE = GS_Q6_K, QK = 256, BB = 210, TAB = 0, RAW = 18;
-    struct Raw { uint4 l0, l1, h0, h1; uint32_t sc, d; };
+    static constexpr int TYPE = GS_Q6_K, QK = 256, BB = 210, TAB = 0, RAW = 18, RAW2 = 9;
+    static constexpr bool PAIR = true, JOINT = true;
+    // single unit: a = ql, b = qh, e0 = its two int8 scales, e1 = d. Pair (load2): w0.a = ql,
+    // w0.e0 = both units' scales, w1.a = qh, w1.e0 = d.
+    struct Raw { uint4 a0, a1, b0, b1; uint32_t e0, e1; };
+    __device__ static __forceinline__ int nat(int v) { return (v & 4) | ((v >> 1) & 1) | ((v & 1) << 1); }
+    __device__ static __forceinline__ int xunit(int up) { return (up & ~7) | nat(up & 7); }
     template <class M>
-    __device__ static __forceinline__ void load(const M &m, uint32_t o, int j, Raw &w) {
-        const uint32_t half = (uint32_t)j >> 2, quarter = (uint32_t)j & 3;
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int v, Raw &w) {
+        const uint32_t n = (uint32_t)nat(v), half = n >> 2, quarter = n & 3;
         const uint32_t ql = o + 64 * half + 32 * (quarter & 1), qh = o + 128 + 32 * half;
-        w.l0 = m.u128(ql);
-        w.l1 = m.u128(ql + 16);
-        w.h0 = m.u128(qh);
-        w.h1 = m.u128(qh + 16);
-        w.sc = m.u16(o + 192 + 8 * half + 2 * quarter);
-        w.d = m.u16(o + 208);
+        w.a0 = m.u128(ql);
+        w.a1 = m.u128(ql + 16);
+        w.b0 = m.u128(qh);
+        w.b1 = m.u128(qh + 16);
+        w.e0 = m.u16(o + 192 + 8 * half + 2 * quarter);
+        w.e1 = m.u16(o + 208);
     }
-    template <int NV, bool XNEG = false>
-    __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
-                                               float (&r)[NV]) {
-        const int quarter = j & 3;
-        const int nsh = quarter >= 2 ? 4 : 0, hsh = 2 * quarter;
-        const uint32_t ql[8] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w, w.l1.x, w.l1.y, w.l1.z, w.l1.w};
-        const uint32_t qh[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int v, Raw &w0, Raw &w1) {
+        const uint32_t half = (uint32_t)v >> 2, qp = ((uint32_t)v >> 1) & 1;
+        const uint32_t ql = o + 64 * half + 32 * qp, qh = o + 128 + 32 * half, sc = o + 192 + 8 * half + 2 * qp;
+        w0.a0 = m.u128(ql);
+        w0.a1 = m.u128(ql + 16);
+        w1.a0 = m.u128(qh);
+        w1.a1 = m.u128(qh + 16);
+        w0.e0 = m.u16(sc) | (m.u16(sc + 4) << 16);
+        w1.e0 = m.u16(o + 208);
+    }
+    // one unit: 6-bit values from nibble shift nsh of ql and field hsh of qh, dotted per 16-element
+    // half with its int8 scale (sum (q-32) x = sum q x - 32 sum x)
+    template <int NV>
+    __device__ static __forceinline__ void dot_q(const uint32_t (&ql)[8], const uint32_t (&qh)[8], int nsh, int hsh,
+                                                 uint32_t sc, float d, const XU (&x)[NV], int nv, float (&r)[NV]) {
         uint32_t q[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = ((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4);
-        const int sc0 = (int8_t)(w.sc & 0xff), sc1 = (int8_t)((w.sc >> 8) & 0xff);
-        const float d = h2f(w.d);
+        const int sc0 = (int8_t)(sc & 0xff), sc1 = (int8_t)((sc >> 8) & 0xff);
 #pragma unroll
         for (int t = 0; t < NV; t++) {
             if (t < nv) {
@@ -223,10 +243,28 @@ struct FQ6_K : UnitGeom<256, 210>, NoTable {
                 for (int i = 0; i < 4; i++) lo = __builtin_amdgcn_sdot4((int)q[i], (int)x[t].q[i], lo, false);
 #pragma unroll
                 for (int i = 4; i < 8; i++) hi = __builtin_amdgcn_sdot4((int)q[i], (int)x[t].q[i], hi, false);
-                // sum (q-32) x = sum q x - 32 sum x, per 16-element half with its own scale
                 r[t] += (d * x[t].D) * (float)(sc0 * (lo - 32 * x[t].slo) + sc1 * (hi - 32 * x[t].shi));
             }
         }
+    }
+    template <int NV, bool XNEG = false>
+    __device__ static __forceinline__ void dot(const Raw &w, int v, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const int quarter = nat(v) & 3;
+        const uint32_t ql[8] = {w.a0.x, w.a0.y, w.a0.z, w.a0.w, w.a1.x, w.a1.y, w.a1.z, w.a1.w};
+        const uint32_t qh[8] = {w.b0.x, w.b0.y, w.b0.z, w.b0.w, w.b1.x, w.b1.y, w.b1.z, w.b1.w};
+        dot_q<NV>(ql, qh, quarter >= 2 ? 4 : 0, 2 * quarter, w.e0, h2f(w.e1), x, nv, r);
+    }
+    // the pair (v even, v + 1) loaded by load2, unit v then unit v + 1 (the order of two dot calls)
+    template <int NV>
+    __device__ static __forceinline__ void dot_pair(const Raw &w0, const Raw &w1, int v, const XU (&x0)[NV],
+                                                    const XU (&x1)[NV], int nv, float (&r)[NV]) {
+        const int qp = (v >> 1) & 1;
+        const uint32_t ql[8] = {w0.a0.x, w0.a0.y, w0.a0.z, w0.a0.w, w0.a1.x, w0.a1.y, w0.a1.z, w0.a1.w};
+        const uint32_t qh[8] = {w1.a0.x, w1.a0.y, w1.a0.z, w1.a0.w, w1.a1.x, w1.a1.y, w1.a1.z, w1.a1.w};
+        const float d = h2f(w1.e0);
+        dot_q<NV>(ql, qh, 0, 2 * qp, w0.e0 & 0xffffu, d, x0, nv, r);
+        dot_q<NV>(ql, qh, 4, 2 * qp + 4, w0.e0 >> 16, d, x1, nv, r);
     }
 };
 

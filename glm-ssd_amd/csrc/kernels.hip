@@ -158,10 +158,25 @@ __device__ __forceinline__ float swiglu_fast(float g, float u, float lim) {
 #ifndef GS_RING_EARLY
 #define GS_RING_EARLY 1
 #endif
+// Formats whose paired units share their bytes (JOINT: load2 fills the pair's registers once,
+// dot_pair decodes both, RAW2 registers per unit; their unit numbering within a block is a
+// permutation, so the activation unit of weight unit up is F::xunit(up)).
+template <class F, class = void> struct Joint { static constexpr bool value = false; static constexpr int raw2 = F::RAW; };
+template <class F> struct Joint<F, decltype((void)F::JOINT, void())> {
+    static constexpr bool value = F::JOINT;
+    static constexpr int raw2 = F::RAW2;
+};
+template <class F, class = void> struct Paired { static constexpr bool value = false; };
+template <class F> struct Paired<F, decltype((void)F::PAIR, void())> { static constexpr bool value = F::PAIR; };
 template <class F, int UMAX, int KIND = 0>
 __device__ __forceinline__ constexpr int pf_depth() {
-    constexpr int n = (KIND == 1 ? GS_PF_REGS_GU : GS_PF_REGS) / (F::RAW * UMAX);
-    return n < 1 ? 1 : (n > 8 ? 8 : n);
+    constexpr int ux = KIND == 1 ? UMAX / 2 : UMAX;
+    constexpr bool joint = Joint<F>::value && Paired<F>::value && ux % 2 == 0;
+    constexpr int n = (KIND == 1 ? GS_PF_REGS_GU : GS_PF_REGS) / ((joint ? Joint<F>::raw2 : F::RAW) * UMAX);
+    // joint formats keep two rows in flight however many units a lane holds: a wave's second row
+    // then streams while the first is decoded (Q6_K K = 12288: 6 units per lane)
+    constexpr int lo = joint ? 2 : 1;
+    return n < lo ? lo : (n > 8 ? 8 : n);
 }
 
 // Load activation unit (vector v, unit up) from the LDS q8_1 staging area; `scale` multiplies D
@@ -241,9 +256,8 @@ __device__ __forceinline__ void store_h(float *p, float v) {
 __device__ __forceinline__ int udiv_small(int u, float rd) { return (int)(((float)u + 0.5f) * rd); }
 
 // Formats that load two consecutive units of a block with one wide access (load2): d once and
-// one 16-byte read for both units' indices, half the vector-memory instructions of two loads.
-template <class F, class = void> struct Paired { static constexpr bool value = false; };
-template <class F> struct Paired<F, decltype((void)F::PAIR, void())> { static constexpr bool value = F::PAIR; };
+// one 16-byte read for both units' indices, half the vector-memory instructions of two loads
+// (Paired, declared with pf_depth above).
 
 // Formats whose units can be decoded ahead of the activations (PreUnit, predecode, dot_pre)
 template <class A, class B> struct is_same_t { static constexpr bool value = false; };
@@ -266,10 +280,15 @@ struct StreamPass {
     // activation prologue: 4 threads per 32-element unit (8 floats each), XP passes of GS_WG/4
     // units in flight before the weight loads (a decode-sized x is one pass: 2 loads per thread)
     static constexpr int XT = 4, XPU = GS_WG / XT;
-    // (down: a row's units, at most 64 * UX for the whole activation set, need UX / 2 passes)
-    static constexpr int XP = KIND == 2 ? (UX / 2 < 1 ? 1 : (UX / 2 > 4 ? 4 : UX / 2)) : (NV < 4 ? NV : 4);
+    // (down: a row's units, at most 64 * UX for the whole activation set, need UX / 2 passes; a
+    // GEMV's NV vectors of up to 64 * UX units each, NV * UX / 2: passes loaded inside the staging
+    // would queue behind the weight loads and wait for them, as vector loads return in order)
+    static constexpr int XPG = (NV * UX + 1) / 2;
+    static constexpr int XP = KIND == 2 ? (UX / 2 < 1 ? 1 : (UX / 2 > 4 ? 4 : UX / 2))
+                                        : KIND == 0 ? (XPG < NV ? NV : (XPG > 4 ? 4 : XPG)) : (NV < 4 ? NV : 4);
     // paired units: the lane's units j, j+1 (j even) are consecutive units of one block
     static constexpr bool PAIRS = Paired<F>::value && UX % 2 == 0;
+    static constexpr bool JOINT = Joint<F>::value && PAIRS;
     __device__ __forceinline__ int unit_of(int j) const {
         return PAIRS ? 2 * (lane + lpr * (j >> 1)) + (j & 1) : lane + lpr * j;
     }
@@ -577,7 +596,9 @@ struct StreamPass {
                 const float w = KIND == 2 ? __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
                                                 (uspan[j] + sy) << 2, __builtin_bit_cast(int, wtl[t])))
                                           : 1.f;   // routing weight folded into D
-                xr[j][t] = load_xu<F, XNEG>(xq, xm, K, nu, v, up, w, uval[j] && t < nv);
+                int xu = up;
+                if constexpr (Joint<F>::value) xu = F::xunit(up);
+                xr[j][t] = load_xu<F, XNEG>(xq, xm, K, nu, v, xu, w, uval[j] && t < nv);
             }
         }
         // Row results are gathered into lanes (lane p*NV + t of the group holds row p, vector t)
@@ -620,6 +641,14 @@ struct StreamPass {
                         if (i + 1 < PF * UMAX) TP::fetch(R[(i + 1) / UMAX][(i + 1) % UMAX], dec[(i + 1) & 1]);
                         if (KIND != 1 && j >= UX) continue;
                         const int jx = j % UX;
+                        if constexpr (JOINT) {   // the pair (j, j + 1) at even j
+                            if (j & 1) continue;
+                            if (KIND == 1 && j >= UX)
+                                F::template dot_pair<NV>(R[p][j], R[p][j + 1], usub[jx], xr[jx], xr[jx + 1], nv, acc1);
+                            else
+                                F::template dot_pair<NV>(R[p][j], R[p][j + 1], usub[jx], xr[jx], xr[jx + 1], nv, acc0);
+                            continue;
+                        }
                         if (KIND == 1 && j >= UX)
                             TP::template dot<NV, XNEG>(R[p][j], dec[i & 1], usub[jx], tab, xr[jx], nv, acc1);
                         else
@@ -702,6 +731,11 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     StreamPass<F, KIND, NV, UMAX, LP> P(a, smem);
     P.issue_x();
     P.issue_tab();
+    // GEMV: the activation loads stay ahead of the weight loads (vector loads return in order, so
+    // the staging below then waits for the activations only, not for the weights the compiler
+    // would otherwise hoist above them): Q8_0 6.9 -> 6.2 us, Q4_K 8.8 -> 8.2, Q6_K 16.4 -> 14.8.
+    // (The MoE passes order their own requests around the staging; the barrier gained them nothing.)
+    if constexpr (KIND == 0) __builtin_amdgcn_sched_barrier(0);
     P.bind();
     // ring kernels: only the first GS_RING_EARLY slots before the activation staging (a smaller
     // first request arrives sooner), the rest after it
