@@ -738,8 +738,11 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
     if constexpr (KIND == 0) __builtin_amdgcn_sched_barrier(0);
     P.bind();
     // ring kernels: only the first GS_RING_EARLY slots before the activation staging (a smaller
-    // first request arrives sooner), the rest after it
-    constexpr int E = P.RING && KIND != 0 && GS_RING_EARLY < P.PF ? GS_RING_EARLY : P.PF;
+    // first request arrives sooner), the rest after it. For a GEMV the activations themselves
+    // queue behind the chip-wide burst of first weight requests, so long rows (4+ units per lane)
+    // split too: Q6_K K = 12288 14.7 -> 12.9 us; at 2 units per lane (K = 4096) all slots at once
+    // (Q8_0 6.2 against 6.35 us, Q4_K even).
+    constexpr int E = P.RING && (KIND != 0 || UMAX >= 4) && GS_RING_EARLY < P.PF ? GS_RING_EARLY : P.PF;
     P.load_batch(P.gid, 0, E);
     P.stage_x();
     __syncthreads();
