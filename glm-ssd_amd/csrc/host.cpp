@@ -341,9 +341,11 @@ GS_EXPORT int gs_quant_q8_1(const float *x, void *q, int64_t n, void *s) {
 // =============================================================================================
 // GEMV (quants.cu:223-256)
 // =============================================================================================
+// nv_tail: vectors of the last blockIdx.y slice when it differs from B (the second group of a
+// 5..7-vector call)
 static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
                      float *y, int64_t y_stride, int B, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs,
-                     int64_t y_bs, void *s) {
+                     int64_t y_bs, void *s, int nv_tail = 0) {
     int qk, bb;
     if (!geometry(ty, qk, bb)) return hipErrorInvalidValue;
     if (K <= 0 || K % 8 != 0 || K % ggml_block_elems(ty) != 0 || K % 32 != 0) return hipErrorInvalidValue;
@@ -351,18 +353,12 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
     if (!check_w(W, row_stride) || (n_batch > 1 && (w_bs & 1))) return hipErrorInvalidValue;
     if (rows == 0) return 0;
     // more than 4 vectors whose units do not fit 8-vector registers (K > 2048): groups of 4 vectors
-    // over the whole K instead of K slices of 8 vectors (8 x 4096 Q8_0: 14 us against 28 us). Both
-    // groups of an 8-vector call run in one launch (blockIdx.y), reading the same weights at the
-    // same time.
-    if (B > 4 && n_batch == 1 && K > 64 * 32) {
-        if (B == 8)
-            return gemv_impl(ty, W, row_stride, K, rows, x, x_stride, y, y_stride, 4, accumulate, 2, 0, 4 * x_stride,
-                             4 * y_stride, s);
-        int e = gemv_impl(ty, W, row_stride, K, rows, x, x_stride, y, y_stride, 4, accumulate, 1, 0, 0, 0, s);
-        if (e) return e;
-        return gemv_impl(ty, W, row_stride, K, rows, x + 4 * x_stride, x_stride, y + 4 * y_stride, y_stride, B - 4,
-                         accumulate, 1, 0, 0, 0, s);
-    }
+    // over the whole K instead of K slices of 8 vectors (8 x 4096 Q8_0: 14 us against 28 us), both
+    // groups in one launch (blockIdx.y; the second holds B - 4 vectors), reading the same weights
+    // at the same time.
+    if (B > 4 && n_batch == 1 && K > 64 * 32)
+        return gemv_impl(ty, W, row_stride, K, rows, x, x_stride, y, y_stride, 4, accumulate, 2, 0, 4 * x_stride,
+                         4 * y_stride, s, B == 8 ? 0 : B - 4);
     // split K so one lane's q8_1 activation units fit in registers: K <= 64 lanes x (8/NV) units x 32
     const int NVt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
     const int kmax_units = 64 * (8 / NVt);
@@ -387,6 +383,7 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
         a.K = kk;
         a.rows = rows;
         a.nvec = B;
+        a.nv_tail = nv_tail;
         a.nseg = 1;
         a.accumulate = (k0 > 0) ? 1 : accumulate;
         a.x_aligned = xal && ((k0 * 4) % 16 == 0);

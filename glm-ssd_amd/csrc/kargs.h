@@ -34,6 +34,7 @@ struct StreamArgs {
     int K;                           // row length (elements)
     int rows;                        // rows per matrix
     int nvec;                        // activation vectors (B or tokens)
+    int nv_tail;                     // GEMV: vectors of the last blockIdx.y slice (0: nvec)
     int nseg;                        // segments (experts) in this launch
     int accumulate;                  // GEMV only: y += result
     float lim;                       // SwiGLU clamp (<= 0: none)

@@ -334,6 +334,7 @@ struct StreamPass {
         y += (int64_t)blockIdx.y * a.y_bs;
         sy = KIND != 0 ? (int)blockIdx.y * a.nseg : 0;
         K = a.K, nu = a.nu, nv = a.nvec, rows = a.rows;
+        if (KIND == 0 && a.nv_tail && blockIdx.y == gridDim.y - 1) nv = a.nv_tail;
         lpr = LP ? LP : a.lpr, lane = tid & (lpr - 1);
         tot = KIND == 2 ? a.nseg * nu : nu;          // units along the (concatenated) row
         // Lane groups: GATEUP pins each wave to one expert (its pointers are wave-uniform) and the

@@ -134,12 +134,16 @@ def _gemv_case(ty, rows, K, B, stream, seed, x_stride=None, accumulate=False, ro
         x[b * xs:b * xs + K] = rng.standard_normal(K).astype(np.float32)
     # float matrices take f32 activations (quants.cu:81-96), the quantized formats q8_1 ones
     want = O.gemv(ty, wbytes, rs, K, rows, x, B=B, x_stride=xs, act="f32" if ty in FLOAT else "q8_1")
-    y0 = rng.standard_normal(B * rows).astype(np.float32)
+    # three sentinel vectors after the B outputs: no launch (or vector group) writes past B
+    y0 = rng.standard_normal((B + 3) * rows).astype(np.float32)
     dw = G.DeviceBuffer.from_array(wbytes)
     dx = G.DeviceBuffer.from_array(x)
     dy = G.DeviceBuffer.from_array(y0)
     G.ops.gemv(ty, dw, rs, K, rows, dx, xs, dy, rows, B, accumulate, stream)
-    got = dy.download(np.float32, B * rows, stream).reshape(B, rows)
+    full = dy.download(np.float32, (B + 3) * rows, stream)
+    assert np.array_equal(full[B * rows:], y0[B * rows:]), "output written past vector B"
+    got = full[:B * rows].reshape(B, rows)
+    y0 = y0[:B * rows]
     if accumulate:
         got = got.astype(np.float64) - y0.reshape(B, rows)
     e = rel_l2(got, want)
