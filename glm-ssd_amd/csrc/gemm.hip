@@ -96,6 +96,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     const float *X = a.X + (int64_t)z * a.x_bs;
     float *Y = a.Y + (int64_t)z * a.y_bs;
     const int K = a.K, rows = a.rows, N = a.N, nsb = K / 256 + (K % 256 != 0);
+    // K slice (blockIdx.z): super-blocks [kb0, kb1)
+    const int ks = blockIdx.z, kb0 = ks * a.ksb, kb1 = min(nsb, kb0 + a.ksb);
     const int r0 = rblk * GM_RB, n0 = tblk * GM_TN;
     const int nrows = min(GM_RB, rows - r0), ntok = min(GM_TN, N - n0);
     const int64_t rs = a.row_stride;
@@ -189,10 +191,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         uint4 rv[NRAW];
         uint32_t rx[NRAW];
         float4 xv[NXA][2];
-        raw_load(0, rv, rx);
-        x_load(0, xv);
-        raw_store(0, 0, rv, rx);
-        x_store(0, 0, xv);
+        raw_load(kb0, rv, rx);
+        x_load(kb0, xv);
+        raw_store(0, kb0, rv, rx);
+        x_store(0, kb0, xv);
         if (tid < 2) gm_fill[tid] = tid == 0 ? GM_WV : 0u;   // buffer 0: step 0, stored by every wave
         __syncthreads();
     }
@@ -212,15 +214,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     };
 
     const int ntt = (ntok + 15) >> 4;   // token row blocks with any token (wave-uniform)
-    for (int b = 0; b < nsb; b++) {
-        const int buf = GM_NBUF == 2 ? b & 1 : 0;
-        const bool more = GM_NBUF == 2 && b + 1 < nsb;
+    for (int b = kb0; b < kb1; b++) {
+        const int bl = b - kb0;   // step within the slice (buffer parity, fill counts)
+        const int buf = GM_NBUF == 2 ? bl & 1 : 0;
+        const bool more = GM_NBUF == 2 && b + 1 < kb1;
         uint4 rv[NRAW];
         uint32_t rx[NRAW];
         float4 xv[NXA][2];
         if (GM_NBUF == 1) {
             // one buffer: the other workgroup on the CU computes while this one loads
-            if (b > 0) __syncthreads();   // every wave is done with step b-1
+            if (bl > 0) __syncthreads();   // every wave is done with step b-1
             raw_load(b, rv, rx);
             x_load(b, xv);
             raw_store(0, b, rv, rx);
@@ -231,7 +234,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
             // last step too, re-reading that step's data, so every wait on them is an exact count)
             raw_load(more ? b + 1 : b, rv, rx);
             x_load(more ? b + 1 : b, xv);
-            if (b > 0) wait_fill(b);
+            if (bl > 0) wait_fill(bl);
         }
         // B fragments: units 2q, 2q+1 of this lane's two rows, rounded to f16
         gh8 bf[GM_NR][2][4];
@@ -287,8 +290,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
                 for (int n = 0; n < GM_NR; n++) {
                     const int rr = wave * 16 * GM_NR + 16 * n + j;
                     if (rr < nrows) {
-                        float *dst = Y + (int64_t)(n0 + t) * a.y_stride + r0 + rr;
-                        *dst = a.accumulate ? *dst + acc[tt][n][i] : acc[tt][n][i];
+                        if (a.part) {   // K slice: its partial, summed in slice order by gs_k_gemm_reduce
+                            a.part[((int64_t)(ks * gridDim.y + z) * N + n0 + t) * rows + r0 + rr] = acc[tt][n][i];
+                        } else {
+                            float *dst = Y + (int64_t)(n0 + t) * a.y_stride + r0 + rr;
+                            *dst = a.accumulate ? *dst + acc[tt][n][i] : acc[tt][n][i];
+                        }
                     }
                 }
             }
@@ -300,3 +307,21 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         gemm_body<QKB, BB, DEC, gs_gemm_nbuf(TY)>(a);                                            \
     }
 GS_TYPE_LIST(GS_GEMM_KERNEL)
+
+// Y[z][n][r] (+)= sum over K slices s = 0, 1, ... of part[s][z][n][r], in slice order (a fixed
+// order: the result does not depend on which slice finished first)
+extern "C" __global__ void __launch_bounds__(256) gs_k_gemm_reduce(GemmReduceArgs a) {
+    const int64_t per = (int64_t)a.N * a.rows, total = per * a.n_batch;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        float v[GS_GEMM_KS_MAX];   // every slice's load issued before the first add
+#pragma unroll
+        for (int s = 0; s < GS_GEMM_KS_MAX; s++) v[s] = s < a.nks ? a.part[(int64_t)s * total + i] : 0.f;
+        float sum = v[0];
+#pragma unroll
+        for (int s = 1; s < GS_GEMM_KS_MAX; s++)
+            if (s < a.nks) sum += v[s];
+        const int64_t z = i / per, rem = i - z * per, n = rem / a.rows, r = rem - n * a.rows;
+        float *dst = a.Y + z * a.y_bs + n * a.y_stride + r;
+        *dst = a.accumulate ? *dst + sum : sum;
+    }
+}

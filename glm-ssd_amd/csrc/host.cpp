@@ -51,6 +51,10 @@ struct DeviceCtx {
     size_t max_lds = 0;
     hipError_t init_err = hipSuccess;
     std::map<std::pair<std::string, int>, int> occ;  // (kernel, lds) -> blocks per CU
+    hipMemPool_t pool = nullptr;  // stream-ordered scratch (K-split GEMM partials), made on first use
+    // per stream: its scratch buffer (calls on one stream run in order, so each reuses the last
+    // call's buffer; calls on different streams never share one)
+    std::map<hipStream_t, std::pair<void *, size_t>> scratch;
 };
 
 std::mutex g_mu;
@@ -599,8 +603,68 @@ GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows
     // row block r runs on XCD r % 8 (workgroup w -> XCD w % 8): 8 x ceil(n_rb / 8) x n_tb workgroups
     const int64_t nwg = (int64_t)8 * ((a.n_rb + 7) / 8) * a.n_tb;
     if (nwg > 0x7fffffff || n_batch > 65535) return hipErrorInvalidValue;
-    return launch("gs_k_gemm_" + std::to_string(ty), dim3((unsigned)nwg, n_batch, 1), dim3(GS_GEMM_THREADS, 1, 1), lds,
-                  (hipStream_t)s, a);
+    const int nsb = (K + 255) / 256;
+    a.ksb = nsb;
+    // Few tiles (small N, few row blocks): K splits into slices on blockIdx.z, each writing f32
+    // partials to stream-ordered scratch that gs_k_gemm_reduce sums in slice order into Y (a fixed
+    // order, so results are reproducible). The slices fill the CUs the tiles leave idle. Slices x
+    // tiles <= CUs and a tile is 128 x 64 outputs, so the scratch of a call is at most
+    // CUs x 32 KB (8 MB on MI355X); it is kept per stream for the next call.
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    const int64_t tiles = (int64_t)a.n_rb * a.n_tb * n_batch;
+    int nks = 1;
+    if (2 * tiles <= c->cu_count && nsb >= 2) {
+        // one super-block per slice where the CUs allow (IQ2_XXS 1536 x 4096, N = 64: 75 -> 16 us;
+        // two per slice: 19 us)
+        nks = (int)std::min<int64_t>(std::min(nsb, GS_GEMM_KS_MAX), c->cu_count / tiles);
+        a.ksb = (nsb + nks - 1) / nks;
+        nks = (nsb + a.ksb - 1) / a.ksb;
+    }
+    const std::string name = "gs_k_gemm_" + std::to_string(ty);
+    if (nks == 1)
+        return launch(name, dim3((unsigned)nwg, n_batch, 1), dim3(GS_GEMM_THREADS, 1, 1), lds, (hipStream_t)s, a);
+    if (!c->pool) {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!c->pool) {
+            int dev = 0;
+            if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+            hipMemPoolProps pp;
+            memset(&pp, 0, sizeof(pp));
+            pp.allocType = hipMemAllocationTypePinned;
+            pp.location.type = hipMemLocationTypeDevice;
+            pp.location.id = dev;
+            hipMemPool_t pool;
+            if ((e = hipMemPoolCreate(&pool, &pp)) != hipSuccess) return e;
+            uint64_t keep = UINT64_MAX;   // keep freed scratch for the next call instead of returning it
+            if ((e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep)) != hipSuccess) return e;
+            c->pool = pool;
+        }
+    }
+    const size_t part_bytes = (size_t)nks * n_batch * N * rows * sizeof(float);
+    void *part = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto &sc = c->scratch[(hipStream_t)s];
+        if (sc.second < part_bytes) {   // grow: the old buffer is released in stream order
+            if (sc.first && (e = hipFreeAsync(sc.first, (hipStream_t)s)) != hipSuccess) return e;
+            sc = {nullptr, 0};
+            const size_t want = std::max(part_bytes, (size_t)1 << 20);
+            if ((e = hipMallocFromPoolAsync(&sc.first, want, c->pool, (hipStream_t)s)) != hipSuccess) return e;
+            sc.second = want;
+        }
+        part = sc.first;
+    }
+    a.part = (float *)part;
+    e = launch(name, dim3((unsigned)nwg, n_batch, nks), dim3(GS_GEMM_THREADS, 1, 1), lds, (hipStream_t)s, a);
+    if (e == hipSuccess) {
+        GemmReduceArgs r{a.part, Y, y_stride, y_bs, rows, N, n_batch, nks, accumulate};
+        const int64_t total = (int64_t)n_batch * N * rows;
+        const unsigned g = (unsigned)std::min<int64_t>((total + 255) / 256, 4 * (int64_t)c->cu_count);
+        e = launch("gs_k_gemm_reduce", dim3(g), dim3(256), 0, (hipStream_t)s, r);
+    }
+    return e;
 }
 
 // =============================================================================================

@@ -125,4 +125,14 @@ struct GemmArgs {
     int64_t w_bs, x_bs, y_bs;   // per blockIdx.y (z) batch strides: bytes / floats / floats
     int K, rows, N, accumulate;
     int n_rb, n_tb;       // row blocks and token blocks of one problem
+    int ksb;              // super-blocks per K slice (blockIdx.z); every super-block when not split
+    float *part;          // K split: slice partials [slice][batch][N][rows] (null: write Y)
+};
+#define GS_GEMM_KS_MAX 16   // K slices of one gs_gemm call at most
+// sum of the K slices' partials in slice order into Y (+= when accumulate)
+struct GemmReduceArgs {
+    const float *part;
+    float *Y;
+    int64_t y_stride, y_bs;
+    int rows, N, n_batch, nks, accumulate;
 };

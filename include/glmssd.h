@@ -130,7 +130,10 @@ int gs_moe_ffn_tokens(int ty_gu, int ty_dn, const GsMoeBatch *b, int n_tok, int6
 int gs_swiglu(const float *g, const float *u, float *y, int64_t n, float lim, void *s);
 /* y += a*x (lib.rs:77; ops.cu:117-125) */
 int gs_axpy(float *y, const float *x, float a, int64_t n, void *s);
-/* Y[n*y_stride + m] (+)= W[m] . X[n*x_stride + :], n < N tokens; z-batched (lib.rs:115-118; gemm.cu:107-123) */
+/* Y[n*y_stride + m] (+)= W[m] . X[n*x_stride + :], n < N tokens; z-batched (lib.rs:115-118; gemm.cu:107-123).
+ * Problems with few 128-row x 64-token tiles split K across workgroups and add the slices in a
+ * fixed order (reproducible); their partials live in scratch taken from a library-owned
+ * stream-ordered pool, at most CUs x 32 KB per stream, kept for the stream's next call. */
 int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
             int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs, void *s);
 /* y[i][:] = x[idx[i]][:] (lib.rs:119; gemm.cu:125-138) */

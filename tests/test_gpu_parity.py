@@ -349,6 +349,30 @@ def test_gemm_every_type(ty, stream):
     assert e <= GEMM_REL
 
 
+def test_gemm_full_grid_and_k_split(stream):
+    # 17 row blocks x 8 token blocks = 136 tiles: one launch over the whole K; then few tiles (12
+    # row blocks, one token block): K split into 16 slices summed by the reduce pass, reproducible
+    # call to call and equal to the unsplit result within the f32 summation-order bound
+    e = _gemm_case(T.Q8_0, 512, 2176, 512, stream, 21)
+    say(f"gemm Q8_0 2176x512 N=512 (full grid): rel-L2 {e:.2e}")
+    assert e <= GEMM_REL
+    ty, K, rows, N = T.IQ2_XXS, 4096, 1536, 64
+    rb = G.row_bytes(ty, K)
+    raw = O.Rng(22).random_blocks(ty, rows * K)
+    X = np.random.default_rng(23).standard_normal((N, K)).astype(np.float32)
+    want = O.gemv(ty, raw, rb, K, rows, X, B=N, act="f16", nthreads=8)
+    dw, dx = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X)
+    outs = []
+    for _ in range(3):
+        dy = G.DeviceBuffer(N * rows * 4)
+        G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, stream)
+        outs.append(dy.download(np.float32, N * rows, stream))
+    e = rel_l2(outs[0].reshape(N, rows), want)
+    say(f"gemm IQ2_XXS 1536x4096 N=64 (K split): rel-L2 {e:.2e}")
+    assert e <= GEMM_REL
+    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
+
+
 def test_gemm_accumulate_strides_and_partial_superblock(stream):
     # Q8_0 with K = 800 (the last 256-element step is partial), strided X / Y, accumulate
     assert _gemm_case(T.Q8_0, 800, 129, 65, stream, 11, accumulate=True, x_stride=804, y_stride=133) <= GEMM_REL
