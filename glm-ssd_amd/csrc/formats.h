@@ -554,9 +554,56 @@ struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
         }
     }
 };
-using FF32 = FGeneric<GS_F32, 8, 32, exact::f32>;
-using FF16 = FGeneric<GS_F16, 8, 16, exact::f16>;
-using FBF16 = FGeneric<GS_BF16, 8, 16, exact::bf16>;
+// Plain float matrices (F32, F16, BF16: the router and other unquantized weights) with f32
+// activations (quants.cu:81-96). A unit's 32 weights are loaded into registers with the row's
+// other units (128 or 64 bytes, so they stream ahead of use like the quantized formats), widened
+// to f32 exactly, and dotted with the staged f32 activations read as float4 from LDS, in four
+// partial sums.
+template <int T, int BB_>
+struct FPlain : UnitGeom<8, BB_>, NoTable {
+    static constexpr int TYPE = T, QK = 8, BB = BB_, TAB = 0;
+    static constexpr bool F32X = true;
+    static constexpr int NW = T == GS_F32 ? 8 : 4;   // 16-byte words per unit
+    static constexpr int RAW = 4 * NW;
+    struct Raw { uint4 d[NW]; };
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int, Raw &w) {
+#pragma unroll
+        for (int k = 0; k < NW; k++) w.d[k] = m.u128(o + 16 * k);
+    }
+    __device__ static __forceinline__ float wf(const Raw &w, int i) {
+        const uint32_t word = (&w.d[0].x)[T == GS_F32 ? i : i >> 1];
+        if (T == GS_F32) return __builtin_bit_cast(float, word);
+        const uint32_t h = (i & 1) ? word >> 16 : word & 0xffffu;
+        return T == GS_BF16 ? __builtin_bit_cast(float, h << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    }
+    template <int NV, bool XNEG = false>
+    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = wf(w, i);
+#pragma unroll
+        for (int t = 0; t < NV; t++) {
+            if (t < nv) {
+                const float4 *xs = (const float4 *)x[t].xs;
+                float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float4 xv = xs[i];
+                    s4[0] += v[4 * i] * xv.x;
+                    s4[1] += v[4 * i + 1] * xv.y;
+                    s4[2] += v[4 * i + 2] * xv.z;
+                    s4[3] += v[4 * i + 3] * xv.w;
+                }
+                r[t] += x[t].D * ((s4[0] + s4[1]) + (s4[2] + s4[3]));
+            }
+        }
+    }
+};
+using FF32 = FPlain<GS_F32, 32>;
+using FF16 = FPlain<GS_F16, 16>;
+using FBF16 = FPlain<GS_BF16, 16>;
 using FQ2_K = FGeneric<GS_Q2_K, 256, 84, exact::q2_k>;
 using FQ3_K = FGeneric<GS_Q3_K, 256, 110, exact::q3_k>;
 using FQ5_K = FGeneric<GS_Q5_K, 256, 176, exact::q5_k>;
