@@ -195,9 +195,13 @@ def test_gemv_accumulate_and_strides(ty, stream):
 
 @pytest.mark.parametrize("ty", [T.Q6_K, T.Q8_0])
 def test_gemv_long_rows_split(ty, stream):
-    # K beyond one launch's register-resident activation (K > 16384 at B=1) takes the K-split path
+    # K beyond one launch's register-resident activation (K > 16384 at B=1) takes the K-split path;
+    # 2..4 vectors whose rows exceed the multi-vector kernels' reach but fit one vector's run as
+    # one single-vector slice per vector (strided, accumulating); past 16384 they split K too
     assert _gemv_case(ty, 64, 24576, 1, stream, 11) <= REL_L2
     assert _gemv_case(ty, 64, 12288, 4, stream, 12) <= REL_L2
+    assert _gemv_case(ty, 96, 8192, 3, stream, 13, accumulate=True, x_stride=8192 + 4) <= REL_L2
+    assert _gemv_case(ty, 64, 24576, 2, stream, 14) <= REL_L2
 
 
 @pytest.mark.parametrize("ty", [T.Q8_0, T.Q4_K, T.IQ2_XXS])
