@@ -521,15 +521,12 @@ struct FIQ3_XXS : UnitGeom<256, 98> {
     }
 };
 
-// Generic path for the remaining types: exact f32 decode of the unit straight from global
-// memory, f32 dot with the dequantized activations (D * q). Slower; used for the non-hot formats.
-//
-// The plain float formats (F32, F16, BF16 — the router and other unquantized matrices) take the
-// activations in f32, as the reference's GEMV does for every type (quants.cu:81-96): F32X.
+// Generic path for the remaining quantized types (Q2_K, Q3_K, Q5_K, IQ2_S, IQ4_XS): exact f32
+// decode of the unit straight from global memory, f32 dot with the dequantized activations
+// (D * q). Slower; used for the non-hot formats.
 template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float (&)[32])>
 struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
     static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0, RAW = 2;
-    static constexpr bool F32X = T == GS_F32 || T == GS_F16 || T == GS_BF16;
     struct Raw { const uint8_t *p; };
     template <class M>
     __device__ static __forceinline__ void load(const M &m, uint32_t o, int, Raw &w) { w.p = m.ptr(o); }
@@ -537,18 +534,13 @@ struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
     __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
                                                float (&r)[NV]) {
         float v[32];
-        DEQ(w.p, QK >= 32 ? j : 0, v);   // plain types: w.p is the unit's first element
+        DEQ(w.p, j, v);
 #pragma unroll
         for (int t = 0; t < NV; t++) {
             if (t < nv) {
                 float s = 0.f;
-                if (F32X) {
 #pragma unroll
-                    for (int i = 0; i < 32; i++) s += v[i] * x[t].xs[i];
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 32; i++) s += v[i] * (float)(int8_t)((x[t].q[i >> 2] >> (8 * (i & 3))) & 0xff);
-                }
+                for (int i = 0; i < 32; i++) s += v[i] * (float)(int8_t)((x[t].q[i >> 2] >> (8 * (i & 3))) & 0xff);
                 r[t] += x[t].D * s;
             }
         }
