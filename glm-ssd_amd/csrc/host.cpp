@@ -616,7 +616,7 @@ GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows
     // partials to stream-ordered scratch that gs_k_gemm_reduce sums in slice order into Y (a fixed
     // order, so results are reproducible). The slices fill the CUs the tiles leave idle. Slices x
     // tiles <= CUs and a tile is 128 x 64 outputs, so the scratch of a call is at most
-    // CUs x 32 KB (8 MB on MI355X); it is kept per stream for the next call.
+    // CUs x 32 KB (8 MB on MI355X); it is kept per stream for the next call (for up to 16 streams).
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
@@ -653,6 +653,13 @@ GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows
     void *part = nullptr;
     {
         std::lock_guard<std::mutex> lk(g_mu);
+        if (c->scratch.size() >= 16 && !c->scratch.count((hipStream_t)s)) {
+            // a 17th stream: release every kept buffer first (hipFree waits for the work using
+            // them), so programs that cycle through many streams do not accumulate scratch
+            for (auto &kv : c->scratch)
+                if (kv.second.first && (e = hipFree(kv.second.first)) != hipSuccess) return e;
+            c->scratch.clear();
+        }
         auto &sc = c->scratch[(hipStream_t)s];
         if (sc.second < part_bytes) {   // grow: the old buffer is released in stream order
             if (sc.first && (e = hipFreeAsync(sc.first, (hipStream_t)s)) != hipSuccess) return e;

@@ -377,6 +377,26 @@ def test_gemm_full_grid_and_k_split(stream):
     assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
 
 
+def test_gemm_k_split_many_streams():
+    # the split's scratch is kept per stream for up to 16 streams; an 18-stream cycle releases and
+    # re-creates it, and every call still returns the same bits
+    ty, K, rows, N = T.Q8_0, 2048, 256, 24
+    rb = G.row_bytes(ty, K)
+    raw = O.Rng(31).random_blocks(ty, rows * K)
+    X = np.random.default_rng(32).standard_normal((N, K)).astype(np.float32)
+    dw, dx = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X)
+    streams = [G.Stream() for _ in range(18)]
+    outs = []
+    for rep in range(2):
+        for st in streams:
+            dy = G.DeviceBuffer(N * rows * 4)
+            G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, st)
+            outs.append(dy.download(np.float32, N * rows, st))
+    want = O.gemv(ty, raw, rb, K, rows, X, B=N, act="f16", nthreads=8)
+    assert rel_l2(outs[0].reshape(N, rows), want) <= GEMM_REL
+    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
+
+
 def test_gemm_accumulate_strides_and_partial_superblock(stream):
     # Q8_0 with K = 800 (the last 256-element step is partial), strided X / Y, accumulate
     assert _gemm_case(T.Q8_0, 800, 129, 65, stream, 11, accumulate=True, x_stride=804, y_stride=133) <= GEMM_REL
