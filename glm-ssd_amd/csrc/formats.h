@@ -189,6 +189,77 @@ struct FQ4_K : UnitGeom<256, 144>, NoTable {
     }
 };
 
+// Q5_K (lib.rs:221-240): Q4_K's header (d, dmin, 12 bytes of 6-bit scales/mins) and nibbles,
+// plus a fifth bit per element: unit j takes nibble j & 1 of the 32 qs bytes at 48 + 32 (j >> 1)
+// and bit j of the 32 qh bytes at 16. Units 2i and 2i + 1 read the same 64 bytes, so a lane's
+// pair loads them once (load2: 10 registers per unit instead of 20).
+struct FQ5_K : UnitGeom<256, 176>, NoTable {
+    static constexpr int TYPE = GS_Q5_K, QK = 256, BB = 176, TAB = 0, RAW = 20, RAW2 = 10;
+    static constexpr bool PAIR = true, JOINT = true;
+    // single unit: a = qs bytes, b = qh bytes, h = header. Pair: w0.a = qs, w0.h = header, w1.a = qh.
+    struct Raw { uint4 a0, a1, b0, b1, h; };
+    __device__ static __forceinline__ int xunit(int up) { return up; }
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int j, Raw &w) {
+        const uint32_t qs = o + 48 + 32 * ((uint32_t)j >> 1);
+        w.h = m.u128(o);
+        w.a0 = m.u128(qs);
+        w.a1 = m.u128(qs + 16);
+        w.b0 = m.u128(o + 16);
+        w.b1 = m.u128(o + 32);
+    }
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int j, Raw &w0, Raw &w1) {
+        const uint32_t qs = o + 48 + 32 * ((uint32_t)j >> 1);
+        w0.h = m.u128(o);
+        w0.a0 = m.u128(qs);
+        w0.a1 = m.u128(qs + 16);
+        w1.a0 = m.u128(o + 16);
+        w1.a1 = m.u128(o + 32);
+    }
+    // unit j: 5-bit values from nibble j & 1 and qh bit j, scale and min from scale_min_k4 (as
+    // Q4_K); sum (d sc q - dmin m) x = d sc sum q x - dmin m sum x
+    template <int NV>
+    __device__ static __forceinline__ void dot_q(const uint4 &hd, const uint32_t (&ql)[8], const uint32_t (&qh)[8], int j,
+                                                 const XU (&x)[NV], int nv, float (&r)[NV]) {
+        const float d = h2f(hd.x & 0xffff), dmin = h2f(hd.x >> 16);
+        const uint32_t hs[3] = {hd.y, hd.z, hd.w};
+        auto sb = [&](int k) -> uint32_t { return (hs[k >> 2] >> (8 * (k & 3))) & 0xff; };
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = sb(j) & 63;
+            mn = sb(j + 4) & 63;
+        } else {
+            sc = (sb(j + 4) & 0xF) | ((sb(j - 4) >> 6) << 4);
+            mn = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
+        }
+        const int sh = (j & 1) * 4;
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = ((ql[i] >> sh) & 0x0F0F0F0Fu) | (((qh[i] >> j) & 0x01010101u) << 4);
+        const float ds = d * (float)sc, dm = dmin * (float)mn;
+#pragma unroll
+        for (int t = 0; t < NV; t++)
+            if (NV == 1 || t < nv) r[t] += x[t].D * (ds * (float)dot8(q, x[t].q) - dm * (float)(x[t].slo + x[t].shi));
+    }
+    template <int NV, bool XNEG = false>
+    __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const uint32_t ql[8] = {w.a0.x, w.a0.y, w.a0.z, w.a0.w, w.a1.x, w.a1.y, w.a1.z, w.a1.w};
+        const uint32_t qh[8] = {w.b0.x, w.b0.y, w.b0.z, w.b0.w, w.b1.x, w.b1.y, w.b1.z, w.b1.w};
+        dot_q<NV>(w.h, ql, qh, j, x, nv, r);
+    }
+    // the pair (j even, j + 1) loaded by load2, unit j then unit j + 1 (the order of two dot calls)
+    template <int NV>
+    __device__ static __forceinline__ void dot_pair(const Raw &w0, const Raw &w1, int j, const XU (&x0)[NV],
+                                                    const XU (&x1)[NV], int nv, float (&r)[NV]) {
+        const uint32_t ql[8] = {w0.a0.x, w0.a0.y, w0.a0.z, w0.a0.w, w0.a1.x, w0.a1.y, w0.a1.z, w0.a1.w};
+        const uint32_t qh[8] = {w1.a0.x, w1.a0.y, w1.a0.z, w1.a0.w, w1.a1.x, w1.a1.y, w1.a1.z, w1.a1.w};
+        dot_q<NV>(w0.h, ql, qh, j, x0, nv, r);
+        dot_q<NV>(w0.h, ql, qh, j + 1, x1, nv, r);
+    }
+};
+
 // Q6_K (lib.rs:243-262). A super-block's 32-element unit of quarter q in half h takes the low
 // (q < 2) or high (q >= 2) nibbles of the 32 ql bytes at 64h + 32(q & 1) and 2-bit fields 2q of
 // the 32 qh bytes at 128 + 32h, so quarters q and q + 2 of a half read the same 64 bytes. The
@@ -598,6 +669,5 @@ using FF16 = FPlain<GS_F16, 16>;
 using FBF16 = FPlain<GS_BF16, 16>;
 using FQ2_K = FGeneric<GS_Q2_K, 256, 84, exact::q2_k>;
 using FQ3_K = FGeneric<GS_Q3_K, 256, 110, exact::q3_k>;
-using FQ5_K = FGeneric<GS_Q5_K, 256, 176, exact::q5_k>;
 using FIQ2_S = FGeneric<GS_IQ2_S, 256, 82, exact::iq2_s>;
 using FIQ4_XS = FGeneric<GS_IQ4_XS, 256, 136, exact::iq4_xs>;
