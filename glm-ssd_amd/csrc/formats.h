@@ -260,6 +260,60 @@ struct FQ5_K : UnitGeom<256, 176>, NoTable {
     }
 };
 
+// IQ4_XS (lib.rs:331-343): per 32-element unit ib, 16 qs bytes at 8 + 16 ib whose low nibbles are
+// elements 0..15 and high nibbles elements 16..31, each an index into the 16 int8 values of
+// kvalues_iq4nl; the unit's 6-bit scale ls (4 bits from scales_l, 2 from scales_h) gives
+// d (ls - 32). The lookup runs in registers: two v_perm_b32 over the table's halves (entries
+// 0..7 and 8..15, selector = index & 7) and a bytewise select on index bit 3, four values per
+// three operations; the unit's sum of kvalue * q is one integer dot.
+struct FIQ4_XS : UnitGeom<256, 136>, NoTable {
+    static constexpr int TYPE = GS_IQ4_XS, QK = 256, BB = 136, TAB = 0, RAW = 6;
+    struct Raw { uint4 q; uint2 h; };   // the unit's 16 qs bytes; block bytes 0..7 (d, scales_h, scales_l)
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int j, Raw &w) {
+        w.h = m.u64(o);
+        w.q = m.u128(o + 8 + 16 * (uint32_t)j);
+    }
+    // units j, j+1 of one block (j even): the header once, their 32 qs bytes together
+    static constexpr bool PAIR = true;
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int j, Raw &w0, Raw &w1) {
+        w0.h = w1.h = m.u64(o);
+        w0.q = m.u128(o + 8 + 16 * (uint32_t)j);
+        w1.q = m.u128(o + 24 + 16 * (uint32_t)j);
+    }
+    __device__ static __forceinline__ uint32_t kv4(int i) {   // table entries 4i..4i+3 as bytes
+        return (uint32_t)(uint8_t)kvalues_iq4nl[4 * i] | ((uint32_t)(uint8_t)kvalues_iq4nl[4 * i + 1] << 8) |
+               ((uint32_t)(uint8_t)kvalues_iq4nl[4 * i + 2] << 16) | ((uint32_t)(uint8_t)kvalues_iq4nl[4 * i + 3] << 24);
+    }
+    // four nibble indices (one per byte, 0..15) -> their four int8 table values
+    __device__ static __forceinline__ uint32_t lut4(uint32_t n, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+        const uint32_t sel = n & 0x07070707u;
+        const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);   // entries 0..7
+        const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);   // entries 8..15
+        const uint32_t m = ((n >> 3) & 0x01010101u) * 0xffu;      // 0xff in the bytes with index bit 3
+        return (hi & m) | (lo & ~m);
+    }
+    template <int NV, bool XNEG = false>
+    __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const uint32_t t0 = kv4(0), t1 = kv4(1), t2 = kv4(2), t3 = kv4(3);
+        const uint32_t qw[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        uint32_t v[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            v[k] = lut4(qw[k] & 0x0F0F0F0Fu, t0, t1, t2, t3);
+            v[k + 4] = lut4((qw[k] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
+        }
+        const uint32_t sh = w.h.x >> 16, sl = w.h.y;
+        const int ls = (int)((sl >> (4 * j)) & 0xfu) | (int)(((sh >> (2 * j)) & 3u) << 4);
+        const float dl = h2f(w.h.x & 0xffff) * (float)(ls - 32);
+#pragma unroll
+        for (int t = 0; t < NV; t++)
+            if (NV == 1 || t < nv) r[t] += (dl * x[t].D) * (float)dot8(v, x[t].q);
+    }
+};
+
 // Q6_K (lib.rs:243-262). A super-block's 32-element unit of quarter q in half h takes the low
 // (q < 2) or high (q >= 2) nibbles of the 32 ql bytes at 64h + 32(q & 1) and 2-bit fields 2q of
 // the 32 qh bytes at 128 + 32h, so quarters q and q + 2 of a half read the same 64 bytes. The
@@ -670,4 +724,3 @@ using FBF16 = FPlain<GS_BF16, 16>;
 using FQ2_K = FGeneric<GS_Q2_K, 256, 84, exact::q2_k>;
 using FQ3_K = FGeneric<GS_Q3_K, 256, 110, exact::q3_k>;
 using FIQ2_S = FGeneric<GS_IQ2_S, 256, 82, exact::iq2_s>;
-using FIQ4_XS = FGeneric<GS_IQ4_XS, 256, 136, exact::iq4_xs>;
