@@ -314,6 +314,149 @@ struct FIQ4_XS : UnitGeom<256, 136>, NoTable {
     }
 };
 
+// Q2_K (lib.rs:139-160) and Q3_K (lib.rs:163-201): unit u = quarter j = u & 3 of the 128-element
+// half n = u >> 2 takes the 2-bit fields 2j of the 32 qs bytes of its half (Q2_K at 16 + 32 n,
+// Q3_K at 32 + 32 n); Q3_K adds bit 4n + j of the 32 hmask bytes (set: +0, clear: -4). Each
+// 16-element half of a unit has its own scale (Q2_K: a byte of 4-bit scale and min; Q3_K: a
+// 6-bit scale unpacked from 12 bytes). Units j and j + 1 of a half read the same bytes, so a
+// lane's pair loads them once. Sums: Q2_K d sc sum q x - dmin m sum x; Q3_K with
+// v = (q | h << 2) - 4: sum v x = sum (q | h << 2) x - 4 sum x.
+struct FQ2_K : UnitGeom<256, 84>, NoTable {
+    static constexpr int TYPE = GS_Q2_K, QK = 256, BB = 84, TAB = 0, RAW = 10, RAW2 = 5;
+    static constexpr bool PAIR = true, JOINT = true;
+    // a = the half's 32 qs bytes, s = scale bytes from 8n + 2j (the unit's two, or the pair's
+    // four), dd = d | dmin << 16
+    struct Raw { uint4 a0, a1; uint32_t s, dd; };
+    __device__ static __forceinline__ int xunit(int up) { return up; }
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int u, Raw &w) {
+        const uint32_t n = (uint32_t)u >> 2, j = (uint32_t)u & 3;
+        w.a0 = m.u128(o + 16 + 32 * n);
+        w.a1 = m.u128(o + 32 + 32 * n);
+        w.s = m.u16(o + 8 * n + 2 * j);
+        w.dd = m.u32(o + 80);
+    }
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int u, Raw &w0, Raw &) {
+        const uint32_t n = (uint32_t)u >> 2, j = (uint32_t)u & 3;
+        w0.a0 = m.u128(o + 16 + 32 * n);
+        w0.a1 = m.u128(o + 32 + 32 * n);
+        w0.s = m.u32(o + 8 * n + 2 * j);
+        w0.dd = m.u32(o + 80);
+    }
+    template <int NV>
+    __device__ static __forceinline__ void dot_q(const Raw &w, int j, uint32_t sc2, const XU (&x)[NV], int nv,
+                                                 float (&r)[NV]) {
+        const uint32_t qw[8] = {w.a0.x, w.a0.y, w.a0.z, w.a0.w, w.a1.x, w.a1.y, w.a1.z, w.a1.w};
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = (qw[i] >> (2 * j)) & 0x03030303u;
+        const float d = h2f(w.dd & 0xffff), dmin = h2f(w.dd >> 16);
+        const int s0 = (int)(sc2 & 0xf), m0 = (int)((sc2 >> 4) & 0xf), s1 = (int)((sc2 >> 8) & 0xf), m1 = (int)((sc2 >> 12) & 0xf);
+#pragma unroll
+        for (int t = 0; t < NV; t++) {
+            if (NV == 1 || t < nv) {
+                int lo = 0, hi = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) lo = __builtin_amdgcn_sdot4((int)q[i], (int)x[t].q[i], lo, false);
+#pragma unroll
+                for (int i = 4; i < 8; i++) hi = __builtin_amdgcn_sdot4((int)q[i], (int)x[t].q[i], hi, false);
+                r[t] += x[t].D * (d * (float)(s0 * lo + s1 * hi) - dmin * (float)(m0 * x[t].slo + m1 * x[t].shi));
+            }
+        }
+    }
+    template <int NV, bool XNEG = false>
+    __device__ static __forceinline__ void dot(const Raw &w, int u, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        dot_q<NV>(w, u & 3, w.s, x, nv, r);
+    }
+    template <int NV>
+    __device__ static __forceinline__ void dot_pair(const Raw &w0, const Raw &, int u, const XU (&x0)[NV],
+                                                    const XU (&x1)[NV], int nv, float (&r)[NV]) {
+        dot_q<NV>(w0, u & 3, w0.s & 0xffff, x0, nv, r);
+        dot_q<NV>(w0, (u & 3) + 1, w0.s >> 16, x1, nv, r);
+    }
+};
+
+struct FQ3_K : UnitGeom<256, 110>, NoTable {
+    static constexpr int TYPE = GS_Q3_K, QK = 256, BB = 110, TAB = 0, RAW = 20, RAW2 = 10;
+    static constexpr bool PAIR = true, JOINT = true;
+    // single unit: a = the half's 32 qs bytes, b = the 32 hmask bytes, sc = the 12 scale bytes,
+    // dd = d. Pair: w0.a = qs, w0.sc, w0.dd; w1.a = hmask.
+    struct Raw { uint4 a0, a1, b0, b1; uint32_t sc0, sc1, sc2, dd; };
+    __device__ static __forceinline__ int xunit(int up) { return up; }
+    template <class M>
+    __device__ static __forceinline__ void load_common(const M &m, uint32_t o, int u, Raw &w) {
+        const uint32_t n = (uint32_t)u >> 2;
+        w.a0 = m.u128(o + 32 + 32 * n);
+        w.a1 = m.u128(o + 48 + 32 * n);
+        const uint2 s01 = m.u64(o + 96);
+        w.sc0 = s01.x;
+        w.sc1 = s01.y;
+        w.sc2 = m.u32(o + 104);
+        w.dd = m.u16(o + 108);
+    }
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int u, Raw &w) {
+        load_common(m, o, u, w);
+        w.b0 = m.u128(o);
+        w.b1 = m.u128(o + 16);
+    }
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int u, Raw &w0, Raw &w1) {
+        load_common(m, o, u, w0);
+        w1.a0 = m.u128(o);
+        w1.a1 = m.u128(o + 16);
+    }
+    // 6-bit scale is (0..15) from the 12 raw bytes (lib.rs:166-179): low nibble of raw byte is & 7
+    // (the high nibble for is >= 8), bits 2 (is >> 2) of raw byte 8 + (is & 3) on top
+    // (selects, not a runtime array index: that would put the words in scratch memory)
+    __device__ static __forceinline__ int scale6(const Raw &w, int is) {
+        const int b = is & 7;
+        const uint32_t word = b >= 4 ? w.sc1 : w.sc0;
+        const uint32_t lo = (word >> (8 * (b & 3) + (is >= 8 ? 4 : 0))) & 0xfu;
+        const uint32_t hi = (w.sc2 >> (8 * (is & 3) + 2 * (is >> 2))) & 3u;
+        return (int)(lo | (hi << 4)) - 32;
+    }
+    template <int NV>
+    __device__ static __forceinline__ void dot_q(const uint32_t (&qw)[8], const uint32_t (&hw)[8], const Raw &ws, int u,
+                                                 const XU (&x)[NV], int nv, float (&r)[NV]) {
+        const int n = u >> 2, j = u & 3;
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            q[i] = ((qw[i] >> (2 * j)) & 0x03030303u) | (((hw[i] >> (4 * n + j)) & 0x01010101u) << 2);
+        const float d = h2f(ws.dd);
+        const int s0 = scale6(ws, 8 * n + 2 * j), s1 = scale6(ws, 8 * n + 2 * j + 1);
+#pragma unroll
+        for (int t = 0; t < NV; t++) {
+            if (NV == 1 || t < nv) {
+                int lo = 0, hi = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) lo = __builtin_amdgcn_sdot4((int)q[i], (int)x[t].q[i], lo, false);
+#pragma unroll
+                for (int i = 4; i < 8; i++) hi = __builtin_amdgcn_sdot4((int)q[i], (int)x[t].q[i], hi, false);
+                r[t] += (d * x[t].D) * (float)(s0 * (lo - 4 * x[t].slo) + s1 * (hi - 4 * x[t].shi));
+            }
+        }
+    }
+    template <int NV, bool XNEG = false>
+    __device__ static __forceinline__ void dot(const Raw &w, int u, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const uint32_t qw[8] = {w.a0.x, w.a0.y, w.a0.z, w.a0.w, w.a1.x, w.a1.y, w.a1.z, w.a1.w};
+        const uint32_t hw[8] = {w.b0.x, w.b0.y, w.b0.z, w.b0.w, w.b1.x, w.b1.y, w.b1.z, w.b1.w};
+        dot_q<NV>(qw, hw, w, u, x, nv, r);
+    }
+    template <int NV>
+    __device__ static __forceinline__ void dot_pair(const Raw &w0, const Raw &w1, int u, const XU (&x0)[NV],
+                                                    const XU (&x1)[NV], int nv, float (&r)[NV]) {
+        const uint32_t qw[8] = {w0.a0.x, w0.a0.y, w0.a0.z, w0.a0.w, w0.a1.x, w0.a1.y, w0.a1.z, w0.a1.w};
+        const uint32_t hw[8] = {w1.a0.x, w1.a0.y, w1.a0.z, w1.a0.w, w1.a1.x, w1.a1.y, w1.a1.z, w1.a1.w};
+        dot_q<NV>(qw, hw, w0, u, x0, nv, r);
+        dot_q<NV>(qw, hw, w0, u + 1, x1, nv, r);
+    }
+};
+
 // Q6_K (lib.rs:243-262). A super-block's 32-element unit of quarter q in half h takes the low
 // (q < 2) or high (q >= 2) nibbles of the 32 ql bytes at 64h + 32(q & 1) and 2-bit fields 2q of
 // the 32 qh bytes at 128 + 32h, so quarters q and q + 2 of a half read the same 64 bytes. The
@@ -721,6 +864,4 @@ struct FPlain : UnitGeom<8, BB_>, NoTable {
 using FF32 = FPlain<GS_F32, 32>;
 using FF16 = FPlain<GS_F16, 16>;
 using FBF16 = FPlain<GS_BF16, 16>;
-using FQ2_K = FGeneric<GS_Q2_K, 256, 84, exact::q2_k>;
-using FQ3_K = FGeneric<GS_Q3_K, 256, 110, exact::q3_k>;
 using FIQ2_S = FGeneric<GS_IQ2_S, 256, 82, exact::iq2_s>;
