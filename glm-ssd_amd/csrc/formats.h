@@ -713,6 +713,111 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
     }
 };
 
+// IQ2_S (lib.rs:291-309): unit u has 4 groups of 8; group l's grid index is qs byte 2 + 4u + l
+// plus bits 2l..2l+1 of qh byte 66 + u as bits 8..9 (1024-entry grid, 8 KiB in LDS), its signs
+// are the raw byte 34 + 4u + l (no parity bit), and the unit's scale byte 74 + u holds one 4-bit
+// scale per 16 elements: db = d (0.5 + s) / 4 = d (2s+1) / 8, the 1/8 folded into the activation
+// scale. The signs go on the activation side through v_perm_b32 selectors (a 256-entry table
+// indexed by the sign byte itself), as for IQ2_XXS.
+__shared__ uint2 gs_iq2s_grid_lds[1024];
+__shared__ uint2 gs_iq2s_sel_lds[256];
+
+// v_perm_b32 selectors for the 8 sign bits s: byte e selects q (e) or -q (e + 4)
+__device__ __forceinline__ uint2 sign_sel_raw(uint32_t s) {
+    uint32_t lo = 0x03020100u, hi = 0x03020100u;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        lo += ((s >> b) & 1u) << (8 * b + 2);
+        hi += ((s >> (b + 4)) & 1u) << (8 * b + 2);
+    }
+    return make_uint2(lo, hi);
+}
+
+struct FIQ2_S : UnitGeom<256, 82> {
+    static constexpr int TYPE = GS_IQ2_S, QK = 256, BB = 82, TAB = 0, RAW = 5;
+    static constexpr bool NEG_X = true;
+    static constexpr float XSCALE = 0.125f;
+    struct Raw { uint32_t a, sg, qh, sc, d; };   // index bytes, sign bytes, qh byte, scale byte, d
+    struct TabReg { uint64_t g0, g1; };
+    __device__ static __forceinline__ void tab_load(int tid, TabReg &r) {
+        r.g0 = tid < 1024 ? iq2s_grid[tid] : 0;
+        r.g1 = tid + 512 < 1024 ? iq2s_grid[tid + 512] : 0;
+    }
+    __device__ static __forceinline__ void tab_store(int tid, const TabReg &r) {
+        if (tid < 1024) gs_iq2s_grid_lds[tid] = make_uint2((uint32_t)r.g0, (uint32_t)(r.g0 >> 32));
+        if (tid + 512 < 1024) gs_iq2s_grid_lds[tid + 512] = make_uint2((uint32_t)r.g1, (uint32_t)(r.g1 >> 32));
+        if (tid < 256) gs_iq2s_sel_lds[tid] = sign_sel_raw((uint32_t)tid);
+    }
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int j, Raw &w) {
+        w.d = m.u16(o);
+        w.a = m.u32(o + 2 + 4 * (uint32_t)j);
+        w.sg = m.u32(o + 34 + 4 * (uint32_t)j);
+        w.qh = m.u16(o + 66 + (uint32_t)j);
+        w.sc = m.u16(o + 74 + (uint32_t)j);
+    }
+    // units j, j+1 of one block (j even): d once, both units' bytes in 8-byte and 2-byte reads
+    static constexpr bool PAIR = true;
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int j, Raw &w0, Raw &w1) {
+        w0.d = w1.d = m.u16(o);
+        const uint2 a = m.u64(o + 2 + 4 * (uint32_t)j), sg = m.u64(o + 34 + 4 * (uint32_t)j);
+        const uint32_t qh = m.u16(o + 66 + (uint32_t)j), sc = m.u16(o + 74 + (uint32_t)j);
+        w0.a = a.x, w1.a = a.y;
+        w0.sg = sg.x, w1.sg = sg.y;
+        w0.qh = qh, w1.qh = qh >> 8;   // the low byte is the unit's (only bits 0..7 are read)
+        w0.sc = sc, w1.sc = sc >> 8;
+    }
+    struct Dec { uint2 g[4], s[4]; };
+    template <int L>
+    __device__ static __forceinline__ uint32_t gofs(const Raw &w) {   // byte offset of group L's grid row
+        return grid_off<L>(w.a) | (((w.qh >> (2 * L)) & 3u) << 11);
+    }
+    __device__ static __forceinline__ void fetch(const Raw &w, Dec &e) {
+        const uint32_t go[4] = {gofs<0>(w), gofs<1>(w), gofs<2>(w), gofs<3>(w)};
+        const uint32_t so[4] = {grid_off<0>(w.sg), grid_off<1>(w.sg), grid_off<2>(w.sg), grid_off<3>(w.sg)};
+#pragma unroll
+        for (int l = 0; l < 4; l++) e.g[l] = *(const uint2 *)((const uint8_t *)gs_iq2s_grid_lds + go[l]);
+#pragma unroll
+        for (int l = 0; l < 4; l++) e.s[l] = *(const uint2 *)((const uint8_t *)gs_iq2s_sel_lds + so[l]);
+    }
+    template <int NV, bool XNEG = true>
+    __device__ static __forceinline__ void dot2(const Raw &w, const Dec &e, const XU (&x)[NV], int nv, float (&r)[NV]) {
+        uint2 g[4] = {e.g[0], e.g[1], e.g[2], e.g[3]};
+        if (!XNEG) {   // signs on the grid bytes (every grid byte is nonzero: 0x01010100 - g negates)
+#pragma unroll
+            for (int l = 0; l < 4; l++) {
+                g[l].x = __builtin_amdgcn_perm(0x01010100u - g[l].x, g[l].x, e.s[l].x);
+                g[l].y = __builtin_amdgcn_perm(0x01010100u - g[l].y, g[l].y, e.s[l].y);
+            }
+        }
+        const int m0 = 2 * (int)(w.sc & 0xfu) + 1, m1 = 2 * (int)((w.sc >> 4) & 0xfu) + 1;
+        const float dh = h2f(w.d);
+#pragma unroll
+        for (int t = 0; t < NV; t++) {
+            if (NV == 1 || t < nv) {
+                int acc[2] = {0, 0};
+#pragma unroll
+                for (int l = 0; l < 4; l++) {
+                    const uint32_t q0 = XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l], x[t].q[2 * l], e.s[l].x) : x[t].q[2 * l];
+                    const uint32_t q1 =
+                        XNEG ? __builtin_amdgcn_perm(x[t].nq[2 * l + 1], x[t].q[2 * l + 1], e.s[l].y) : x[t].q[2 * l + 1];
+                    acc[l >> 1] = __builtin_amdgcn_sdot4((int)g[l].x, (int)q0, acc[l >> 1], false);
+                    acc[l >> 1] = __builtin_amdgcn_sdot4((int)g[l].y, (int)q1, acc[l >> 1], false);
+                }
+                r[t] += (dh * x[t].D) * (float)(acc[0] * m0 + acc[1] * m1);
+            }
+        }
+    }
+    template <int NV, bool XNEG = true>
+    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        Dec e;
+        fetch(w, e);
+        dot2<NV, XNEG>(w, e, x, nv, r);
+    }
+};
+
 // IQ3_XXS: a unit is 8 grid indices (one byte each, 4 values per entry) and one 32-bit word of
 // four 7-bit sign indices plus the 4-bit scale (lib.rs:312-328). The 256-entry grid (1 KiB) sits
 // in LDS next to the IQ2_XXS sign selectors (shared: both formats use ksigns), and the signs go on
@@ -789,31 +894,6 @@ struct FIQ3_XXS : UnitGeom<256, 98> {
     }
 };
 
-// Generic path for the remaining quantized types (Q2_K, Q3_K, Q5_K, IQ2_S, IQ4_XS): exact f32
-// decode of the unit straight from global memory, f32 dot with the dequantized activations
-// (D * q). Slower; used for the non-hot formats.
-template <int T, int QK_, int BB_, void (*DEQ)(const uint8_t *, int, float (&)[32])>
-struct FGeneric : UnitGeom<QK_, BB_>, NoTable {
-    static constexpr int TYPE = T, QK = QK_, BB = BB_, TAB = 0, RAW = 2;
-    struct Raw { const uint8_t *p; };
-    template <class M>
-    __device__ static __forceinline__ void load(const M &m, uint32_t o, int, Raw &w) { w.p = m.ptr(o); }
-    template <int NV, bool XNEG = false>
-    __device__ static __forceinline__ void dot(const Raw &w, int j, const uint8_t *, const XU (&x)[NV], int nv,
-                                               float (&r)[NV]) {
-        float v[32];
-        DEQ(w.p, j, v);
-#pragma unroll
-        for (int t = 0; t < NV; t++) {
-            if (t < nv) {
-                float s = 0.f;
-#pragma unroll
-                for (int i = 0; i < 32; i++) s += v[i] * (float)(int8_t)((x[t].q[i >> 2] >> (8 * (i & 3))) & 0xff);
-                r[t] += x[t].D * s;
-            }
-        }
-    }
-};
 // Plain float matrices (F32, F16, BF16: the router and other unquantized weights) with f32
 // activations (quants.cu:81-96). A unit's 32 weights are loaded into registers with the row's
 // other units (128 or 64 bytes, so they stream ahead of use like the quantized formats), widened
@@ -864,4 +944,3 @@ struct FPlain : UnitGeom<8, BB_>, NoTable {
 using FF32 = FPlain<GS_F32, 32>;
 using FF16 = FPlain<GS_F16, 16>;
 using FBF16 = FPlain<GS_BF16, 16>;
-using FIQ2_S = FGeneric<GS_IQ2_S, 256, 82, exact::iq2_s>;
