@@ -39,17 +39,33 @@ CASES = [(T.IQ2_XXS, T.IQ2_XXS, 1, 8, 4096, 1536, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 1
          # (validate.rs:376-386), one decode token and a 2-token MTP step
          (T.IQ2_XXS, T.IQ3_XXS, 1, 8, 4096, 2048, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 2, 8, 4096, 2048, 0.0),
          # down with more rows than one batch per wave (n_embd 8192: the down row ring)
-         (T.IQ2_XXS, T.IQ2_XXS, 1, 4, 8192, 512, 0.0)]
+         (T.IQ2_XXS, T.IQ2_XXS, 1, 4, 8192, 512, 0.0),
+         # the other streaming formats through gate/up and down (paired units split between gate
+         # and up; one and two tokens)
+         (T.Q2_K, T.Q3_K, 1, 3, 1024, 512, 0.0), (T.Q3_K, T.Q2_K, 2, 2, 1024, 512, 5.0),
+         (T.IQ4_XS, T.IQ2_S, 1, 3, 1024, 768, 0.0), (T.IQ2_S, T.IQ4_XS, 2, 2, 2048, 512, 0.0),
+         (T.F16, T.BF16, 1, 2, 1024, 512, 0.0)]
+
+
+def _weights(rng, nrng, ty, n_elems):
+    """Random blocks of a quantized type; for the float types finite values (random 16-bit words
+    hold NaN/Inf), scaled like a trained matrix's."""
+    if ty == T.F16:
+        return (0.05 * nrng.standard_normal(n_elems)).astype(np.float16).view(np.uint8)
+    if ty == T.BF16:
+        v = (0.05 * nrng.standard_normal(n_elems)).astype(np.float32).view(np.uint32)
+        return (v >> 16).astype(np.uint16).view(np.uint8)
+    return rng.random_blocks(ty, n_elems)
 
 
 @pytest.mark.parametrize("ty_gu,ty_dn,nt,n,n_embd,n_ff,lim", CASES)
 def test_moe_ffn(ty_gu, ty_dn, nt, n, n_embd, n_ff, lim, stream):
     say(f"moe_ffn {G.TYPE_NAMES[ty_gu]}/{G.TYPE_NAMES[ty_dn]} nt={nt} n={n} {n_embd}x{n_ff} lim={lim}")
     rng = O.Rng(777 + 31 * ty_gu + ty_dn + n)
-    gate = [rng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(n)]
-    up = [rng.random_blocks(ty_gu, n_ff * n_embd) for _ in range(n)]
-    down = [rng.random_blocks(ty_dn, n_embd * n_ff) for _ in range(n)]
     nrng = np.random.default_rng(n_embd + n)
+    gate = [_weights(rng, nrng, ty_gu, n_ff * n_embd) for _ in range(n)]
+    up = [_weights(rng, nrng, ty_gu, n_ff * n_embd) for _ in range(n)]
+    down = [_weights(rng, nrng, ty_dn, n_embd * n_ff) for _ in range(n)]
     x = nrng.standard_normal((nt, n_embd)).astype(np.float32)
     w = nrng.random((nt, n)).astype(np.float32)
     if n > 1:
@@ -59,7 +75,11 @@ def test_moe_ffn(ty_gu, ty_dn, nt, n, n_embd, n_ff, lim, stream):
         for e in range(n):
             pt.append(t); pe.append(e); pw.append(w[t, e])
     rbg, rbd = G.row_bytes(ty_gu, n_embd), G.row_bytes(ty_dn, n_ff)
-    want = O.moe_ffn(ty_gu, ty_dn, gate, up, down, rbg, rbd, n_embd, n_ff, x, pt, pe, pw, lim=lim, nthreads=8)
+    # the float formats keep f32 activations; the quantized ones quantize them to q8_1
+    flt = (T.F32, T.F16, T.BF16)
+    assert (ty_gu in flt) == (ty_dn in flt)
+    want = O.moe_ffn(ty_gu, ty_dn, gate, up, down, rbg, rbd, n_embd, n_ff, x, pt, pe, pw, lim=lim, nthreads=8,
+                     act="f32" if ty_gu in flt else "q8_1")
     bufs = [G.DeviceBuffer.from_array(a) for a in gate + up + down]
     b = G.MoeBatch()
     b.n = n
