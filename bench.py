@@ -10,7 +10,13 @@ Also reported (secondary): config 1 (Q8_0 GEMV), config 3 (Q4_K / Q6_K GEMV), we
 rotated over > 512 MB. The CPU baseline is the oracle's C port of the reference CPU path
 (crates/quants dequantize + f64 dot, crates/engine/src/qtest.rs:77-108) on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps 500] [--warmup 50] [--no-cpu] [--calib]
+Each timed loop runs its W warm-up steps and then more, untimed, until at least --ramp-ms
+(default 100) of GPU time has passed: after the host has spent seconds generating a workload's
+data the GPU's clocks need tens of milliseconds of load to come back up (config 2: 17.9 us per step
+after 50 warm-up steps, 16.7 us once 85 ms of steps have run). Then exactly K steps are timed,
+continuing the weight rotation.
+
+Usage: python bench.py [--gpus 1] [--steps 500] [--warmup 50] [--ramp-ms 100] [--no-cpu] [--calib]
 """
 import argparse
 import ctypes as C
@@ -62,6 +68,8 @@ def bench_lib():
     L.bn_read.argtypes = [P, C.c_int, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_gemm.argtypes = [C.c_int, P, C.c_int, I64, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P,
                           C.POINTER(C.c_float)]
+    L.bn_set_ramp_ms.argtypes = [C.c_float]
+    L.bn_set_ramp_ms.restype = None
     L.bn_moe_grouped.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, P, P, P, P, C.c_int, I64, C.c_int, C.c_int, I64, P, P,
                                  P, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     return L
@@ -363,6 +371,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--ramp-ms", type=float, default=100.0,
+                    help="minimum GPU time of each timed loop's warm-up (the W steps, then more until this much "
+                         "GPU time has passed): the clocks come back up from idle over tens of milliseconds")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--calib", action="store_true", help="also run a 1 GiB d2d copy (HBM counter calibration)")
@@ -373,6 +384,7 @@ def main():
         sys.exit(2)
     import glmssd as G
     L = bench_lib()
+    L.bn_set_ramp_ms(args.ramp_ms)
     s = G.Stream()
     info = G.device_info(0)
     log(f"device: {info.name.decode()} CUs={info.sm_count}")
@@ -453,6 +465,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_gpu_ms": args.ramp_ms,
         "ms_per_step": round(res["ms_step"], 6),
         "higher_is_better": True,
         "scaling": "weak",

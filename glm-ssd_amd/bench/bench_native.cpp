@@ -24,7 +24,38 @@ struct Timer {
         if (b) gs_event_destroy(b);
     }
 };
+
+// Minimum GPU time of warm-up before a timed loop (bn_set_ramp_ms). After an idle stretch (the host
+// generating a workload's data) the GPU's clocks need tens of milliseconds of load to come back
+// up, far longer than a few dozen warm-up steps of a few microseconds: config 2 times 17.9 us per
+// step after 50 warm-up steps against 16.7 us once 85 ms of steps have run.
+float g_ramp_ms = 100.0f;
+
+// The `warmup` steps step(0 .. warmup-1), then more (in chunks, with a GPU-time check between
+// chunks) until at least g_ramp_ms of GPU time has passed; *done = steps run, so the timed steps
+// continue the rotation and none of them re-reads data a warm-up step just left in the caches.
+template <class F>
+int warm(F &&step, int warmup, void *s, int *done) {
+    Timer t;
+    CK(t.init());
+    CK(gs_stream_sync(s));
+    CK(gs_event_record(t.a, s));
+    int i = 0;
+    for (; i < warmup; i++) CK(step(i));
+    while (g_ramp_ms > 0.0f) {
+        CK(gs_event_record(t.b, s));
+        CK(gs_event_sync(t.b));
+        float ms = 0.0f;
+        CK(gs_event_elapsed_ms(&ms, t.a, t.b));
+        if (ms >= g_ramp_ms) break;
+        for (int j = 0; j < 32; j++, i++) CK(step(i));
+    }
+    *done = i;
+    return gs_stream_sync(s);
+}
 }  // namespace
+
+BN_EXPORT void bn_set_ramp_ms(float ms) { g_ramp_ms = ms; }
 
 // Decode step = gs_moe_gateup + gs_moe_down over batch (i % nb). ms_step: mean per step;
 // ms_gateup: mean of a separate loop of gs_moe_gateup alone (dominant kernel).
@@ -33,15 +64,16 @@ BN_EXPORT int bn_moe_decode(int ty_gu, int ty_dn, const GsMoeBatch *batches, int
                             void *s, float *ms_step, float *ms_gateup) {
     Timer t;
     CK(t.init());
-    for (int i = 0; i < warmup; i++) {
+    auto step = [&](int i) {
         const GsMoeBatch *b = &batches[i % nb];
         CK(gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, 0.0f, s));
-        CK(gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y, s));
-    }
-    CK(gs_stream_sync(s));
+        return gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y, s);
+    };
+    int w0 = 0;
+    CK(warm(step, warmup, s, &w0));
     CK(gs_event_record(t.a, s));
     for (int i = 0; i < steps; i++) {
-        const GsMoeBatch *b = &batches[(warmup + i) % nb];
+        const GsMoeBatch *b = &batches[(w0 + i) % nb];
         CK(gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, 0.0f, s));
         CK(gs_moe_down(ty_dn, b, nt, rs_dn, n_ff, n_embd, h, y, s));
     }
@@ -52,7 +84,7 @@ BN_EXPORT int bn_moe_decode(int ty_gu, int ty_dn, const GsMoeBatch *batches, int
     CK(gs_stream_sync(s));
     CK(gs_event_record(t.a, s));
     for (int i = 0; i < steps; i++) {
-        const GsMoeBatch *b = &batches[i % nb];
+        const GsMoeBatch *b = &batches[(w0 + steps + i) % nb];
         CK(gs_moe_gateup(ty_gu, b, nt, rs_gu, n_embd, n_ff, x, h, 0.0f, s));
     }
     CK(gs_event_record(t.b, s));
@@ -68,12 +100,13 @@ BN_EXPORT int bn_moe_ffn(int ty_gu, int ty_dn, const GsMoeBatch *batches, int nb
                          float *ms_step) {
     Timer t;
     CK(t.init());
-    for (int i = 0; i < warmup; i++)
-        CK(gs_moe_ffn(ty_gu, ty_dn, &batches[i % nb], nt, rs_gu, n_embd, n_ff, rs_dn, x, h, y, 0.0f, s));
-    CK(gs_stream_sync(s));
+    auto step = [&](int i) {
+        return gs_moe_ffn(ty_gu, ty_dn, &batches[i % nb], nt, rs_gu, n_embd, n_ff, rs_dn, x, h, y, 0.0f, s);
+    };
+    int w0 = 0;
+    CK(warm(step, warmup, s, &w0));
     CK(gs_event_record(t.a, s));
-    for (int i = 0; i < steps; i++)
-        CK(gs_moe_ffn(ty_gu, ty_dn, &batches[(warmup + i) % nb], nt, rs_gu, n_embd, n_ff, rs_dn, x, h, y, 0.0f, s));
+    for (int i = 0; i < steps; i++) CK(step(w0 + i));
     CK(gs_event_record(t.b, s));
     CK(gs_event_sync(t.b));
     CK(gs_event_elapsed_ms(ms_step, t.a, t.b));
@@ -88,14 +121,14 @@ BN_EXPORT int bn_moe_ffn_tokens(int ty_gu, int ty_dn, const GsMoeBatch *batches,
                                 int warmup, void *s, float *ms_step) {
     Timer t;
     CK(t.init());
-    for (int i = 0; i < warmup; i++)
-        CK(gs_moe_ffn_tokens(ty_gu, ty_dn, &batches[(i % nr) * n_tok], n_tok, rs_gu, n_embd, n_ff, rs_dn, x, h, y,
-                             0.0f, s));
-    CK(gs_stream_sync(s));
+    auto step = [&](int i) {
+        return gs_moe_ffn_tokens(ty_gu, ty_dn, &batches[(i % nr) * n_tok], n_tok, rs_gu, n_embd, n_ff, rs_dn, x, h, y,
+                                 0.0f, s);
+    };
+    int w0 = 0;
+    CK(warm(step, warmup, s, &w0));
     CK(gs_event_record(t.a, s));
-    for (int i = 0; i < steps; i++)
-        CK(gs_moe_ffn_tokens(ty_gu, ty_dn, &batches[((warmup + i) % nr) * n_tok], n_tok, rs_gu, n_embd, n_ff, rs_dn, x,
-                             h, y, 0.0f, s));
+    for (int i = 0; i < steps; i++) CK(step(w0 + i));
     CK(gs_event_record(t.b, s));
     CK(gs_event_sync(t.b));
     CK(gs_event_elapsed_ms(ms_step, t.a, t.b));
@@ -108,10 +141,11 @@ BN_EXPORT int bn_gemv(int ty, const void *const *Ws, int nw, int64_t rs, int K, 
                       int B, int steps, int warmup, void *s, float *ms) {
     Timer t;
     CK(t.init());
-    for (int i = 0; i < warmup; i++) CK(gs_gemv(ty, Ws[i % nw], rs, K, rows, x, K, y, rows, B, 0, s));
-    CK(gs_stream_sync(s));
+    auto step = [&](int i) { return gs_gemv(ty, Ws[i % nw], rs, K, rows, x, K, y, rows, B, 0, s); };
+    int w0 = 0;
+    CK(warm(step, warmup, s, &w0));
     CK(gs_event_record(t.a, s));
-    for (int i = 0; i < steps; i++) CK(gs_gemv(ty, Ws[i % nw], rs, K, rows, x, K, y, rows, B, 0, s));
+    for (int i = 0; i < steps; i++) CK(step(w0 + i));
     CK(gs_event_record(t.b, s));
     CK(gs_event_sync(t.b));
     CK(gs_event_elapsed_ms(ms, t.a, t.b));
@@ -133,10 +167,10 @@ BN_EXPORT int bn_moe_grouped(int ty_gu, int ty_dn, const GsExpertPtrs *experts, 
         return gs_moe_grouped(ty_gu, ty_dn, experts, n_exp, offs[r], idx[r], w[r], n_pairs[r], n_tok, rs_gu, n_embd, n_ff,
                               rs_dn, x, y, 0.0f, work, work_bytes, s);
     };
-    for (int i = 0; i < warmup; i++) CK(call(i));
-    CK(gs_stream_sync(s));
+    int w0 = 0;
+    CK(warm(call, warmup, s, &w0));
     CK(gs_event_record(t.a, s));
-    for (int i = 0; i < steps; i++) CK(call(warmup + i));
+    for (int i = 0; i < steps; i++) CK(call(w0 + i));
     CK(gs_event_record(t.b, s));
     CK(gs_event_sync(t.b));
     CK(gs_event_elapsed_ms(ms, t.a, t.b));
@@ -192,10 +226,10 @@ BN_EXPORT int bn_read(const void *const *bases, int nb, size_t bytes, int steps,
     };
     Timer t;
     CK(t.init());
-    for (int i = 0; i < warmup; i++) CK(call(i));
-    CK(gs_stream_sync(s));
+    int w0 = 0;
+    CK(warm(call, warmup, s, &w0));
     CK(gs_event_record(t.a, s));
-    for (int i = 0; i < steps; i++) CK(call(warmup + i));
+    for (int i = 0; i < steps; i++) CK(call(w0 + i));
     CK(gs_event_record(t.b, s));
     CK(gs_event_sync(t.b));
     CK(gs_event_elapsed_ms(ms, t.a, t.b));
@@ -208,10 +242,11 @@ BN_EXPORT int bn_gemm(int ty, const void *const *Ws, int nw, int64_t rs, int K, 
                       int N, int steps, int warmup, void *s, float *ms) {
     Timer t;
     CK(t.init());
-    for (int i = 0; i < warmup; i++) CK(gs_gemm(ty, Ws[i % nw], rs, K, rows, X, K, Y, rows, N, 0, 1, 0, 0, 0, s));
-    CK(gs_stream_sync(s));
+    auto step = [&](int i) { return gs_gemm(ty, Ws[i % nw], rs, K, rows, X, K, Y, rows, N, 0, 1, 0, 0, 0, s); };
+    int w0 = 0;
+    CK(warm(step, warmup, s, &w0));
     CK(gs_event_record(t.a, s));
-    for (int i = 0; i < steps; i++) CK(gs_gemm(ty, Ws[i % nw], rs, K, rows, X, K, Y, rows, N, 0, 1, 0, 0, 0, s));
+    for (int i = 0; i < steps; i++) CK(step(w0 + i));
     CK(gs_event_record(t.b, s));
     CK(gs_event_sync(t.b));
     CK(gs_event_elapsed_ms(ms, t.a, t.b));
