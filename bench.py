@@ -229,10 +229,12 @@ def run_moe_per_token(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
                 calls_per_step=n_tok, routings_rotated=n_rout)
 
 
-def run_read_ceiling(L, s, sizes, steps, warmup, min_pool=768 << 20):
+def run_read_ceiling(L, s, sizes, steps, warmup, ramp_ms, min_pool=768 << 20):
     """Plain HBM read (bench_kernels.hip bn_k_read) of each byte count, the start address rotated
     over a pool of at least 768 MB so no call is served from the last-level cache: the achievable
-    ceiling the streaming kernels are compared with at the same byte count."""
+    ceiling the streaming kernels are compared with at the same byte count. The warm-up floor
+    applies before the first size only (the sizes follow each other with no idle time between
+    them), so every later size is exactly `warmup` + `steps` launches."""
     import glmssd as G
     sizes = [(n + 4095) // 4096 * 4096 for n in sizes]
     pool_bytes = max(min_pool, max(sizes))
@@ -245,9 +247,11 @@ def run_read_ceiling(L, s, sizes, steps, warmup, min_pool=768 << 20):
         assert all(o + n <= pool_bytes for o in offs)   # every read stays inside the pool
         bases = (C.c_void_p * nb)(*[pool.p.value + o for o in offs])
         ms = C.c_float()
+        L.bn_set_ramp_ms(ramp_ms if n == sizes[0] else 0.0)
         G.check(L.bn_read(C.cast(bases, C.c_void_p), nb, n, steps, warmup, s.raw(), C.byref(ms)))
         out[str(n)] = {"bytes": n, "us": round(ms.value * 1e3, 2), "GB/s": round(n / (ms.value * 1e-3) / 1e9, 1),
                        "rotated_bases": nb}
+    L.bn_set_ramp_ms(ramp_ms)
     return out
 
 
@@ -439,7 +443,7 @@ def main():
             secondary[name] = r
             log(f"{name}: {r}")
         rc = run_read_ceiling(L, s, [17825792, 25952256, 28311552, 38928384, 41287680, 1 << 30], args.steps,
-                              args.warmup)
+                              args.warmup, args.ramp_ms)
         secondary["plain_read_ceiling"] = rc
         log(f"plain-read ceiling: {rc}")
         for name, r in [("config1_q8_0_gemv_4096x4096", r1), ("config3_q4_k_gemv_k4096_rows12288", r3a),
