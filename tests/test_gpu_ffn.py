@@ -44,7 +44,9 @@ CASES = [(T.IQ2_XXS, T.IQ2_XXS, 1, 8, 4096, 1536, 0.0), (T.IQ2_XXS, T.IQ3_XXS, 1
          # and up; one and two tokens)
          (T.Q2_K, T.Q3_K, 1, 3, 1024, 512, 0.0), (T.Q3_K, T.Q2_K, 2, 2, 1024, 512, 5.0),
          (T.IQ4_XS, T.IQ2_S, 1, 3, 1024, 768, 0.0), (T.IQ2_S, T.IQ4_XS, 2, 2, 2048, 512, 0.0),
-         (T.F16, T.BF16, 1, 2, 1024, 512, 0.0)]
+         (T.F16, T.BF16, 1, 2, 1024, 512, 0.0),
+         # one token over 12 experts at n_ff 2048: the down pass as two launches (8 + 4 experts)
+         (T.IQ2_XXS, T.IQ2_XXS, 1, 12, 2048, 2048, 0.0)]
 
 
 def _weights(rng, nrng, ty, n_elems):
