@@ -7,8 +7,8 @@
 // with lib.rs's f32 operation order; FP contraction is off for the whole file, so no multiply and
 // add are fused (Q2_K / Q4_K / Q5_K subtract the min after the scaled product, as lib.rs does).
 //
-// Used by gs_dequant_f32 / gs_dequant_f16 (one thread per unit) and by the generic matmul path
-// of the formats without a fast integer decode.
+// Used by gs_dequant_f32 / gs_dequant_f16 (one thread per unit) and by gs_gemm's tiles (each
+// lane decodes its own units from the raw super-blocks staged in LDS, then rounds them to f16).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
