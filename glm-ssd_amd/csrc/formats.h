@@ -2,12 +2,14 @@
 //
 // Two families:
 //   * exact::* (exact.h): exact dequantization of one 32-element unit, bit-identical to the CPU
-//               reference (crates/quants/src/lib.rs:131-343). Used by gs_dequant_* and by the
-//               generic matmul path.
-//   * F*::load/dot : the fast integer paths for Q8_0 / Q4_K / Q6_K / IQ2_XXS. load() fetches one
+//               reference (crates/quants/src/lib.rs:131-343). Used by gs_dequant_* and by
+//               gs_gemm's tiles.
+//   * F*::load/dot : the streaming kernels' paths, one per format (F32, F16, BF16, Q8_0, Q2_K,
+//               Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_S, IQ3_XXS, IQ4_XS). load() fetches one
 //               32-element "unit" of a weight row straight from HBM into registers; dot() decodes it
-//               and dots it with up to NV q8_1 activation units held in registers (v_dot4_i32_i8),
-//               applying the block scales in f32.
+//               and dots it with up to NV activation units held in registers (q8_1 with
+//               v_dot4_i32_i8 for the quantized formats, f32 for the plain ones), applying the
+//               block scales in f32.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
