@@ -1,5 +1,8 @@
-// gfx950 kernels of the quantized-matmul hot path. Compiled to one code object
-// (hipcc --genco --offload-arch=gfx950) that host.cpp loads with hipModuleLoadData; every
+// gfx950 kernels of the quantized-matmul hot path. Compiled (hipcc --genco --offload-arch=gfx950)
+// into one code object per weight format (GS_STREAM_F / GS_STREAM_ID select that format's
+// streaming kernels) and one with the format-independent kernels (GS_COMMON: quantization,
+// dequantization, gather/scatter, SwiGLU, axpy, f16 conversion); host.cpp loads them all with
+// hipModuleLoadData. Every
 // kernel is extern "C" with a fixed name and takes one argument block from kargs.h by value.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -789,7 +792,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
 #define GS_STREAM_ALL(F, NAME) GS_STREAM_MV(F, NAME, 0) GS_STREAM_GU(F, NAME) GS_STREAM_MV(F, NAME, 2) GS_STREAM_W(F, NAME)
 
 // One code object per format keeps the build parallel: the Makefile compiles this file once
-// per GS_STREAM_TYPE (F-struct, type id) and once with GS_COMMON for the kernels below.
+// per format (GS_STREAM_F: the F-struct, GS_STREAM_ID: its type id) and once with GS_COMMON for
+// the kernels below.
 #if defined(GS_STREAM_F)
 GS_STREAM_ALL(GS_STREAM_F, GS_STREAM_ID)
 #endif
