@@ -2,8 +2,8 @@
 // into one code object per weight format (GS_STREAM_F / GS_STREAM_ID select that format's
 // streaming kernels) and one with the format-independent kernels (GS_COMMON: quantization,
 // dequantization, gather/scatter, SwiGLU, axpy, f16 conversion); host.cpp loads them all with
-// hipModuleLoadData. Every
-// kernel is extern "C" with a fixed name and takes one argument block from kargs.h by value.
+// hipModuleLoadData. Every kernel is extern "C" with a fixed name and takes one argument block
+// from kargs.h by value.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "kargs.h"
