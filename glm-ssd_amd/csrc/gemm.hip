@@ -45,6 +45,10 @@ template <bool B> struct BoolC { static constexpr bool value = B; };
 // gm_fill[s] waves so far
 __shared__ uint32_t gm_fill[2];
 
+// Sticky expiry flag of this code object's bounded LDS waits (host.cpp gs_wait_status reads and
+// clears it): nonzero once any wait gave up before its count arrived.
+__device__ uint32_t gs_wait_expired;
+
 // 8 floats -> 8 halves (round to nearest even, as __floats2half2_rn)
 // (a vector conversion: v_cvt_pk_f16_f32, two values per instruction, round to nearest even)
 typedef float gf8 __attribute__((ext_vector_type(8)));
@@ -202,15 +206,22 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     // every wave has stored its share of it (the buffer's fill count reaches GM_WV (b / 2 + 1));
     // each wave stores step b + 1 at the end of step b and then counts the fill. A wave reading
     // step b thus knows every wave has finished computing step b - 1, the last reader of the
-    // buffer it overwrites next. The wait is bounded (2^16 polls; it keeps a lost fill from
-    // hanging the GPU).
+    // buffer it overwrites next. The count is read relaxed and followed by an acquire fence on
+    // LDS at workgroup scope (the storing wave's release fence precedes its increment). The wait
+    // is bounded (a.wait_limit polls, 2^16 by default; it keeps a lost fill from hanging the GPU)
+    // and an expiry sets gs_wait_expired; a.wait_force (the host's test hook) makes the count
+    // unreachable so the wait runs to its limit.
     auto wait_fill = [&](int b) __attribute__((always_inline)) {
-        const uint32_t want = (uint32_t)GM_WV * (uint32_t)(b / 2 + 1);
-        for (int spin = 0; spin < (1 << 16); spin++) {
+        const uint32_t want = (uint32_t)GM_WV * (uint32_t)(b / 2 + 1) + (a.wait_force ? 0x40000000u : 0u);
+        for (uint32_t spin = 0;; spin++) {
             if (__hip_atomic_load(&gm_fill[b & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) break;
+            if (spin >= a.wait_limit) {
+                if (lane == 0) __hip_atomic_fetch_or(&gs_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
-        asm volatile("" ::: "memory");   // no LDS read moves above the wait
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
 
     const int ntt = (ntok + 15) >> 4;   // token row blocks with any token (wave-uniform)
@@ -274,7 +285,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         if (more) {
             raw_store(buf ^ 1, b + 1, rv, rx);
             x_store(buf ^ 1, b + 1, xv);
-            asm volatile("" ::: "memory");   // counted after this wave's stores (LDS keeps a wave's order)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");   // this wave's stores, then the count
             if (lane == 0) __hip_atomic_fetch_add(&gm_fill[buf ^ 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }

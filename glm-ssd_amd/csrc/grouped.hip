@@ -57,6 +57,11 @@ struct GrpMeta {
 };
 static_assert(sizeof(GrpMeta) <= GS_GRP_META_BYTES, "bookkeeping fits its LDS share");
 
+// Sticky expiry flag of this code object's bounded LDS waits (host.cpp gs_wait_status reads and
+// clears it): nonzero once any wait gave up before its count arrived, i.e. some output of a
+// launch since the last clear may be wrong.
+__device__ uint32_t gs_wait_expired;
+
 template <int TY, int NTH>
 __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
     // thread -> (grid index g, 8 of the 16 scales): one table read per thread, issued up front
@@ -343,6 +348,9 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     }
     if (tid < 4) M.cnt[tid] = tid < 2 ? NTH / 64 : 0u;   // slots 0, 1: positions 0, 1, stored by every wave
     if (tid < 2) M.ep_seq[tid] = 0xffffffffu;
+    // token slots hold a valid token id (0) before the first publication, so an epilogue that
+    // ran past an expired wait still addresses rows of y
+    if (tid < 128) (&M.ep_tok[0][0])[tid] = 0;
     __syncthreads();
 
     // Epilogue operands of the current tile (per token slot: token id, combine weight, activation
@@ -380,24 +388,30 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     // most two positions apart, and the slot a wave overwrites at the end of P (last read at
     // P - 2) is no longer read by anyone. The epilogue operands of tile T are published with T's
     // sequence number (per tile parity) and awaited before the epilogue. Every wait is bounded:
-    // it gives up after 2^16 polls (no configuration comes near; it keeps a lost fill from
-    // hanging the GPU).
+    // it gives up after a.wait_limit polls (2^16 by default; no configuration comes near; it
+    // keeps a lost fill from hanging the GPU) and then sets gs_wait_expired.
     int b = 0, buf = 0, tpar = 0;
     uint32_t pos = 0, tseq = 0;
-    auto wait_count = [&](const uint32_t *c, uint32_t want) __attribute__((always_inline)) {
-        for (int spin = 0; spin < (1 << 16); spin++) {
-            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= want) break;
+    // The count (or sequence number) is read relaxed and followed by an acquire fence on LDS at
+    // workgroup scope; the writer's release fence on LDS precedes its increment (store), so a
+    // wave that sees the count also sees the stores it counts. a.wait_force (set only by the
+    // host's test hook) makes the target unreachable, so every wait runs to its limit.
+    const uint32_t wlim = a.wait_limit, wadd = a.wait_force ? 0x40000000u : 0u;
+    auto wait_lds = [&](const uint32_t *c, uint32_t want, bool eq) __attribute__((always_inline)) {
+        want += wadd;
+        for (uint32_t spin = 0;; spin++) {
+            const uint32_t v = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (eq ? v == want : v >= want) break;
+            if (spin >= wlim) {   // expired: recorded, and the wave goes on (never hangs)
+                if (lane == 0) __hip_atomic_fetch_or(&gs_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
-        asm volatile("" ::: "memory");   // no LDS read moves above the wait
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
-    auto wait_seq = [&](const uint32_t *c, uint32_t want) __attribute__((always_inline)) {
-        for (int spin = 0; spin < (1 << 16); spin++) {
-            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == want) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
-        asm volatile("" ::: "memory");
-    };
+    auto wait_count = [&](const uint32_t *c, uint32_t want) __attribute__((always_inline)) { wait_lds(c, want, false); };
+    auto wait_seq = [&](const uint32_t *c, uint32_t want) __attribute__((always_inline)) { wait_lds(c, want, true); };
     auto wait_slot = [&]() __attribute__((always_inline)) {
         if (pos > 1) wait_count(&M.cnt[buf], (uint32_t)(NTH / 64) * (pos / 4u + 1u));
     };
@@ -514,7 +528,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             M.ep_tok[tpar][tid] = ep_tok;
             M.ep_w[tpar][tid] = ep_w;
             M.ep_sc[tpar][tid] = ep_sc;
-            asm volatile("" ::: "memory");   // published after wave 0's stores (LDS keeps a wave's order)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");   // wave 0's stores, then the sequence number
             if (tid == 0) __hip_atomic_store(&M.ep_seq[tpar], tseq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         if (!have1) return false;
@@ -525,7 +539,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
 #pragma unroll
             for (int k = 0; k < NLD; k++)
                 if (NCH % NTH == 0 || tid + NTH * k < NCH) *(u4 *)(stage + sbuf * SLAB + dst[k]) = stg[k];
-            asm volatile("" ::: "memory");   // the fill is counted after this wave's stores (LDS keeps a wave's order)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");   // this wave's stores, then the count
             if (lane == 0) __hip_atomic_fetch_add(&M.cnt[sbuf], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         buf = (buf + 1) & 3;

@@ -51,14 +51,14 @@ struct DeviceCtx {
     size_t max_lds = 0;
     hipError_t init_err = hipSuccess;
     std::map<std::pair<std::string, int>, int> occ;  // (kernel, lds) -> blocks per CU
-    hipMemPool_t pool = nullptr;  // stream-ordered scratch (K-split GEMM partials), made on first use
-    // per stream: its scratch buffer (calls on one stream run in order, so each reuses the last
-    // call's buffer; calls on different streams never share one)
-    std::map<hipStream_t, std::pair<void *, size_t>> scratch;
+    std::vector<void *> wait_flags;   // gs_wait_expired of each code object that has one
 };
 
 std::mutex g_mu;
 std::map<int, DeviceCtx *> g_ctx;
+// poll bound of the MFMA kernels' LDS fill waits, and the test hook that makes them expire
+std::atomic<uint32_t> g_wait_limit{1u << 16};
+std::atomic<uint32_t> g_wait_force{0};
 
 DeviceCtx *ctx(hipError_t *err) {
     int dev = 0;
@@ -91,6 +91,12 @@ DeviceCtx *ctx(hipError_t *err) {
             e = hipModuleLoadData(&m, (const void *)b.p);
             if (e != hipSuccess) break;
             c->mods.push_back(m);
+            hipDeviceptr_t fp = nullptr;
+            size_t fsz = 0;
+            if (hipModuleGetGlobal(&fp, &fsz, m, "gs_wait_expired") == hipSuccess && fsz == 4)
+                c->wait_flags.push_back((void *)fp);
+            else
+                (void)hipGetLastError();   // code objects without bounded waits
         }
     }
     c->init_err = e;
@@ -236,6 +242,25 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     return launch(name, dim3(grid, n_batch, 1), dim3(GS_WG, 1, 1), P.lds, s, a);
 }
 
+// Row-length-independent kernels (kernels.hip gs_k_any_<kind>_<type>): one wave per row, for the
+// shapes the streaming kernels' register plan does not hold; blockIdx.y = GEMV batch or expert.
+hipError_t stream_any(int kind, int ty, const StreamArgs &a, int ny, hipStream_t s) {
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    const int grid = std::max(1, std::min((a.rows + 3) / 4, 8 * c->cu_count / std::max(1, ny)));
+    return launch("gs_k_any_" + std::to_string(kind) + "_" + std::to_string(ty), dim3(grid, ny, 1), dim3(256, 1, 1), 0, s, a);
+}
+
+// whether one streaming launch can hold the plan for these arguments (kind 1 or 2)
+bool stream_fits(int kind, int ty, StreamArgs a) {
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return true;   // the launch itself reports the error
+    StreamPlan P;
+    return plan_stream(c, kind, ty, a, P) == hipSuccess;
+}
+
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 int check_w(const void *W, int64_t row_stride) { return ((uintptr_t)W & 1) == 0 && (row_stride & 1) == 0; }
@@ -352,10 +377,29 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
                      int64_t y_bs, void *s, int nv_tail = 0) {
     int qk, bb;
     if (!geometry(ty, qk, bb)) return hipErrorInvalidValue;
-    if (K <= 0 || K % 8 != 0 || K % ggml_block_elems(ty) != 0 || K % 32 != 0) return hipErrorInvalidValue;
-    if (B < 1 || B > 8 || rows < 0 || n_batch < 1) return hipErrorInvalidValue;
+    if (K <= 0 || K % 8 != 0 || K % ggml_block_elems(ty) != 0) return hipErrorInvalidValue;
+    if (B < 1 || B > 8 || rows < 0 || n_batch < 1 || n_batch > 65535) return hipErrorInvalidValue;
     if (!check_w(W, row_stride) || (n_batch > 1 && (w_bs & 1))) return hipErrorInvalidValue;
     if (rows == 0) return 0;
+    if (K % 32 != 0) {   // plain types only (quantized blocks are multiples of 32): 8-element rows
+        StreamArgs a;
+        memset(&a, 0, sizeof(a));
+        a.w0[0] = (const uint8_t *)W;
+        a.x = x;
+        a.y = y;
+        a.row_stride = row_stride;
+        a.x_stride = x_stride;
+        a.y_stride = y_stride;
+        a.w_bs = w_bs;
+        a.x_bs = x_bs;
+        a.y_bs = y_bs;
+        a.K = K;
+        a.rows = rows;
+        a.nvec = B;
+        a.nseg = 1;
+        a.accumulate = accumulate;
+        return stream_any(0, ty, a, n_batch, (hipStream_t)s);
+    }
     // more than 4 vectors whose units do not fit 8-vector registers (K > 2048): groups of 4 vectors
     // over the whole K instead of K slices of 8 vectors (8 x 4096 Q8_0: 14 us against 28 us), both
     // groups in one launch (blockIdx.y; the second holds B - 4 vectors), reading the same weights
@@ -420,7 +464,7 @@ GS_EXPORT int gs_gemv_batched(int ty, const void *W, int64_t row_stride, int K, 
 static int moe_check(int ty, const GsMoeBatch *b, int nt, int K, int rows, int64_t row_stride) {
     int qk, bb;
     if (!b || b->n <= 0 || b->n > GS_MOE_MAX || nt < 1 || nt > GS_MOE_NT) return hipErrorInvalidValue;
-    if (K <= 0 || rows <= 0 || K % 8 != 0 || K % 32 != 0) return hipErrorInvalidValue;
+    if (K <= 0 || rows <= 0 || K % 8 != 0) return hipErrorInvalidValue;
     if (!geometry(ty, qk, bb) || K % ggml_block_elems(ty) != 0 || (row_stride & 1)) return hipErrorInvalidValue;
     return 0;
 }
@@ -487,6 +531,9 @@ GS_EXPORT int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_str
     if (rc) return rc;
     StreamArgs a;
     if ((rc = gateup_args(a, b, nt, row_stride, K, rows, x, h, lim))) return rc;
+    // rows longer than the lanes' register plan holds, or plain rows of 8-element multiples: the
+    // row-length-independent kernel, one blockIdx.y slice per expert
+    if (K % 32 != 0 || !stream_fits(1, ty, a)) return stream_any(1, ty, a, b->n, (hipStream_t)s);
     return stream(1, ty, a, (hipStream_t)s);
 }
 
@@ -495,6 +542,13 @@ GS_EXPORT int gs_moe_down(int ty, const GsMoeBatch *b, int nt, int64_t row_strid
     int rc = moe_check(ty, b, nt, K, rows, row_stride);
     if (rc) return rc;
     const int per = down_per_launch(nt, K);
+    StreamArgs a1;
+    if ((rc = down_args(a1, b, 0, 1, nt, row_stride, K, rows, h, y))) return rc;
+    if (K % 32 != 0 || !stream_fits(2, ty, a1)) {   // one expert's row exceeds the register plan
+        StreamArgs a;
+        if ((rc = down_args(a, b, 0, b->n, nt, row_stride, K, rows, h, y))) return rc;
+        return stream_any(2, ty, a, 1, (hipStream_t)s);
+    }
     for (int e0 = 0; e0 < b->n; e0 += per) {
         const int n = std::min(per, b->n - e0);
         StreamArgs a;
@@ -545,6 +599,18 @@ GS_EXPORT int gs_moe_ffn_tokens(int ty_gu, int ty_dn, const GsMoeBatch *b, int n
     if (n_tok * n > GS_SEG_MAX) return hipErrorInvalidValue;
     StreamArgs a, at;
     int rc;
+    {   // shapes outside the streaming plan: the per-token FFN (the same arithmetic)
+        StreamArgs g, d;
+        if ((rc = gateup_args(g, &b[0], 1, rs_gu, n_embd, n_ff, x, h, lim))) return rc;
+        if ((rc = down_args(d, &b[0], 0, 1, 1, rs_dn, n_ff, n_embd, h, y))) return rc;
+        if (n_embd % 32 != 0 || n_ff % 32 != 0 || !stream_fits(1, ty_gu, g) || !stream_fits(2, ty_dn, d)) {
+            for (int t = 0; t < n_tok; t++)
+                if ((rc = gs_moe_ffn(ty_gu, ty_dn, &b[t], 1, rs_gu, n_embd, n_ff, rs_dn, x + (int64_t)t * n_embd,
+                                     h + (int64_t)t * n * n_ff, y + (int64_t)t * n_embd, lim, s)))
+                    return rc;
+            return 0;
+        }
+    }
     for (int t = 0; t < n_tok; t++) {
         if ((rc = gateup_args(at, &b[t], 1, rs_gu, n_embd, n_ff, x, h, lim))) return rc;
         if (t == 0) a = at;
@@ -573,9 +639,27 @@ GS_EXPORT int gs_moe_ffn_tokens(int ty_gu, int ty_dn, const GsMoeBatch *b, int n
 // =============================================================================================
 // GEMM (gemm.cu:107-123): MFMA tiles of 128 weight rows x 64 tokens (gemm.hip)
 // =============================================================================================
-GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride,
-                      float *Y, int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs,
-                      int64_t y_bs, void *s) {
+namespace {
+// K slices of a gs_gemm problem: small grids (at most half as many 128 x 64 tiles as CUs) split K
+// over blockIdx.z so the slices fill the idle CUs; 1 = no split.
+int gemm_slices(DeviceCtx *c, int K, int rows, int N, int n_batch, int *ksb) {
+    const int nsb = (K + 255) / 256;
+    const int64_t tiles = (int64_t)((rows + 127) / 128) * ((N + 63) / 64) * n_batch;
+    *ksb = nsb;
+    if (!(2 * tiles <= c->cu_count && nsb >= 2)) return 1;
+    // one super-block per slice where the CUs allow (IQ2_XXS 1536 x 4096, N = 64: 75 -> 16 us;
+    // two per slice: 19 us)
+    int nks = (int)std::min<int64_t>(std::min(nsb, GS_GEMM_KS_MAX), c->cu_count / tiles);
+    *ksb = (nsb + nks - 1) / nks;
+    return (nsb + *ksb - 1) / *ksb;
+}
+size_t gemm_part_bytes(int nks, int rows, int N, int n_batch) {
+    return nks > 1 ? (size_t)nks * n_batch * N * rows * sizeof(float) : 0;
+}
+
+int gemm_impl(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
+              int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs,
+              void *work, size_t work_bytes, void *s) {
     if (K <= 0 || K % 32 != 0 || N < 1 || n_batch < 1 || x_stride % 4 != 0 || rows < 0) return hipErrorInvalidValue;
     int qk, bb;
     if (!geometry(ty, qk, bb) || K % ggml_block_elems(ty) != 0) return hipErrorInvalidValue;
@@ -605,72 +689,28 @@ GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows
     a.rows = rows;
     a.N = N;
     a.accumulate = accumulate;
+    a.wait_limit = g_wait_limit.load();
+    a.wait_force = g_wait_force.load();
     a.n_rb = (rows + 127) / 128;
     a.n_tb = (N + 63) / 64;
     // row block r runs on XCD r % 8 (workgroup w -> XCD w % 8): 8 x ceil(n_rb / 8) x n_tb workgroups
     const int64_t nwg = (int64_t)8 * ((a.n_rb + 7) / 8) * a.n_tb;
     if (nwg > 0x7fffffff || n_batch > 65535) return hipErrorInvalidValue;
-    const int nsb = (K + 255) / 256;
-    a.ksb = nsb;
-    // Few tiles (small N, few row blocks): K splits into slices on blockIdx.z, each writing f32
-    // partials to stream-ordered scratch that gs_k_gemm_reduce sums in slice order into Y (a fixed
-    // order, so results are reproducible). The slices fill the CUs the tiles leave idle. Slices x
-    // tiles <= CUs and a tile is 128 x 64 outputs, so the scratch of a call is at most
-    // CUs x 32 KB (8 MB on MI355X); it is kept per stream for the next call (for up to 16 streams).
+    a.ksb = (K + 255) / 256;
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
-    const int64_t tiles = (int64_t)a.n_rb * a.n_tb * n_batch;
-    int nks = 1;
-    if (2 * tiles <= c->cu_count && nsb >= 2) {
-        // one super-block per slice where the CUs allow (IQ2_XXS 1536 x 4096, N = 64: 75 -> 16 us;
-        // two per slice: 19 us)
-        nks = (int)std::min<int64_t>(std::min(nsb, GS_GEMM_KS_MAX), c->cu_count / tiles);
-        a.ksb = (nsb + nks - 1) / nks;
-        nks = (nsb + a.ksb - 1) / a.ksb;
-    }
     const std::string name = "gs_k_gemm_" + std::to_string(ty);
+    // K split only into the caller's workspace: each slice writes its f32 partial tile there and
+    // gs_k_gemm_reduce sums the slices in slice order into Y (a fixed order, so the result is
+    // reproducible). Without a workspace the whole K runs in one tile pass.
+    int ksb = 0;
+    const int nks = work ? gemm_slices(c, K, rows, N, n_batch, &ksb) : 1;
     if (nks == 1)
         return launch(name, dim3((unsigned)nwg, n_batch, 1), dim3(GS_GEMM_THREADS, 1, 1), lds, (hipStream_t)s, a);
-    if (!c->pool) {
-        std::lock_guard<std::mutex> lk(g_mu);
-        if (!c->pool) {
-            int dev = 0;
-            if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
-            hipMemPoolProps pp;
-            memset(&pp, 0, sizeof(pp));
-            pp.allocType = hipMemAllocationTypePinned;
-            pp.location.type = hipMemLocationTypeDevice;
-            pp.location.id = dev;
-            hipMemPool_t pool;
-            if ((e = hipMemPoolCreate(&pool, &pp)) != hipSuccess) return e;
-            uint64_t keep = UINT64_MAX;   // keep freed scratch for the next call instead of returning it
-            if ((e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep)) != hipSuccess) return e;
-            c->pool = pool;
-        }
-    }
-    const size_t part_bytes = (size_t)nks * n_batch * N * rows * sizeof(float);
-    void *part = nullptr;
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        if (c->scratch.size() >= 16 && !c->scratch.count((hipStream_t)s)) {
-            // a 17th stream: release every kept buffer first (hipFree waits for the work using
-            // them), so programs that cycle through many streams do not accumulate scratch
-            for (auto &kv : c->scratch)
-                if (kv.second.first && (e = hipFree(kv.second.first)) != hipSuccess) return e;
-            c->scratch.clear();
-        }
-        auto &sc = c->scratch[(hipStream_t)s];
-        if (sc.second < part_bytes) {   // grow: the old buffer is released in stream order
-            if (sc.first && (e = hipFreeAsync(sc.first, (hipStream_t)s)) != hipSuccess) return e;
-            sc = {nullptr, 0};
-            const size_t want = std::max(part_bytes, (size_t)1 << 20);
-            if ((e = hipMallocFromPoolAsync(&sc.first, want, c->pool, (hipStream_t)s)) != hipSuccess) return e;
-            sc.second = want;
-        }
-        part = sc.first;
-    }
-    a.part = (float *)part;
+    if (work_bytes < gemm_part_bytes(nks, rows, N, n_batch) || !aligned16(work)) return hipErrorInvalidValue;
+    a.ksb = ksb;
+    a.part = (float *)work;
     e = launch(name, dim3((unsigned)nwg, n_batch, nks), dim3(GS_GEMM_THREADS, 1, 1), lds, (hipStream_t)s, a);
     if (e == hipSuccess) {
         GemmReduceArgs r{a.part, Y, y_stride, y_bs, rows, N, n_batch, nks, accumulate};
@@ -679,6 +719,31 @@ GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows
         e = launch("gs_k_gemm_reduce", dim3(g), dim3(256), 0, (hipStream_t)s, r);
     }
     return e;
+}
+}  // namespace
+
+GS_EXPORT int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride,
+                      float *Y, int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs,
+                      int64_t y_bs, void *s) {
+    return gemm_impl(ty, W, row_stride, K, rows, X, x_stride, Y, y_stride, N, accumulate, n_batch, w_bs, x_bs, y_bs,
+                     nullptr, 0, s);
+}
+
+GS_EXPORT int gs_gemm_workspace(int K, int rows, int N, int n_batch, size_t *bytes) {
+    if (!bytes || K <= 0 || rows < 0 || N < 1 || n_batch < 1) return hipErrorInvalidValue;
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    int ksb = 0;
+    *bytes = rows == 0 ? 0 : gemm_part_bytes(gemm_slices(c, K, rows, N, n_batch, &ksb), rows, N, n_batch);
+    return 0;
+}
+
+GS_EXPORT int gs_gemm_ex(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride,
+                         float *Y, int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs,
+                         int64_t y_bs, void *work, size_t work_bytes, void *s) {
+    return gemm_impl(ty, W, row_stride, K, rows, X, x_stride, Y, y_stride, N, accumulate, n_batch, w_bs, x_bs, y_bs,
+                     work, work_bytes, s);
 }
 
 // =============================================================================================
@@ -846,6 +911,8 @@ int grouped_ffn(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, 
     a.rows = n_ff;
     a.n_exp = n_exp;
     a.lim = lim;
+    a.wait_limit = g_wait_limit.load();
+    a.wait_force = g_wait_force.load();
     if ((e = grouped_launch(1, ty_gu, a, n_pairs, st)) != hipSuccess) return e;
     if ((e = rows_f16(h, n_ff, n_ff, n_pairs, h16, hs, st)) != hipSuccess) return e;
     a.act = h16;
@@ -876,3 +943,30 @@ GS_EXPORT int gs_moe_grouped_scatter(int ty_gu, int ty_down, const GsExpertPtrs 
 }
 
 
+
+// =============================================================================================
+// bounded-wait status (no counterpart in the reference)
+// =============================================================================================
+GS_EXPORT int gs_wait_status(void *s) {
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    if ((e = hipStreamSynchronize((hipStream_t)s)) != hipSuccess) return e;
+    bool expired = false;
+    for (void *f : c->wait_flags) {
+        uint32_t v = 0;
+        if ((e = hipMemcpy(&v, f, 4, hipMemcpyDeviceToHost)) != hipSuccess) return e;
+        if (v) {
+            expired = true;
+            const uint32_t zero = 0;
+            if ((e = hipMemcpy(f, &zero, 4, hipMemcpyHostToDevice)) != hipSuccess) return e;
+        }
+    }
+    return expired ? hipErrorLaunchFailure : hipSuccess;
+}
+
+GS_EXPORT int gs_debug_wait_limit(uint32_t polls, int force) {
+    g_wait_limit.store(polls);
+    g_wait_force.store(force ? 1u : 0u);
+    return 0;
+}

@@ -96,6 +96,8 @@ struct GroupedArgs {
     int rows;                        // rows per expert matrix
     int n_exp;
     float lim;                       // SwiGLU clamp (<= 0: none)
+    uint32_t wait_limit;             // polls before an LDS fill wait gives up (and flags it)
+    uint32_t wait_force;             // test hook: nonzero makes every such wait run to its limit
 };
 
 // f32 rows -> f16 with a power-of-two row scale (grouped GEMM operands)
@@ -127,6 +129,8 @@ struct GemmArgs {
     int n_rb, n_tb;       // row blocks and token blocks of one problem
     int ksb;              // super-blocks per K slice (blockIdx.z); every super-block when not split
     float *part;          // K split: slice partials [slice][batch][N][rows] (null: write Y)
+    uint32_t wait_limit;  // polls before an LDS fill wait gives up (and flags it)
+    uint32_t wait_force;  // test hook: nonzero makes every such wait run to its limit
 };
 #define GS_GEMM_KS_MAX 16   // K slices of one gs_gemm call at most
 // sum of the K slices' partials in slice order into Y (+= when accumulate)

@@ -911,4 +911,136 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_scatter_add_rows(RowsArgs
     const float s = a.w[i];
     for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < a.n; c += gridDim.x * blockDim.x) dst[c] += s * src[c];
 }
+
+// =============================================================================================
+// Row-length-independent matrix-vector kernels: the shapes the streaming kernels' register plan
+// does not hold (gate/up rows longer than 64 lanes x 4 units per token, a down expert longer than
+// 64 x 8 units) and plain-type rows whose length is a multiple of 8 but not of 32. The reference
+// takes any K % 8 == 0 and K % QK == 0 (quants.cu:225-229, 380-381, 396-397); so do these.
+// One wave per output row; lane l walks units l, l + 64, ... of the row, decodes each with the
+// exact unit decoder and quantizes the matching activation unit to q8_1 on the fly (quant_unit,
+// the same values the streaming kernels stage), so the result is the q8_1 product of the fast
+// path up to f32 summation order. Plain types (F32, F16, BF16) take the f32 activations as they
+// are, as the streaming kernels do.
+//   kind 0 GEMV:   y[z][b][r] (+)= W[z][r] . x[z][b]              blockIdx.y = batch z
+//   kind 1 GATEUP: h[e][t][r] = swiglu(gate_e[r] . x[t], up_e[r] . x[t])   blockIdx.y = expert e
+//   kind 2 DOWN:   y[t][r] += sum_e w[t][e] (down_e[r] . h[e][t])
+// Not a hot path: every row re-quantizes its activation units (they come from L2).
+// =============================================================================================
+template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
+__device__ __forceinline__ void any_unit_w(const uint8_t *row, int u, int K, float (&v)[32]) {
+    if (QKB == 256) {
+        DEC(row + (u >> 3) * BB, u & 7, v);
+    } else if (QKB == 32) {
+        DEC(row + u * BB, 0, v);
+    } else {   // plain: the last unit of a row may be partial (K % 32 != 0): zero-padded copy
+        const uint8_t *p = row + (int64_t)u * 32 * BB;
+        const int cnt = min(32, K - 32 * u);
+        if (cnt == 32) {
+            DEC(p, 0, v);
+        } else {
+            uint8_t tmp[32 * BB];
+            for (int i = 0; i < 32 * BB; i++) tmp[i] = i < cnt * BB ? p[i] : 0;
+            DEC(tmp, 0, v);
+        }
+    }
+}
+// dot of 32 decoded weights with activation unit u of the row at xr
+template <bool PLAIN>
+__device__ __forceinline__ float any_unit_dot(const float (&w)[32], const float *xr, int u, int K) {
+    float v[32];
+    const int cnt = min(32, K - 32 * u);
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] = i < cnt ? xr[32 * u + i] : 0.f;
+    if (PLAIN) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) s += w[i] * v[i];
+        return s;
+    }
+    const Q81 q = quant_unit(v);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) s += w[i] * (float)(int8_t)(q.q[i >> 2] >> (8 * (i & 3)));
+    return h2f(f2h(q.d)) * s;
+}
+__device__ __forceinline__ float any_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+template <int KIND, int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
+__device__ __forceinline__ void any_body(const StreamArgs &a) {
+    constexpr bool PLAIN = QKB == 1;
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6), nwave = gridDim.x * (blockDim.x >> 6);
+    const int K = a.K, nu = (K + 31) / 32, nv = a.nvec;
+    const int64_t rs = a.row_stride;
+    for (int r = wave; r < a.rows; r += nwave) {
+        float acc[GS_NT_MAX], acc2[GS_NT_MAX];
+#pragma unroll
+        for (int t = 0; t < GS_NT_MAX; t++) acc[t] = acc2[t] = 0.f;
+        if (KIND == 0) {
+            const int z = blockIdx.y;
+            const uint8_t *row = a.w0[0] + (int64_t)z * a.w_bs + (int64_t)r * rs;
+            const float *x = a.x + (int64_t)z * a.x_bs;
+            for (int u = lane; u < nu; u += 64) {
+                float w[32];
+                any_unit_w<QKB, BB, DEC>(row, u, K, w);
+#pragma unroll
+                for (int t = 0; t < GS_NT_MAX; t++)
+                    if (t < nv) acc[t] += any_unit_dot<PLAIN>(w, x + (int64_t)t * a.x_stride, u, K);
+            }
+        } else if (KIND == 1) {
+            const int e = blockIdx.y;
+            const uint8_t *rg = a.w0[e] + (int64_t)r * rs, *ru = a.w1[e] + (int64_t)r * rs;
+            for (int u = lane; u < nu; u += 64) {
+                float wg[32], wu[32];
+                any_unit_w<QKB, BB, DEC>(rg, u, K, wg);
+                any_unit_w<QKB, BB, DEC>(ru, u, K, wu);
+#pragma unroll
+                for (int t = 0; t < GS_NT_MAX; t++)
+                    if (t < nv) {
+                        acc[t] += any_unit_dot<PLAIN>(wg, a.x + (int64_t)t * a.x_stride, u, K);
+                        acc2[t] += any_unit_dot<PLAIN>(wu, a.x + (int64_t)t * a.x_stride, u, K);
+                    }
+            }
+        } else {
+            for (int e = 0; e < a.nseg; e++) {
+                const uint8_t *row = a.w0[e] + (int64_t)r * rs;
+                float pe[GS_NT_MAX];
+#pragma unroll
+                for (int t = 0; t < GS_NT_MAX; t++) pe[t] = 0.f;
+                for (int u = lane; u < nu; u += 64) {
+                    float w[32];
+                    any_unit_w<QKB, BB, DEC>(row, u, K, w);
+#pragma unroll
+                    for (int t = 0; t < GS_NT_MAX; t++)
+                        if (t < nv && a.wt[t][e] != 0.f) pe[t] += any_unit_dot<PLAIN>(w, a.x + ((int64_t)e * nv + t) * K, u, K);
+                }
+#pragma unroll
+                for (int t = 0; t < GS_NT_MAX; t++)
+                    if (t < nv && a.wt[t][e] != 0.f) acc[t] += a.wt[t][e] * pe[t];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < GS_NT_MAX; t++) {
+            if (t >= nv) continue;
+            const float s = any_wave_sum(acc[t]);
+            if (KIND == 1) {
+                const float s2 = any_wave_sum(acc2[t]);
+                if (lane == 0) a.y[((int64_t)blockIdx.y * nv + t) * a.rows + r] = swiglu(s, s2, a.lim);
+            } else if (lane == 0) {
+                float *dst = KIND == 0 ? a.y + (int64_t)blockIdx.y * a.y_bs + (int64_t)t * a.y_stride + r
+                                       : a.y + (int64_t)t * a.y_stride + r;
+                *dst = (KIND == 2 || a.accumulate) ? *dst + s : s;
+            }
+        }
+    }
+}
+#define GS_ANY_KERNEL(TY, QKB, BB, DEC)                                                          \
+    extern "C" __global__ void __launch_bounds__(256) gs_k_any_0_##TY(StreamArgs a) { any_body<0, QKB, BB, DEC>(a); } \
+    extern "C" __global__ void __launch_bounds__(256) gs_k_any_1_##TY(StreamArgs a) { any_body<1, QKB, BB, DEC>(a); } \
+    extern "C" __global__ void __launch_bounds__(256) gs_k_any_2_##TY(StreamArgs a) { any_body<2, QKB, BB, DEC>(a); }
+GS_TYPE_LIST(GS_ANY_KERNEL)
 #endif  // GS_COMMON

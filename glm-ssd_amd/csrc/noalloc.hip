@@ -48,6 +48,15 @@ extern "C" __attribute__((visibility("default"))) int gs_moe_grouped_noalloc(
     if (need > (size_t)GS_MOE_GROUPED_SCRATCH_MAX) return hipErrorInvalidValue;   // beyond the array
     void *work = nullptr;
     if ((rc = scratch_ptr(&work)) != hipSuccess) return rc;
-    return gs_moe_grouped(ty_gu, ty_down, experts, n_exp, offs, idx, w, n_pairs, n_tok, gu_row_stride, K, n_ff,
-                          down_row_stride, x, y, lim, work, (size_t)GS_MOE_GROUPED_SCRATCH_MAX, s);
+    rc = gs_moe_grouped(ty_gu, ty_down, experts, n_exp, offs, idx, w, n_pairs, n_tok, gu_row_stride, K, n_ff,
+                        down_row_stride, x, y, lim, work, (size_t)GS_MOE_GROUPED_SCRATCH_MAX, s);
+    if (rc != hipSuccess && rc != hipErrorInvalidValue) {
+        // a runtime failure (e.g. after a device reset): look the address up again next time
+        int dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            std::lock_guard<std::mutex> lk(g_mu);
+            g_ptr.erase(dev);
+        }
+    }
+    return rc;
 }

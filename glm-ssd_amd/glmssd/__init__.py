@@ -87,6 +87,11 @@ SIGNATURES = {
     "gs_axpy": [_P, _P, C.c_float, _I64, _P],
     "gs_gemm": [C.c_int, _P, _I64, C.c_int, C.c_int, _P, _I64, _P, _I64, C.c_int, C.c_int, C.c_int, _I64, _I64, _I64,
                 _P],
+    "gs_gemm_workspace": [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_size_t)],
+    "gs_gemm_ex": [C.c_int, _P, _I64, C.c_int, C.c_int, _P, _I64, _P, _I64, C.c_int, C.c_int, C.c_int, _I64, _I64,
+                   _I64, _P, C.c_size_t, _P],
+    "gs_wait_status": [_P],
+    "gs_debug_wait_limit": [C.c_uint32, C.c_int],
     "gs_gather_rows": [_P, _P, _P, C.c_int, C.c_int, _P],
     "gs_scatter_add_rows": [_P, _P, _P, _P, C.c_int, C.c_int, _P],
     "gs_f32_to_f16": [_P, _P, _I64, _P],
@@ -297,6 +302,30 @@ class ops:
              y_bs=0, s=None):
         check(lib().gs_gemm(ty, _p(w), row_stride, k, rows, _p(x), x_stride, _p(y), y_stride, n,
                             1 if accumulate else 0, n_batch, w_bs, x_bs, y_bs, _raw(s)))
+
+    @staticmethod
+    def gemm_workspace(k, rows, n, n_batch=1):
+        """gs_gemm_workspace: bytes of K-split scratch gs_gemm_ex would use (0: no split)."""
+        b = C.c_size_t()
+        check(lib().gs_gemm_workspace(k, rows, n, n_batch, C.byref(b)))
+        return b.value
+
+    @staticmethod
+    def gemm_ex(ty, w, row_stride, k, rows, x, x_stride, y, y_stride, n, accumulate=False, n_batch=1, w_bs=0, x_bs=0,
+                y_bs=0, work=None, work_bytes=0, s=None):
+        """gs_gemm_ex: gs_gemm with a caller workspace for the K split."""
+        check(lib().gs_gemm_ex(ty, _p(w), row_stride, k, rows, _p(x), x_stride, _p(y), y_stride, n,
+                               1 if accumulate else 0, n_batch, w_bs, x_bs, y_bs, _p(work), work_bytes, _raw(s)))
+
+    @staticmethod
+    def wait_status(s=None):
+        """gs_wait_status: raises GsError if a bounded LDS wait expired since the last query."""
+        check(lib().gs_wait_status(_raw(s)))
+
+    @staticmethod
+    def debug_wait_limit(polls, force=False):
+        """gs_debug_wait_limit: test hook for the bounded LDS waits (poll bound, forced expiry)."""
+        check(lib().gs_debug_wait_limit(polls, 1 if force else 0))
 
     @staticmethod
     def moe_grouped_workspace(n_tok, n_pairs, k, n_ff):

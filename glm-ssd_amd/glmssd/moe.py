@@ -186,13 +186,18 @@ class MoeLayer:
         return b
 
     def _mm(self, m, x, y, t, s, x_stride=None, y_stride=None):
-        """forward.rs:700-710 mm_s: GEMV for up to 8 vectors, else GEMM"""
+        """forward.rs:700-710 mm_s: GEMV for up to 8 vectors, else GEMM (gs_gemm_ex: small problems
+        split K into the layer's workspace; the layer's calls run in order on one stream, so they
+        share it)"""
         xs = m.K if x_stride is None else x_stride
         ys = m.rows if y_stride is None else y_stride
         if t <= 8:
             ops.gemv(m.ty, m.ptr(), m.row_bytes, m.K, m.rows, x, xs, y, ys, t, False, s)
         else:
-            ops.gemm(m.ty, m.ptr(), m.row_bytes, m.K, m.rows, x, xs, y, ys, t, False, 1, 0, 0, 0, s)
+            need = ops.gemm_workspace(m.K, m.rows, t)
+            wk = self._buf("gemm_ws", need) if need else None
+            ops.gemm_ex(m.ty, m.ptr(), m.row_bytes, m.K, m.rows, x, xs, y, ys, t, False, 1, 0, 0, 0, wk,
+                        wk.nbytes if wk else 0, s)
 
     def forward(self, xn, out, t, s=None):
         """xn: device [t][n_embd] (normalised hidden states); out: device [t][n_embd], overwritten

@@ -10,8 +10,8 @@
  *
  * Activations entering a quantized matmul are quantized to q8_1 inside the kernels (blocks of
  * 32: f16 scale d = amax/127, int8 q = round(x/d)); the f32 activation ABI is unchanged.
- * Constraints beyond the reference's: K % 32 == 0 for the matmul entry points, weight rows
- * 2-byte aligned (every ggml tensor is).
+ * Constraints beyond the reference's: weight rows 2-byte aligned (every ggml tensor is). Row
+ * lengths are the reference's (K % 8 == 0 and a whole number of blocks; gs_gemm K % 32 == 0).
  */
 #ifndef GLMSSD_H
 #define GLMSSD_H
@@ -99,9 +99,9 @@ int gs_gemv_batched(int ty, const void *W, int64_t row_stride, int K, int rows, 
                     int64_t w_bs, int64_t x_bs, int64_t y_bs, void *s);
 
 /* fused routed-expert gate/up + SwiGLU: h[e][t][r] = swiglu(gate_e[r].x[t], up_e[r].x[t]);
- * x [nt][K], h [b->n][nt][rows] (lib.rs:62-65; quants.cu:378-393). K <= 8192 for one token and
- * K <= 4096 for two (a lane holds its share of the row's units; the target model has K = 4096);
- * larger K returns hipErrorInvalidValue. */
+ * x [nt][K], h [b->n][nt][rows] (lib.rs:62-65; quants.cu:378-393). Any K the reference takes;
+ * rows longer than the fast kernels' per-lane register plan (K > 8192 for one token, K > 4096
+ * for two) run on a slower one-wave-per-row kernel with the same q8_1 arithmetic. */
 int gs_moe_gateup(int ty, const GsMoeBatch *b, int nt, int64_t row_stride, int K, int rows, const float *x, float *h,
                   float lim, void *s);
 
@@ -131,11 +131,20 @@ int gs_swiglu(const float *g, const float *u, float *y, int64_t n, float lim, vo
 /* y += a*x (lib.rs:77; ops.cu:117-125) */
 int gs_axpy(float *y, const float *x, float a, int64_t n, void *s);
 /* Y[n*y_stride + m] (+)= W[m] . X[n*x_stride + :], n < N tokens; z-batched (lib.rs:115-118; gemm.cu:107-123).
- * Problems with few 128-row x 64-token tiles split K across workgroups and add the slices in a
- * fixed order (reproducible); their partials live in scratch taken from a library-owned
- * stream-ordered pool, at most CUs x 32 KB per stream, kept for the stream's next call. */
+ * Like the reference, allocates nothing and never synchronizes. */
 int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
             int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs, void *s);
+/* Additive (no counterpart in the reference): gs_gemm with a caller-owned workspace. Problems with
+ * few 128-row x 64-token tiles (small N, few rows) then split K across workgroups: each slice
+ * writes its f32 partial tile into `work` and the slices are added in a fixed order (results are
+ * reproducible; they differ from gs_gemm only in f32 summation order). gs_gemm_workspace gives the
+ * bytes a problem needs on the current device (0: no split, `work` unused; at most CUs x 32 KB).
+ * work: 16-byte aligned, >= that many bytes, not used by another call in flight; work == NULL
+ * runs as gs_gemm. Allocates nothing and never synchronizes. */
+int gs_gemm_workspace(int K, int rows, int N, int n_batch, size_t *bytes);
+int gs_gemm_ex(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
+               int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs,
+               void *work, size_t work_bytes, void *s);
 /* y[i][:] = x[idx[i]][:] (lib.rs:119; gemm.cu:125-138) */
 int gs_gather_rows(const float *x, const int *idx, float *y, int rows, int n, void *s);
 /* acc[idx[i]][:] += w[i] * y[i][:], idx unique within a call (lib.rs:120-122; gemm.cu:139-152) */
@@ -199,9 +208,24 @@ int gs_moe_grouped_scatter(int ty_gu, int ty_down, const GsExpertPtrs *experts, 
  * calls that overlap in time on one GPU (other streams, other threads) race and must not be
  * issued. */
 #define GS_MOE_GROUPED_SCRATCH_MAX (48u << 20)
+/* (The array is reserved on every GPU on which the library is used, whether or not this entry
+ * point is called.) */
 int gs_moe_grouped_noalloc(int ty_gu, int ty_down, const GsExpertPtrs *experts, int n_exp, const int *offs,
                            const int *idx, const float *w, int n_pairs, int n_tok, int64_t gu_row_stride, int K,
                            int n_ff, int64_t down_row_stride, const float *x, float *y, float lim, void *s);
+
+/* No counterpart in the reference. The MFMA kernels of gs_gemm(_ex) and gs_moe_grouped* pass work
+ * between the waves of a workgroup through LDS fill counters (release / acquire at workgroup
+ * scope). Each wait for a count is bounded (2^16 polls, far beyond any legitimate wait) so that a
+ * lost fill can never hang the GPU; a wait that runs out sets a sticky per-device flag, and the
+ * output of that launch is then unreliable. gs_wait_status synchronizes `stream`, returns
+ * hipErrorLaunchFailure if any wait has expired on the current device since the last query (and
+ * clears the flag), else 0. */
+int gs_wait_status(void *stream);
+/* Test hook (no counterpart in the reference): sets the poll bound of those waits for later
+ * launches (default 2^16); force != 0 makes every wait run to the bound and expire, so the
+ * expiry path can be exercised without a fault. Outputs of such launches are meaningless. */
+int gs_debug_wait_limit(uint32_t polls, int force);
 
 #ifdef __cplusplus
 }

@@ -487,7 +487,8 @@ static void quant_dequant_row(const float *x, int K, float *xh, int mode) {
 int or_gemv(int ty, const uint8_t *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride,
             int B, int quant_x, double *y, int nthreads) {
     int be, bb;
-    if (or_block(ty, &be, &bb) != 0 || K % be != 0 || K % 32 != 0 || B < 1 || quant_x < 0 || quant_x > 5) return -1;
+    if (or_block(ty, &be, &bb) != 0 || K % be != 0 || B < 1 || quant_x < 0 || quant_x > 5) return -1;
+    if (quant_x == OR_ACT_Q8_1 ? K % 32 != 0 : K % 8 != 0) return -1;   /* q8_1 units of 32; plain rows of 8 */
     float *xh = (float *)malloc(sizeof(float) * (size_t)K * B);
     for (int b = 0; b < B; b++) quant_dequant_row(x + (int64_t)b * x_stride, K, xh + (int64_t)b * K, quant_x);
     if (nthreads < 1) nthreads = 1;

@@ -170,6 +170,110 @@ def test_moe_ffn_tokens(ty_gu, ty_dn, n_tok, n, pool, n_embd, n_ff, lim, stream)
         assert np.array_equal(h, h1) and np.array_equal(y, y1)
 
 
+def test_moe_ffn_tokens_config4(stream):
+    """BASELINE config 4 through the MoE layer's path for up to 16 tokens: 4 tokens, each top-8
+    Zipf(1.1) over 288 resident IQ2_XXS experts (4096 / 1536, d ~ |N(0, 0.02)|), as one
+    gs_moe_ffn_tokens call; every token's output against the oracle's q8_1 FFN."""
+    from glmssd import synth
+    n_exp, n_tok, k, n_embd, n_ff = 288, 4, 8, 4096, 1536
+    rng = np.random.default_rng(4)
+    experts = [synth.iq2_xxs_expert(rng, n_embd, n_ff) for _ in range(n_exp)]
+    routes = synth.zipf_topk(rng, n_tok, n_exp, k)
+    x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    bufs = [[G.DeviceBuffer.from_array(m) for m in ex] for ex in experts]
+    batches = []
+    for ex, wt in routes:
+        b = G.MoeBatch()
+        b.n = k
+        for i, e in enumerate(ex):
+            b.gate[i], b.up[i], b.down[i] = (bufs[e][0].p.value, bufs[e][1].p.value, bufs[e][2].p.value)
+            b.w[0][i] = wt[i]
+        batches.append(b)
+    rbg, rbd = G.row_bytes(T.IQ2_XXS, n_embd), G.row_bytes(T.IQ2_XXS, n_ff)
+    dx = G.DeviceBuffer.from_array(x)
+    dh = G.DeviceBuffer(n_tok * k * n_ff * 4)
+    dy = G.DeviceBuffer.from_array(np.zeros((n_tok, n_embd), np.float32))
+    G.ops.moe_ffn_tokens(T.IQ2_XXS, T.IQ2_XXS, batches, rbg, n_embd, n_ff, rbd, dx, dh, dy, 0.0, stream)
+    got = dy.download(np.float32, n_tok * n_embd, stream).reshape(n_tok, n_embd)
+    used = sorted({int(e) for ex, _ in routes for e in ex})
+    pos = {e: i for i, e in enumerate(used)}
+    pt = [t for t in range(n_tok) for _ in range(k)]
+    pe = [pos[int(e)] for ex, _ in routes for e in ex]
+    pw = [float(v) for _, wt in routes for v in wt]
+    want = O.moe_ffn(T.IQ2_XXS, T.IQ2_XXS, [experts[e][0] for e in used], [experts[e][1] for e in used],
+                     [experts[e][2] for e in used], rbg, rbd, n_embd, n_ff, x, pt, pe, pw, nthreads=16, act="q8_1")
+    errs = [rel_l2(got[t], want[t]) for t in range(n_tok)]
+    say(f"  config 4 (288 experts, {len(used)} used, 4 tokens): per-token rel-L2 " + " ".join(f"{e:.2e}" for e in errs))
+    assert max(errs) <= REL_L2
+
+
+# shapes beyond the streaming kernels' register plan: the reference takes any K % QK == 0
+# (quants.cu:378-392); (gate/up type, down type, tokens, experts, n_embd, n_ff)
+LONG_K = [(T.IQ2_XXS, T.IQ2_XXS, 1, 3, 12288, 512), (T.Q4_K, T.Q4_K, 2, 2, 8192, 1024),
+          (T.IQ2_XXS, T.IQ3_XXS, 1, 2, 1024, 20480), (T.F16, T.F16, 2, 2, 1000, 520)]
+
+
+@pytest.mark.parametrize("ty_gu,ty_dn,nt,n,n_embd,n_ff", LONG_K)
+def test_moe_ffn_any_k(ty_gu, ty_dn, nt, n, n_embd, n_ff, stream):
+    """gs_moe_gateup / gs_moe_down at K = 12288 (one token), K = 8192 (two tokens), a down row of
+    20480, and float rows of 8-element multiples (K % 32 != 0): within the matmul bound of the
+    oracle; gs_moe_ffn_tokens over the same experts equals gs_moe_ffn per token bit for bit."""
+    say(f"moe_ffn any K {G.TYPE_NAMES[ty_gu]}/{G.TYPE_NAMES[ty_dn]} nt={nt} n={n} {n_embd}x{n_ff}")
+    rng = O.Rng(55 + n_embd + n_ff)
+    nrng = np.random.default_rng(n_embd * 3 + n)
+    gate = [_weights(rng, nrng, ty_gu, n_ff * n_embd) for _ in range(n)]
+    up = [_weights(rng, nrng, ty_gu, n_ff * n_embd) for _ in range(n)]
+    down = [_weights(rng, nrng, ty_dn, n_embd * n_ff) for _ in range(n)]
+    x = nrng.standard_normal((nt, n_embd)).astype(np.float32)
+    w = nrng.random((nt, n)).astype(np.float32)
+    pt = [t for t in range(nt) for _ in range(n)]
+    pe = [e for _ in range(nt) for e in range(n)]
+    pw = [float(w[t, e]) for t in range(nt) for e in range(n)]
+    rbg, rbd = G.row_bytes(ty_gu, n_embd), G.row_bytes(ty_dn, n_ff)
+    flt = ty_gu in (T.F32, T.F16, T.BF16)
+    want = O.moe_ffn(ty_gu, ty_dn, gate, up, down, rbg, rbd, n_embd, n_ff, x, pt, pe, pw, nthreads=16,
+                     act="f32" if flt else "q8_1")
+    bufs = [G.DeviceBuffer.from_array(a) for a in gate + up + down]
+    b = G.MoeBatch()
+    b.n = n
+    for e in range(n):
+        b.gate[e], b.up[e], b.down[e] = bufs[e].p.value, bufs[n + e].p.value, bufs[2 * n + e].p.value
+        for t in range(nt):
+            b.w[t][e] = w[t, e]
+    dx = G.DeviceBuffer.from_array(x)
+    dh = G.DeviceBuffer(n * nt * n_ff * 4)
+    dy = G.DeviceBuffer.from_array(np.zeros((nt, n_embd), np.float32))
+    G.ops.moe_gateup(ty_gu, b, nt, rbg, n_embd, n_ff, dx, dh, 0.0, stream)
+    G.ops.moe_down(ty_dn, b, nt, rbd, n_ff, n_embd, dh, dy, stream)
+    got = dy.download(np.float32, nt * n_embd, stream).reshape(nt, n_embd)
+    e = rel_l2(got, want)
+    say(f"  y rel-L2 vs oracle {e:.2e}")
+    assert e <= REL_L2
+    if nt == 1:
+        return
+    # the token loop: one-token batches of the same experts
+    bs = []
+    for t in range(nt):
+        bt = G.MoeBatch()
+        bt.n = n
+        for i in range(n):
+            bt.gate[i], bt.up[i], bt.down[i] = b.gate[i], b.up[i], b.down[i]
+            bt.w[0][i] = w[t, i]
+        bs.append(bt)
+    dh1 = G.DeviceBuffer(nt * n * n_ff * 4)
+    dy1 = G.DeviceBuffer.from_array(np.zeros((nt, n_embd), np.float32))
+    for t in range(nt):
+        G.ops.moe_ffn(ty_gu, ty_dn, bs[t], 1, rbg, n_embd, n_ff, rbd, dx.p.value + t * n_embd * 4,
+                      dh1.p.value + t * n * n_ff * 4, dy1.p.value + t * n_embd * 4, 0.0, stream)
+    dh2 = G.DeviceBuffer(nt * n * n_ff * 4)
+    dy2 = G.DeviceBuffer.from_array(np.zeros((nt, n_embd), np.float32))
+    G.ops.moe_ffn_tokens(ty_gu, ty_dn, bs, rbg, n_embd, n_ff, rbd, dx, dh2, dy2, 0.0, stream)
+    y1 = dy1.download(np.float32, nt * n_embd, stream)
+    y2 = dy2.download(np.float32, nt * n_embd, stream)
+    assert rel_l2(y1.reshape(nt, n_embd), want) <= REL_L2
+    assert np.array_equal(y1, y2)
+
+
 def test_moe_ffn_tokens_rejects(stream):
     """Unequal expert counts, and more than 32 (token, expert) pairs, are rejected before any launch."""
     b1, b2 = G.MoeBatch(), G.MoeBatch()

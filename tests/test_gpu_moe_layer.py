@@ -83,3 +83,46 @@ def test_moe_layer(t, ty_dn):
     e, er, es = rel_l2(got, want), rel_l2(acc, routed), rel_l2(got - acc, sh)
     say(f"  MoE layer t={t} down={G.TYPE_NAMES[ty_dn]}: rel-L2 {e:.2e}; routed {er:.2e}; shared {es:.2e}")
     assert e <= REL_L2 and er <= REL_L2 and es <= REL_L2
+
+
+def test_moe_layer_expert_rows_q4_k():
+    """Non-IQ routed experts (Q4_K) at t = 20: the per-expert multi-token branch (run_expert_rows,
+    forward.rs:1399-1413: gather, gate/up matmuls, SwiGLU, down, weighted scatter-add), where each
+    matmul is mm_s (forward.rs:700-710): a q8_1 GEMV for an expert group of up to 8 pairs, the f16
+    GEMM above. The oracle follows the same split per expert."""
+    t, n_embd, n_ff, n_sh, ne, k = 20, 1024, 512, 512, 24, 8
+    lim_e = 7.0
+    rrng = np.random.default_rng(4242)
+    router = (rrng.standard_normal((ne, n_embd)) * 0.05).astype(np.float32)
+    bias = (rrng.standard_normal(ne) * 0.5).astype(np.float32)   # skewed popularity: groups of 1..20 pairs
+    x = rrng.standard_normal((t, n_embd)).astype(np.float32)
+    nrng = np.random.default_rng(4243)
+    shared = [synth.random_blocks(nrng, T.Q6_K, n_sh * n_embd, 1e-4, [208]),
+              synth.random_blocks(nrng, T.Q6_K, n_sh * n_embd, 1e-4, [208]),
+              synth.random_blocks(nrng, T.Q6_K, n_embd * n_sh, 1e-4, [208])]
+    # small Q4_K scales keep h inside the f16 range of the GEMM semantics
+    experts = [tuple(synth.random_blocks(nrng, T.Q4_K, n_ff * n_embd, 2e-4, [0, 2]) for _ in range(3))
+               for _ in range(ne)]
+    s = G.Stream()
+    layer = MoeLayer(router.view(np.uint8).reshape(-1), bias, shared, experts, n_embd, n_ff, T.Q4_K, T.Q4_K, k=k,
+                     clamp_exp=lim_e, n_ff_shexp=n_sh, s=s)
+    assert layer.grouped is None
+    dx, dout = G.DeviceBuffer.from_array(x, s), G.DeviceBuffer(t * n_embd * 4)
+    routes = layer.forward(dx, dout, t, s)
+    acc = layer._scratch["acc"].download(np.float32, t * n_embd, s).reshape(t, n_embd)   # routed part
+    groups = {}
+    for ti, r in enumerate(routes):
+        for e, w in r:
+            groups.setdefault(e, []).append((ti, w))
+    sizes = sorted(len(v) for v in groups.values())
+    assert sizes[0] <= 8 < sizes[-1], sizes   # both matmul branches run
+    rb = G.row_bytes(T.Q4_K, n_embd)
+    rbd = G.row_bytes(T.Q4_K, n_ff)
+    want = np.zeros((t, n_embd))
+    for e, prs in groups.items():
+        act = "q8_1" if len(prs) <= 8 else "f16"
+        want += O.moe_ffn(T.Q4_K, T.Q4_K, [experts[e][0]], [experts[e][1]], [experts[e][2]], rb, rbd, n_embd, n_ff,
+                          x, [p[0] for p in prs], [0] * len(prs), [p[1] for p in prs], lim=lim_e, nthreads=8, act=act)
+    e = rel_l2(acc, want)
+    say(f"  MoE layer t={t} Q4_K experts (group sizes {sizes[0]}..{sizes[-1]}): routed rel-L2 {e:.2e}")
+    assert e <= REL_L2

@@ -214,6 +214,15 @@ def test_gemv_5_to_8_vectors_token_groups(ty, stream):
     assert _gemv_case(ty, 130, 4096, 6, stream, 62, accumulate=True) <= REL_L2
 
 
+@pytest.mark.parametrize("ty", [T.F32, T.F16])
+def test_gemv_float_rows_of_8(ty, stream):
+    # plain rows whose length is a multiple of 8 but not of 32 (the reference's K % 8 rule,
+    # quants.cu:225-229), with strides, accumulate and several vectors
+    for B in (1, 3, 8):
+        assert _gemv_case(ty, 77, 1000, B, stream, 70 + B) <= REL_L2_F32
+    assert _gemv_case(ty, 45, 264, 2, stream, 80, accumulate=True, x_stride=268) <= REL_L2_F32
+
+
 def test_gemv_batched(stream):
     ty, K, rows, nb = T.Q4_K, 512, 96, 5
     rb = G.row_bytes(ty, K)
@@ -354,47 +363,60 @@ def test_gemm_every_type(ty, stream):
 
 
 def test_gemm_full_grid_and_k_split(stream):
-    # 17 row blocks x 8 token blocks = 136 tiles: one launch over the whole K; then few tiles (12
-    # row blocks, one token block): K split into 16 slices summed by the reduce pass, reproducible
-    # call to call and equal to the unsplit result within the f32 summation-order bound
+    # 17 row blocks x 8 token blocks = 136 tiles: one launch over the whole K, no workspace needed.
+    # Few tiles (12 row blocks, one token block): gs_gemm_ex splits K into 16 slices in the caller's
+    # workspace, summed by the reduce pass, reproducible call to call; plain gs_gemm runs the same
+    # problem unsplit (it allocates nothing) -- both within the f32 summation-order bound
     e = _gemm_case(T.Q8_0, 512, 2176, 512, stream, 21)
     say(f"gemm Q8_0 2176x512 N=512 (full grid): rel-L2 {e:.2e}")
     assert e <= GEMM_REL
+    assert G.ops.gemm_workspace(512, 2176, 512) == 0
     ty, K, rows, N = T.IQ2_XXS, 4096, 1536, 64
     rb = G.row_bytes(ty, K)
     raw = O.Rng(22).random_blocks(ty, rows * K)
     X = np.random.default_rng(23).standard_normal((N, K)).astype(np.float32)
     want = O.gemv(ty, raw, rb, K, rows, X, B=N, act="f16", nthreads=8)
     dw, dx = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X)
+    need = G.ops.gemm_workspace(K, rows, N)
+    assert 0 < need <= 256 * 32768
+    wk = G.DeviceBuffer(need)
     outs = []
     for _ in range(3):
         dy = G.DeviceBuffer(N * rows * 4)
-        G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, stream)
+        G.ops.gemm_ex(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, wk, need, stream)
         outs.append(dy.download(np.float32, N * rows, stream))
     e = rel_l2(outs[0].reshape(N, rows), want)
-    say(f"gemm IQ2_XXS 1536x4096 N=64 (K split): rel-L2 {e:.2e}")
+    say(f"gemm_ex IQ2_XXS 1536x4096 N=64 (K split): rel-L2 {e:.2e}")
     assert e <= GEMM_REL
     assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
+    dy = G.DeviceBuffer(N * rows * 4)
+    G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, stream)
+    e = rel_l2(dy.download(np.float32, N * rows, stream).reshape(N, rows), want)
+    say(f"gemm IQ2_XXS 1536x4096 N=64 (unsplit): rel-L2 {e:.2e}")
+    assert e <= GEMM_REL
+    # a workspace smaller than the query's answer is refused before any launch
+    with pytest.raises(G.GsError):
+        G.ops.gemm_ex(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, wk, need - 4, stream)
 
 
-def test_gemm_k_split_many_streams():
-    # the split's scratch is kept per stream for up to 16 streams; an 18-stream cycle releases and
-    # re-creates it, and every call still returns the same bits
-    ty, K, rows, N = T.Q8_0, 2048, 256, 24
+def test_gemm_ex_accumulate_and_batches(stream):
+    # the K split with accumulate and n_batch = 2: slices summed in order, then added to Y
+    ty, K, rows, N, nb = T.Q8_0, 2048, 256, 24, 2
     rb = G.row_bytes(ty, K)
-    raw = O.Rng(31).random_blocks(ty, rows * K)
-    X = np.random.default_rng(32).standard_normal((N, K)).astype(np.float32)
-    dw, dx = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X)
-    streams = [G.Stream() for _ in range(18)]
-    outs = []
-    for rep in range(2):
-        for st in streams:
-            dy = G.DeviceBuffer(N * rows * 4)
-            G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, st)
-            outs.append(dy.download(np.float32, N * rows, st))
-    want = O.gemv(ty, raw, rb, K, rows, X, B=N, act="f16", nthreads=8)
-    assert rel_l2(outs[0].reshape(N, rows), want) <= GEMM_REL
-    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
+    raw = O.Rng(31).random_blocks(ty, nb * rows * K)
+    X = np.random.default_rng(32).standard_normal((nb, N, K)).astype(np.float32)
+    wants = [O.gemv(ty, raw[z * rows * rb:(z + 1) * rows * rb], rb, K, rows, X[z], B=N, act="f16", nthreads=8)
+             for z in range(nb)]
+    # prior contents on the scale of the product, so the f32 sum keeps the product's bits
+    y0 = (np.random.default_rng(33).standard_normal((nb, N, rows)) * np.std(wants[0])).astype(np.float32)
+    dw, dx, dy = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer.from_array(y0)
+    need = G.ops.gemm_workspace(K, rows, N, nb)
+    assert need > 0
+    wk = G.DeviceBuffer(need)
+    G.ops.gemm_ex(ty, dw, rb, K, rows, dx, K, dy, rows, N, True, nb, rows * rb, N * K, N * rows, wk, need, stream)
+    got = dy.download(np.float32, nb * N * rows, stream).reshape(nb, N, rows).astype(np.float64) - y0
+    for z in range(nb):
+        assert rel_l2(got[z], wants[z]) <= GEMM_REL
 
 
 def test_gemm_accumulate_strides_and_partial_superblock(stream):
