@@ -67,7 +67,7 @@ def bench_lib():
     L.bn_copy.argtypes = [P, P, C.c_size_t, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_read.argtypes = [P, C.c_int, C.c_size_t, C.c_int, C.c_int, P, C.POINTER(C.c_float)]
     L.bn_gemm.argtypes = [C.c_int, P, C.c_int, I64, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P,
-                          C.POINTER(C.c_float)]
+                          C.c_size_t, P, C.POINTER(C.c_float)]
     L.bn_set_ramp_ms.argtypes = [C.c_float]
     L.bn_set_ramp_ms.restype = None
     L.bn_moe_grouped.argtypes = [C.c_int, C.c_int, P, C.c_int, C.c_int, P, P, P, P, C.c_int, I64, C.c_int, C.c_int, I64, P, P,
@@ -275,7 +275,8 @@ def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 
 
 
 def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 << 20):
-    """gs_gemm (f16 MFMA tiles) of N tokens through a rows x K matrix, weight copies rotated."""
+    """gs_gemm_ex (f16 MFMA tiles; a workspace for the K split where the problem takes one) of N tokens
+    through a rows x K matrix, weight copies rotated."""
     import glmssd as G
     rng = np.random.default_rng(seed)
     raw = make(rng, rows, K)
@@ -288,12 +289,14 @@ def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 
     ptrs = (C.c_void_p * n)(*[buf.p.value + i * raw.nbytes for i in range(n)])
     x = G.DeviceBuffer.from_array(rng.standard_normal(N * K).astype(np.float32), s)
     y = G.DeviceBuffer(N * rows * 4)
+    need = G.ops.gemm_workspace(K, rows, N)
+    wk = G.DeviceBuffer(need) if need else None
     ms = C.c_float()
     G.check(L.bn_gemm(ty, C.cast(ptrs, C.c_void_p), n, G.row_bytes(ty, K), K, rows, x.p, y.p, N, steps, warmup,
-                      s.raw(), C.byref(ms)))
+                      wk.p if wk else None, need, s.raw(), C.byref(ms)))
     t = ms.value * 1e-3
     flops = 2.0 * N * rows * K
-    return {"us_per_call": round(ms.value * 1e3, 2), "TFLOPs": round(flops / t / 1e12, 1),
+    return {"us_per_call": round(ms.value * 1e3, 2), "TFLOPs": round(flops / t / 1e12, 1), "k_split_workspace": need,
             "frac_mfma_f16_peak": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
             "weight_GBps": round(raw.nbytes / t / 1e9, 1), "tokens": N, "rotated_copies": n}
 

@@ -238,11 +238,14 @@ BN_EXPORT int bn_read(const void *const *bases, int nb, size_t bytes, int steps,
 }
 
 // gs_gemm over rotating weight copies Ws[i % nw]: Y[N][rows] = X[N][K] . W^T; mean ms per call.
+// gs_gemm_ex with the caller's workspace (work = NULL: plain gs_gemm)
 BN_EXPORT int bn_gemm(int ty, const void *const *Ws, int nw, int64_t rs, int K, int rows, const float *X, float *Y,
-                      int N, int steps, int warmup, void *s, float *ms) {
+                      int N, int steps, int warmup, void *work, size_t work_bytes, void *s, float *ms) {
     Timer t;
     CK(t.init());
-    auto step = [&](int i) { return gs_gemm(ty, Ws[i % nw], rs, K, rows, X, K, Y, rows, N, 0, 1, 0, 0, 0, s); };
+    auto step = [&](int i) {
+        return gs_gemm_ex(ty, Ws[i % nw], rs, K, rows, X, K, Y, rows, N, 0, 1, 0, 0, 0, work, work_bytes, s);
+    };
     int w0 = 0;
     CK(warm(step, warmup, s, &w0));
     CK(gs_event_record(t.a, s));

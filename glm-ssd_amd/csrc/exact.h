@@ -186,6 +186,63 @@ __device__ __forceinline__ void iq4_xs(const uint8_t *b, int u, float (&y)[32]) 
     }
 }
 
+// ---- the same decoders over a 4-byte aligned copy of a 256-element group in LDS ---------------
+// (gs_gemm stages each row's super-block into an LDS slot that starts on a dword.) They read whole
+// dwords and convert bytes with shifts and masks, where the byte-wise decoders above compile to
+// one LDS read per byte, and evaluate the same f32 expressions in the same order, so their output
+// is bit-identical.
+namespace al {
+__device__ __forceinline__ uint32_t w32(const uint8_t *p, int off) { return *(const uint32_t *)(p + off); }
+__device__ __forceinline__ float h16(uint32_t w, int hi) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? w >> 16 : w)); }
+__device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)(int)(int8_t)(w >> (8 * i)); }
+__device__ __forceinline__ float ubyte(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
+
+// Q8_0: unit u = block u of the group (34-byte blocks, so block u starts 2 (u & 1) bytes past a dword)
+__device__ __forceinline__ void q8_0(const uint8_t *p, int u, float (&y)[32]) {
+    const int o = 34 * u, base = o & ~3, sh = o & 3;
+    uint32_t w[10];
+    for (int i = 0; i < 10; i++) w[i] = w32(p, base + 4 * i);
+    const float d = h16(w[0], sh);
+    for (int k = 0; k < 8; k++) {
+        const uint32_t q = sh ? w[k + 1] : __builtin_amdgcn_alignbyte(w[k + 1], w[k], 2);
+        for (int i = 0; i < 4; i++) y[4 * k + i] = sbyte(q, i) * d;
+    }
+}
+
+// Q4_K: d and dmin in dword 0, the 12 scale bytes in dwords 1..3, unit u's nibbles in the 32 qs
+// bytes at 16 + 32 (u >> 1)
+__device__ __forceinline__ void q4_k(const uint8_t *p, int u, float (&y)[32]) {
+    const uint32_t dd = w32(p, 0);
+    // scale_min_k4 (lib.rs:87-93) on byte j & 3 of the three scale dwords
+    const uint32_t sh = 8u * (uint32_t)(u & 3);
+    const uint32_t b1 = (w32(p, 4) >> sh) & 0xffu, b2 = (w32(p, 8) >> sh) & 0xffu, b3 = (w32(p, 12) >> sh) & 0xffu;
+    const uint32_t sci = u < 4 ? b1 & 63u : (b3 & 0xfu) | ((b1 >> 6) << 4);
+    const uint32_t mni = u < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
+    const float dl = h16(dd, 0) * (float)sci, ml = h16(dd, 1) * (float)mni;
+    const int nib = 4 * (u & 1);
+    for (int k = 0; k < 8; k++) {
+        const uint32_t q = (w32(p, 16 + 32 * (u >> 1) + 4 * k) >> nib) & 0x0f0f0f0fu;
+        for (int i = 0; i < 4; i++) y[4 * k + i] = dl * ubyte(q, i) - ml;
+    }
+}
+
+// Q6_K: unit u = quarter k = u % 4 of half n = u / 4; ql, qh, the int8 scales and d all start on
+// dwords
+__device__ __forceinline__ void q6_k(const uint8_t *p, int u, float (&y)[32]) {
+    const int n = u >> 2, k = u & 3;
+    const float d = h16(w32(p, 208), 0);
+    // scale bytes 2k and 2k + 1 of the half (elements 0..15, 16..31), in the dword at 4 (k >> 1)
+    const uint32_t scw = w32(p, 192 + 8 * n + 4 * (k >> 1));
+    const float s0 = d * sbyte(scw, 2 * (k & 1)), s1 = d * sbyte(scw, 2 * (k & 1) + 1);
+    for (int m = 0; m < 8; m++) {
+        const uint32_t lo = (w32(p, 64 * n + 32 * (k & 1) + 4 * m) >> (4 * (k >> 1))) & 0x0f0f0f0fu;
+        const uint32_t hi = ((w32(p, 128 + 32 * n + 4 * m) >> (2 * k)) & 0x03030303u) << 4;
+        const uint32_t q = lo | hi;
+        for (int i = 0; i < 4; i++) y[4 * m + i] = (m < 4 ? s0 : s1) * (float)((int)((q >> (8 * i)) & 0xffu) - 32);
+    }
+}
+}  // namespace al
+
 }  // namespace exact
 
 #pragma clang fp contract(fast)

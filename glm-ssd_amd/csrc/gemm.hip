@@ -75,6 +75,13 @@ struct GemmFmt {
         else if (QKB == 32) DEC(p + u * BB, 0, v);
         else DEC(p + 32 * u * BB, 0, v);
     }
+    // the same from the dword-aligned LDS slot: the dword decoders where the format has one
+    __device__ static __forceinline__ void slot_unit(const uint8_t *p, int u, float (&v)[32]) {
+        if constexpr (DEC == &exact::q8_0) exact::al::q8_0(p, u, v);
+        else if constexpr (DEC == &exact::q4_k) exact::al::q4_k(p, u, v);
+        else if constexpr (DEC == &exact::q6_k) exact::al::q6_k(p, u, v);
+        else unit(p, u, v);
+    }
 };
 
 template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32]), int GM_NBUF>
@@ -261,7 +268,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
                 } else if constexpr (F::PLAIN) {
                     F::unit(W + (int64_t)(r0 + rr) * rs + (int64_t)256 * b * BB, 2 * q + hu, v);
                 } else {
-                    F::unit((const uint8_t *)__builtin_assume_aligned(rawbuf + buf * RAWB + rr * F::SBP, 4), 2 * q + hu, v);
+                    F::slot_unit((const uint8_t *)__builtin_assume_aligned(rawbuf + buf * RAWB + rr * F::SBP, 4), 2 * q + hu, v);
                 }
 #pragma unroll
                 for (int g = 0; g < 4; g++) bf[n][hu][g] = to_h8(v + 8 * g);
@@ -269,19 +276,26 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         }
         // contraction: MFMA m takes group m & 3 of unit 2q + (m >> 2)
         const uint8_t *slab = abuf + buf * ASLAB;
+        // (a full tile contracts without branches: a per-MFMA branch serializes each fragment
+        // read with its MFMA)
+        auto contract = [&](auto full) {
 #pragma unroll
-        for (int m = 0; m < 8; m++) {
-            const int cc = 8 * q + m;   // = 8q + 4 (m >> 2) + (m & 3)
+            for (int m = 0; m < 8; m++) {
+                const int cc = 8 * q + m;   // = 8q + 4 (m >> 2) + (m & 3)
+                gh8 av[4];
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++) {
-                if (tt < ntt) {
-                    const gh8 av = *(const gh8 *)(slab + (16 * tt + j) * 512 + ((cc ^ j) << 4));
+                for (int tt = 0; tt < 4; tt++)
+                    if (decltype(full)::value || tt < ntt) av[tt] = *(const gh8 *)(slab + (16 * tt + j) * 512 + ((cc ^ j) << 4));
 #pragma unroll
-                    for (int n = 0; n < GM_NR; n++)
-                        acc[tt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[n][m >> 2][m & 3], acc[tt][n], 0, 0, 0);
-                }
+                for (int tt = 0; tt < 4; tt++)
+                    if (decltype(full)::value || tt < ntt)
+#pragma unroll
+                        for (int n = 0; n < GM_NR; n++)
+                            acc[tt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[tt], bf[n][m >> 2][m & 3], acc[tt][n], 0, 0, 0);
             }
-        }
+        };
+        if (ntt == 4) contract(BoolC<true>{});
+        else contract(BoolC<false>{});
         if (more) {
             raw_store(buf ^ 1, b + 1, rv, rx);
             x_store(buf ^ 1, b + 1, xv);

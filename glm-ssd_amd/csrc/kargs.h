@@ -114,9 +114,10 @@ struct RowsQArgs {
 // threads per gs_k_gemm_* workgroup (gemm.hip: 8 waves, 16 weight rows each)
 #define GS_GEMM_THREADS 512
 // LDS buffers per gs_k_gemm_* workgroup: 2 = the next super-block prefetched through registers
-// (one workgroup per CU); 1 = single-buffered steps, two workgroups per CU taking turns (measured
-// faster for Q4_K only: 173 against 212 us at 12288 x 4096 x 512; Q8_0 and Q6_K slower)
-static inline constexpr int gs_gemm_nbuf(int ty) { return ty == 12 ? 1 : 2; }
+// (one workgroup per CU); 1 = single-buffered steps, two workgroups per CU taking turns (Q4_K
+// 12288 x 4096 x 512 measured 173 against 212 us that way until the contraction lost its
+// per-MFMA branches; since then both take about 165 us and every format is double-buffered)
+static inline constexpr int gs_gemm_nbuf(int) { return 2; }
 struct GemmArgs {
     const uint8_t *W;
     const float *X;

@@ -355,6 +355,33 @@ def test_gemm_hot_types(ty, N, stream):
     assert e <= GEMM_REL
 
 
+@pytest.mark.parametrize("ty", ALL)
+def test_gemm_weights_bit_exact(ty, stream):
+    # X = the identity (token n one-hot at element n): Y[n][r] is then exactly the f16 rounding of
+    # weight (r, n), so the tile decoders (byte-wise and dword-wise) are checked bit for bit
+    # against the oracle's dequantization, for every element of two super-blocks of 70 rows
+    K, rows = 512, 70
+    rb = G.row_bytes(ty, K)
+    if ty in FLOAT:
+        v = np.random.default_rng(ty).standard_normal(rows * K).astype(np.float32)
+        raw = {T.F32: v.view(np.uint8), T.F16: v.astype(np.float16).view(np.uint8),
+               T.BF16: (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)}[ty]
+    else:
+        raw = O.Rng(3 * ty + 1).random_blocks(ty, rows * K)
+    with np.errstate(over="ignore", invalid="ignore"):
+        w16 = O.dequantize(ty, raw, rows * K).reshape(rows, K).astype(np.float16)
+    ok = np.all(np.isfinite(w16), axis=1)   # a non-finite weight makes 0 x w non-finite in its row
+    assert ok.mean() > 0.5
+    X = np.eye(K, dtype=np.float32)
+    dw, dx, dy = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(K * rows * 4)
+    G.ops.gemm(ty, dw, rb, K, rows, dx, K, dy, rows, K, False, 1, 0, 0, 0, stream)
+    got = dy.download(np.float32, K * rows, stream).reshape(K, rows).T
+    want = w16.astype(np.float32) + np.float32(0)   # -0 -> +0: a sum of products that starts at +0
+    bad = np.count_nonzero(got[ok].view(np.uint32) != want[ok].view(np.uint32))
+    say(f"gemm weights {G.TYPE_NAMES[ty]}: {ok.sum()} finite rows, {bad} mismatching elements")
+    assert bad == 0
+
+
 @pytest.mark.parametrize("ty", [t for t in ALL])
 def test_gemm_every_type(ty, stream):
     e = _gemm_case(ty, 512, 131, 70, stream, seed=7 * ty)

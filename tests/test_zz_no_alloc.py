@@ -58,6 +58,16 @@ def test_noalloc_matches_workspace_call():
     _compare(layer, 20, 32, s)    # a second, smaller call reuses it
 
 
+def test_noalloc_near_the_array_bound():
+    # the sizing the header quotes: 512 tokens x top-8 at 4096 / 1536 (4096 pairs, about 42 MB of
+    # the 48 MiB array), so the layout's last regions (h16 and its row scales) lie near its end
+    s = G.Stream()
+    layer = _layer(12, 4096, 1536, 5)
+    need = G.ops.moe_grouped_workspace(512, 4096, 4096, 1536)
+    assert 40 << 20 < need <= (48 << 20)
+    _compare(layer, 512, 51, s)
+
+
 def test_noalloc_rejects_beyond_scratch():
     s = G.Stream()
     layer = _layer(4, 2048, 1024, 4)
