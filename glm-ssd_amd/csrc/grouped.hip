@@ -31,15 +31,17 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));   // staging chunk (a native vector, so it stays in VGPRs)
 
 // Decode tables in LDS, built by every workgroup at start:
-//   signs (16 KB, at byte 0): for a 7-bit sign index i, the 8 elements' f16 sign bits as four
-//     words (bit 15 / bit 31 of word w: element 2w / 2w+1 of ksigns(i) negative), 16 bytes,
-//     replicated 8 times: lane j reads its copy at 128 i + 16 (j & 7), so the 8 lanes of an LDS
-//     phase never share a bank;
+//   signs (16 KB, at byte 0): for a 7-bit sign index i, the 8 elements' sign bits of ksigns(i) as
+//     two words P (elements 0..3) and Q (4..7), 8 bytes: P holds element 0 at bit 15, 1 at bit 31,
+//     2 at bit 14 and 3 at bit 30, so P & 0x80008000 and (P << 1) & 0x80008000 are the f16 sign
+//     masks of element pairs (0, 1) and (2, 3); Q likewise for 4..7. Replicated 16 times: lane j
+//     reads its copy at 128 i + 8 (j & 15), so the 16 lanes reading at once never share a bank;
 //   grid (64 KB, at byte GS_GRP_GRID_OFF): for grid index g and unit scale s (0..15), the 8
 //     (IQ2_XXS) or 4 (IQ3_XXS) grid values times 2s+1 as f16 at 256 g + 16 s -- the address is one
 //     v_perm of the index byte and the scale nibble (grid * (2s+1) <= 43 * 31 = 1333 for IQ2_XXS,
 //     62 * 31 = 1922 for IQ3_XXS: exact in f16).
-// A B fragment (8 weights) is one 16-byte grid read, one 16-byte sign read and 4 XORs.
+// A B fragment (8 weights) is one 16-byte grid read, one 8-byte sign read, 2 shifts and 4
+// mask-and-XORs (one v_bitop3 each).
 #define GS_GRP_GRID_OFF 16384
 #define GS_GRP_TAB_BYTES (16384 + 65536)
 // Workgroup bookkeeping, in the dynamic LDS after the tables and the activation slots (the kernels
@@ -86,12 +88,15 @@ __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
         }
         *(uint4 *)(tab + GS_GRP_GRID_OFF + (e << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    for (int e = tid; e < 128 * 8; e += NTH) {
-        const uint32_t k = ksigns((uint32_t)(e >> 3));
-        uint32_t w[4];
+    for (int e = tid; e < 128 * 16; e += NTH) {
+        const uint32_t k = ksigns((uint32_t)(e >> 4));
+        uint32_t w[2];
 #pragma unroll
-        for (int i = 0; i < 4; i++) w[i] = (((k >> (2 * i)) & 1u) << 15) | (((k >> (2 * i + 1)) & 1u) << 31);
-        *(uint4 *)(tab + (e << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
+        for (int h = 0; h < 2; h++) {
+            const uint32_t b = k >> (4 * h);
+            w[h] = ((b & 1u) << 15) | (((b >> 1) & 1u) << 31) | (((b >> 2) & 1u) << 14) | (((b >> 3) & 1u) << 30);
+        }
+        *(uint2 *)(tab + (e << 3)) = make_uint2(w[0], w[1]);
     }
 }
 
@@ -100,11 +105,11 @@ __device__ __forceinline__ void grp_tables(uint8_t *tab, int tid) {
 //   IQ2_XXS: a0 = the unit's 4 grid-index bytes, a1 = signs | s << 28; one 16-byte grid read;
 //   IQ3_XXS: g0, g1 = its 8 index bytes, a1 as above; two 8-byte reads of 4-value entries
 //     (lib.rs:312-328);
-// both: one 16-byte sign-mask read (r16 = 16 (j & 7), the lane's replica); finish applies it
-// with XOR.
+// both: one 8-byte sign read (r16 = 8 (j & 15), the lane's replica); finish expands it to the
+// four f16 sign masks and applies them with XOR.
 struct FragRaw {
     uint4 g;
-    uint4 sm;
+    uint2 sm;
     uint2 g2;   // IQ3_XXS: the second 4-value entry
 };
 template <int G>
@@ -115,7 +120,7 @@ template <int G>
 __device__ __forceinline__ void iq2_frag_fetch(const uint8_t *tab, uint32_t a0, uint32_t a1, uint32_t r16, FragRaw &r) {
     const uint32_t ga = __builtin_amdgcn_perm(a0, a1 & 0xF0000000u, 0x0c0c0403u + (G << 8));
     r.g = *(const uint4 *)(tab + GS_GRP_GRID_OFF + ga);
-    r.sm = *(const uint4 *)(tab + sign_off<G>(a1, r16));
+    r.sm = *(const uint2 *)(tab + sign_off<G>(a1, r16));
 }
 template <int G>
 __device__ __forceinline__ void iq3_frag_fetch(const uint8_t *tab, uint32_t g0, uint32_t g1, uint32_t a1, uint32_t r16,
@@ -126,7 +131,7 @@ __device__ __forceinline__ void iq3_frag_fetch(const uint8_t *tab, uint32_t g0, 
     const uint2 lo = *(const uint2 *)(tab + GS_GRP_GRID_OFF + __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + (b0 << 8)));
     r.g2 = *(const uint2 *)(tab + GS_GRP_GRID_OFF + __builtin_amdgcn_perm(gw, hs, 0x0c0c0403u + ((b0 + 1) << 8)));
     r.g = make_uint4(lo.x, lo.y, 0u, 0u);
-    r.sm = *(const uint4 *)(tab + sign_off<G>(a1, r16));
+    r.sm = *(const uint2 *)(tab + sign_off<G>(a1, r16));
 }
 // Load of a wave-uniform address in data no kernel of this launch writes (the CSR offsets and the
 // expert table), through the constant address space: a scalar load, waited on by its own counter
@@ -138,7 +143,9 @@ __device__ __forceinline__ T ld_scalar(const T *p) {
 template <bool IQ3>
 __device__ __forceinline__ h8 frag_finish(const FragRaw &r) {
     const uint4 g = IQ3 ? make_uint4(r.g.x, r.g.y, r.g2.x, r.g2.y) : r.g;
-    return __builtin_bit_cast(h8, make_uint4(g.x ^ r.sm.x, g.y ^ r.sm.y, g.z ^ r.sm.z, g.w ^ r.sm.w));
+    constexpr uint32_t M = 0x80008000u;
+    return __builtin_bit_cast(h8, make_uint4(g.x ^ (r.sm.x & M), g.y ^ ((r.sm.x << 1) & M), g.z ^ (r.sm.y & M),
+                                             g.w ^ ((r.sm.y << 1) & M)));
 }
 
 #define GS_GRP_AV_LOAD(tt, cc) __builtin_bit_cast(h8, *(const uint4 *)(slab + (16 * (tt) + j) * 512 + ((((cc) ^ j)) << 4)))
@@ -215,7 +222,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
         (uint8_t *)__builtin_bit_cast(__attribute__((address_space(3))) uint8_t *, (uint32_t)0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, q = lane >> 4;
-    const uint32_t r16 = (uint32_t)(j & 7) << 4;   // the lane's sign-table replica
+    const uint32_t r16 = (uint32_t)j << 3;   // the lane's sign-table replica
     const int K = a.K, rows = a.rows, nsb = K / 256;
     const int nrb = (rows + RB - 1) / RB;
     const uint32_t rs = (uint32_t)a.row_stride;
