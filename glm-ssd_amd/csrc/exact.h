@@ -25,6 +25,11 @@ __device__ __forceinline__ uint32_t le32(const uint8_t *b, int off) {
     return (uint32_t)b[off] | ((uint32_t)b[off + 1] << 8) | ((uint32_t)b[off + 2] << 16) | ((uint32_t)b[off + 3] << 24);
 }
 // ggml get_scale_min_k4 (lib.rs:87-93): 6-bit scale and min of sub-block j from the 12 packed bytes
+// dl * q - ml of the K-quants with mins (Q2_K, Q4_K, Q5_K) as one fused multiply-add: dl is an f16
+// times a scale of at most 6 bits (at most 17 significant bits) and q has at most 5, so dl * q is
+// exact in f32 and the single rounding of the fma equals lib.rs's rounding of the subtraction
+__device__ __forceinline__ float dq_min(float dl, float q, float ml) { return __builtin_fmaf(dl, q, -ml); }
+
 __device__ __forceinline__ void k4_scale_min(int j, const uint8_t *q, float &sc, float &mn) {
     uint32_t s, m;
     if (j < 4) {
@@ -68,7 +73,7 @@ __device__ __forceinline__ void q2_k(const uint8_t *b, int u, float (&y)[32]) {
     for (int half = 0; half < 2; half++) {
         const uint32_t sc = b[8 * n + 2 * (u & 3) + half];
         const float dl = d * (float)(sc & 0xFu), ml = mn * (float)(sc >> 4);
-        for (int l = 0; l < 16; l++) y[16 * half + l] = dl * (float)((q[l + 16 * half] >> shift) & 3) - ml;
+        for (int l = 0; l < 16; l++) y[16 * half + l] = dq_min(dl, (float)((q[l + 16 * half] >> shift) & 3), ml);
     }
 }
 
@@ -104,7 +109,7 @@ __device__ __forceinline__ void q4_k(const uint8_t *b, int u, float (&y)[32]) {
     k4_scale_min(u, b + 4, sc, mn);
     const float dl = half_at(b, 0) * sc, ml = half_at(b, 2) * mn;
     const uint8_t *q = b + 16 + 32 * jb;
-    for (int l = 0; l < 32; l++) y[l] = dl * (float)((q[l] >> nib) & 0xF) - ml;
+    for (int l = 0; l < 32; l++) y[l] = dq_min(dl, (float)((q[l] >> nib) & 0xF), ml);
 }
 
 // ---- block_q5_K { half d; half dmin; u8 scales[12]; u8 qh[32]; u8 qs[128] } (lib.rs:221-240)
@@ -117,7 +122,7 @@ __device__ __forceinline__ void q5_k(const uint8_t *b, int u, float (&y)[32]) {
     const uint8_t *q = b + 48 + 32 * jb;
     for (int l = 0; l < 32; l++) {
         const uint32_t v = ((q[l] >> nib) & 0xFu) + ((b[16 + l] >> u) & 1u) * 16u;
-        y[l] = dl * (float)v - ml;
+        y[l] = dq_min(dl, (float)v, ml);
     }
 }
 
@@ -196,6 +201,12 @@ __device__ __forceinline__ uint32_t w32(const uint8_t *p, int off) { return *(co
 __device__ __forceinline__ float h16(uint32_t w, int hi) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? w >> 16 : w)); }
 __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)(int)(int8_t)(w >> (8 * i)); }
 __device__ __forceinline__ float ubyte(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
+// a value whose bits the compiler must not track: byte i of it then converts with one
+// v_cvt_f32_ubyte<i> instead of a bit-field extract of the known nibble plus a conversion
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
 
 // Q8_0: unit u = block u of the group (34-byte blocks, so block u starts 2 (u & 1) bytes past a dword)
 __device__ __forceinline__ void q8_0(const uint8_t *p, int u, float (&y)[32]) {
@@ -216,13 +227,15 @@ __device__ __forceinline__ void q4_k(const uint8_t *p, int u, float (&y)[32]) {
     // scale_min_k4 (lib.rs:87-93) on byte j & 3 of the three scale dwords
     const uint32_t sh = 8u * (uint32_t)(u & 3);
     const uint32_t b1 = (w32(p, 4) >> sh) & 0xffu, b2 = (w32(p, 8) >> sh) & 0xffu, b3 = (w32(p, 12) >> sh) & 0xffu;
-    const uint32_t sci = u < 4 ? b1 & 63u : (b3 & 0xfu) | ((b1 >> 6) << 4);
-    const uint32_t mni = u < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
+    // both forms computed and one selected (u varies across the lanes: no divergent branch)
+    const uint32_t sc_lo = b1 & 63u, sc_hi = (b3 & 0xfu) | ((b1 >> 6) << 4);
+    const uint32_t mn_lo = b2 & 63u, mn_hi = (b3 >> 4) | ((b2 >> 6) << 4);
+    const uint32_t sci = u < 4 ? sc_lo : sc_hi, mni = u < 4 ? mn_lo : mn_hi;
     const float dl = h16(dd, 0) * (float)sci, ml = h16(dd, 1) * (float)mni;
     const int nib = 4 * (u & 1);
     for (int k = 0; k < 8; k++) {
-        const uint32_t q = (w32(p, 16 + 32 * (u >> 1) + 4 * k) >> nib) & 0x0f0f0f0fu;
-        for (int i = 0; i < 4; i++) y[4 * k + i] = dl * ubyte(q, i) - ml;
+        const uint32_t q = opaque((w32(p, 16 + 32 * (u >> 1) + 4 * k) >> nib) & 0x0f0f0f0fu);
+        for (int i = 0; i < 4; i++) y[4 * k + i] = dq_min(dl, ubyte(q, i), ml);
     }
 }
 
@@ -237,8 +250,8 @@ __device__ __forceinline__ void q6_k(const uint8_t *p, int u, float (&y)[32]) {
     for (int m = 0; m < 8; m++) {
         const uint32_t lo = (w32(p, 64 * n + 32 * (k & 1) + 4 * m) >> (4 * (k >> 1))) & 0x0f0f0f0fu;
         const uint32_t hi = ((w32(p, 128 + 32 * n + 4 * m) >> (2 * k)) & 0x03030303u) << 4;
-        const uint32_t q = lo | hi;
-        for (int i = 0; i < 4; i++) y[4 * m + i] = (m < 4 ? s0 : s1) * (float)((int)((q >> (8 * i)) & 0xffu) - 32);
+        const uint32_t q = opaque(lo | hi);
+        for (int i = 0; i < 4; i++) y[4 * m + i] = (m < 4 ? s0 : s1) * (ubyte(q, i) - 32.f);
     }
 }
 }  // namespace al

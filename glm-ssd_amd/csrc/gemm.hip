@@ -255,47 +255,57 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
             if (bl > 0) wait_fill(bl);
         }
         // B fragments: units 2q, 2q+1 of this lane's two rows, rounded to f16
-        gh8 bf[GM_NR][2][4];
-#pragma unroll
-        for (int n = 0; n < GM_NR; n++) {
-            const int rr = min(wave * 16 * GM_NR + 16 * n + j, nrows - 1);
+        // (the step that ends past the row, K % 256 != 0, is a workgroup-uniform second path, so
+        // the others carry no masking)
+        // Per unit hu: decode (B fragments of unit 2q + hu, rounded to f16), then the four MFMAs of
+        // each token block that take it (MFMA m takes group m & 3 of unit 2q + (m >> 2)). Each
+        // (full tile, step inside the row) combination is one straight-line block, so the matrix
+        // core runs unit 0's products while the VALU decodes unit 1. A partial tile guards each
+        // token block (a per-MFMA branch serializes each fragment read with its MFMA, so full
+        // tiles have none); the step that ends past the row (K % 256 != 0) zeroes those units.
+        const uint8_t *slab = abuf + buf * ASLAB;
+        auto compute = [&](auto full, auto tail) __attribute__((always_inline)) {
 #pragma unroll
             for (int hu = 0; hu < 2; hu++) {
-                float v[32];
-                if (256 * b + 32 * (2 * q + hu) >= K) {   // past the row (K % 256 != 0): zero weights
+                gh8 bf[GM_NR][4];
 #pragma unroll
-                    for (int e = 0; e < 32; e++) v[e] = 0.f;
-                } else if constexpr (F::PLAIN) {
-                    F::unit(W + (int64_t)(r0 + rr) * rs + (int64_t)256 * b * BB, 2 * q + hu, v);
-                } else {
-                    F::slot_unit((const uint8_t *)__builtin_assume_aligned(rawbuf + buf * RAWB + rr * F::SBP, 4), 2 * q + hu, v);
+                for (int n = 0; n < GM_NR; n++) {
+                    const int rr = min(wave * 16 * GM_NR + 16 * n + j, nrows - 1);
+                    const bool past = decltype(tail)::value && 256 * b + 32 * (2 * q + hu) >= K;
+                    float v[32];
+                    if constexpr (F::PLAIN) {   // straight from memory: nothing is read past the row
+                        if (past) {
+#pragma unroll
+                            for (int e = 0; e < 32; e++) v[e] = 0.f;
+                        } else {
+                            F::unit(W + (int64_t)(r0 + rr) * rs + (int64_t)256 * b * BB, 2 * q + hu, v);
+                        }
+                    } else {   // the LDS slot is always readable: decode, then zero what is past the row
+                        F::slot_unit((const uint8_t *)__builtin_assume_aligned(rawbuf + buf * RAWB + rr * F::SBP, 4), 2 * q + hu, v);
+                    }
+#pragma unroll
+                    for (int g = 0; g < 4; g++) bf[n][g] = past ? gh8{} : to_h8(v + 8 * g);
                 }
 #pragma unroll
-                for (int g = 0; g < 4; g++) bf[n][hu][g] = to_h8(v + 8 * g);
-            }
-        }
-        // contraction: MFMA m takes group m & 3 of unit 2q + (m >> 2)
-        const uint8_t *slab = abuf + buf * ASLAB;
-        // (a full tile contracts without branches: a per-MFMA branch serializes each fragment
-        // read with its MFMA)
-        auto contract = [&](auto full) {
+                for (int g = 0; g < 4; g++) {
+                    const int cc = 8 * q + 4 * hu + g;
+                    gh8 av[4];
 #pragma unroll
-            for (int m = 0; m < 8; m++) {
-                const int cc = 8 * q + m;   // = 8q + 4 (m >> 2) + (m & 3)
-                gh8 av[4];
+                    for (int tt = 0; tt < 4; tt++)
+                        if (decltype(full)::value || tt < ntt) av[tt] = *(const gh8 *)(slab + (16 * tt + j) * 512 + ((cc ^ j) << 4));
 #pragma unroll
-                for (int tt = 0; tt < 4; tt++)
-                    if (decltype(full)::value || tt < ntt) av[tt] = *(const gh8 *)(slab + (16 * tt + j) * 512 + ((cc ^ j) << 4));
+                    for (int tt = 0; tt < 4; tt++)
+                        if (decltype(full)::value || tt < ntt)
 #pragma unroll
-                for (int tt = 0; tt < 4; tt++)
-                    if (decltype(full)::value || tt < ntt)
-#pragma unroll
-                        for (int n = 0; n < GM_NR; n++)
-                            acc[tt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[tt], bf[n][m >> 2][m & 3], acc[tt][n], 0, 0, 0);
+                            for (int n = 0; n < GM_NR; n++)
+                                acc[tt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[tt], bf[n][g], acc[tt][n], 0, 0, 0);
+                }
             }
         };
-        if (ntt == 4) contract(BoolC<true>{});
-        else contract(BoolC<false>{});
+        const bool tail = 256 * (b + 1) > K;   // workgroup-uniform
+        if (ntt == 4 && !tail) compute(BoolC<true>{}, BoolC<false>{});
+        else if (!tail) compute(BoolC<false>{}, BoolC<false>{});
+        else compute(BoolC<false>{}, BoolC<true>{});
         if (more) {
             raw_store(buf ^ 1, b + 1, rv, rx);
             x_store(buf ^ 1, b + 1, xv);
