@@ -404,11 +404,14 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     // wave that sees the count also sees the stores it counts. a.wait_force (set only by the
     // host's test hook) makes the target unreachable, so every wait runs to its limit.
     const uint32_t wlim = a.wait_limit, wadd = a.wait_force ? 0x40000000u : 0u;
+    bool waited = false;   // the last wait found its count short (this wave was ahead)
     auto wait_lds = [&](const uint32_t *c, uint32_t want, bool eq) __attribute__((always_inline)) {
         want += wadd;
+        waited = false;
         for (uint32_t spin = 0;; spin++) {
             const uint32_t v = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             if (eq ? v == want : v >= want) break;
+            waited = true;
             if (spin >= wlim) {   // expired: recorded, and the wave goes on (never hangs)
                 if (lane == 0) __hip_atomic_fetch_or(&gs_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
@@ -424,6 +427,15 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
     };
     auto step = [&](WRegs &wu, WRegs &wl) __attribute__((always_inline)) -> bool {
         wait_slot();
+        // Issue priority follows the lag: every wave stores its share of each slot, so the
+        // workgroup runs at the pace of its slowest wave. A wave that found its slot already
+        // filled is that wave (the others were waiting on it) and takes a higher priority for this
+        // position; one that had to wait drops to the lowest. Without this the waves that issue
+        // their loads later on each SIMD lost the vector-memory arbitration position after
+        // position (phase clocks: 4 of the 8 waves spent 3.6x as long issuing loads, the other 4
+        // waited on them): config 5 783 -> 728 us.
+        if (waited) __builtin_amdgcn_s_setprio(0);
+        else __builtin_amdgcn_s_setprio(2);
         // ---- issue: activations of position +1, weights of position +2 -------------------
         const bool last_sb = b == nsb - 1;
         const bool have1 = !last_sb || has_nxt;
