@@ -296,7 +296,7 @@ def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 
                       wk.p if wk else None, need, s.raw(), C.byref(ms)))
     t = ms.value * 1e-3
     flops = 2.0 * N * rows * K
-    return {"us_per_call": round(ms.value * 1e3, 2), "TFLOPs": round(flops / t / 1e12, 1), "k_split_workspace": need,
+    return {"us_per_call": round(ms.value * 1e3, 2), "TFLOPs": round(flops / t / 1e12, 1), "workspace_bytes": need,
             "frac_mfma_f16_peak": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
             "weight_GBps": round(raw.nbytes / t / 1e9, 1), "tokens": N, "rotated_copies": n}
 

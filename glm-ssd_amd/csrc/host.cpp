@@ -6,6 +6,7 @@
 // validation mirrors the reference's (crates/cuda/kernels/quants.cu:223-256,378-409,
 // gemm.cu:107-152) and returns hipErrorInvalidValue without launching on bad input.
 #include <hip/hip_runtime_api.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
 #include <atomic>
@@ -52,6 +53,17 @@ struct DeviceCtx {
     hipError_t init_err = hipSuccess;
     std::map<std::pair<std::string, int>, int> occ;  // (kernel, lds) -> blocks per CU
     std::vector<void *> wait_flags;   // gs_wait_expired of each code object that has one
+    // GEMM library path (gs_gemm_ex at N >= GS_GEMM_LIB_MIN_N): the device's hipBLASLt handle,
+    // created on first use, and one plan per problem shape
+    std::mutex lt_mu;
+    hipblasLtHandle_t lt = nullptr;
+    bool lt_failed = false;
+    struct LtPlan {
+        hipblasLtMatmulDesc_t desc;
+        hipblasLtMatrixLayout_t la, lb, lc;
+        hipblasLtMatmulAlgo_t algo;
+    };
+    std::map<std::vector<int64_t>, LtPlan> lt_plans;
 };
 
 std::mutex g_mu;
@@ -657,6 +669,87 @@ size_t gemm_part_bytes(int nks, int rows, int N, int n_batch) {
     return nks > 1 ? (size_t)nks * n_batch * N * rows * sizeof(float) : 0;
 }
 
+// ---- library path: dequantize to f16, convert X to f16, contract on hipBLASLt -----------------
+// At N >= GS_GEMM_LIB_MIN_N tokens, with a workspace, gs_gemm_ex writes the weights once as f16
+// (the same f16(dequant) values the tile kernel rounds to), converts X to f16 (same rounding) and
+// runs the contraction as a plain f16 x f16 -> f32 GEMM (f32 accumulation) in hipBLASLt: Q4_K
+// 12288 x 4096 x 512 tokens 126 us in the tile kernel against about 82 us this way (dequant
+// pass ~24 us, conversion ~3 us, library GEMM ~55 us). Below that N the dequant pass costs more
+// than it saves. The algorithm is the library heuristic's first choice for the shape (fixed per
+// shape, so results repeat call to call).
+constexpr int GS_GEMM_LIB_MIN_N = 384;
+constexpr size_t GS_GEMM_LT_WS = (size_t)32 << 20;
+size_t a256(size_t n) { return (n + 255) & ~(size_t)255; }
+size_t gemm_lib_bytes(int K, int rows, int N) {
+    return a256((size_t)rows * K * 2) + a256((size_t)N * K * 2) + GS_GEMM_LT_WS;
+}
+// the plan for this shape; nullptr if the library is unavailable (the caller then runs the tiles)
+DeviceCtx::LtPlan *lt_plan(DeviceCtx *c, int K, int rows, int N, int64_t y_stride) {
+    std::lock_guard<std::mutex> lk(c->lt_mu);
+    if (c->lt_failed) return nullptr;
+    if (!c->lt && hipblasLtCreate(&c->lt) != HIPBLAS_STATUS_SUCCESS) {
+        c->lt = nullptr;
+        c->lt_failed = true;
+        return nullptr;
+    }
+    const std::vector<int64_t> key{K, rows, N, y_stride};
+    auto it = c->lt_plans.find(key);
+    if (it != c->lt_plans.end()) return &it->second;
+    // column-major view: Y (rows x N, ld y_stride) = W16^T (W16: K x rows, ld K) * X16 (K x N, ld K)
+    DeviceCtx::LtPlan P;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    bool ok = hipblasLtMatmulDescCreate(&P.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&P.la, HIP_R_16F, K, rows, K) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&P.lb, HIP_R_16F, K, N, K) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&P.lc, HIP_R_32F, rows, N, y_stride) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    size_t ws = GS_GEMM_LT_WS;
+    ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulHeuristicResult_t r;
+    int nr = 0;
+    ok = ok && hipblasLtMatmulAlgoGetHeuristic(c->lt, P.desc, P.la, P.lb, P.lc, P.lc, pref, 1, &r, &nr) ==
+                   HIPBLAS_STATUS_SUCCESS && nr > 0;
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    (void)hipGetLastError();
+    if (!ok) return nullptr;   // no algorithm for this shape: the tiles run it
+    P.algo = r.algo;
+    return &(c->lt_plans[key] = P);
+}
+// -1: not taken (the tile kernel runs the problem); otherwise the HIP status of the launches
+int gemm_lib(DeviceCtx *c, int ty, const uint8_t *W, int K, int rows, const float *X, int64_t x_stride, float *Y,
+             int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs, void *work,
+             hipStream_t s) {
+    DeviceCtx::LtPlan *P = lt_plan(c, K, rows, N, y_stride);
+    if (!P) return -1;
+    uint8_t *w16 = (uint8_t *)work;
+    uint16_t *x16 = (uint16_t *)(w16 + a256((size_t)rows * K * 2));
+    void *lws = (uint8_t *)x16 + a256((size_t)N * K * 2);
+    const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
+    for (int z = 0; z < n_batch; z++) {
+        const void *a16 = w16;
+        if (ty == GS_F16) {   // already f16 (contiguous rows): the library reads it in place
+            a16 = W + z * w_bs;
+        } else {
+            const int e = dequant(ty, W + z * w_bs, (int64_t)rows * K, w16, s, "f16");
+            if (e != hipSuccess) return e;
+        }
+        int e;
+        CvtArgs cv{X + z * x_bs, x16, x_stride, K, N};
+        const int64_t thr = (int64_t)N * (K / 8);
+        e = launch("gs_k_rows_to_f16", dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, cv);
+        if (e != hipSuccess) return e;
+        float *y = Y + z * y_bs;
+        if (hipblasLtMatmul(c->lt, P->desc, &alpha, a16, P->la, x16, P->lb, &beta, y, P->lc, y, P->lc, &P->algo, lws,
+                            GS_GEMM_LT_WS, s) != HIPBLAS_STATUS_SUCCESS)
+            return hipErrorLaunchFailure;
+    }
+    return hipSuccess;
+}
+
 int gemm_impl(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
               int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs,
               void *work, size_t work_bytes, void *s) {
@@ -700,6 +793,17 @@ int gemm_impl(int ty, const void *W, int64_t row_stride, int K, int rows, const 
     hipError_t e;
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
+    // many tokens and a workspace for the f16 operands: dequantize + library GEMM (contiguous rows;
+    // the block formats whose tile decode costs more than a dequant pass, and F16 weights as they
+    // are; Q8_0's tile decode is cheap enough that the tile kernel stays faster: 46 against 49 us
+    // at 4096 x 4096 x 512)
+    const bool lib_ty = ty != GS_Q8_0 && ty != GS_F32 && ty != GS_BF16;
+    if (work && lib_ty && N >= GS_GEMM_LIB_MIN_N && row_stride == (int64_t)(K / qk) * bb && y_stride >= rows &&
+        work_bytes >= gemm_lib_bytes(K, rows, N) && aligned16(work)) {
+        const int r = gemm_lib(c, ty, (const uint8_t *)W, K, rows, X, x_stride, Y, y_stride, N, accumulate, n_batch, w_bs,
+                               x_bs, y_bs, work, (hipStream_t)s);
+        if (r >= 0) return r;
+    }
     const std::string name = "gs_k_gemm_" + std::to_string(ty);
     // K split only into the caller's workspace: each slice writes its f32 partial tile there and
     // gs_k_gemm_reduce sums the slices in slice order into Y (a fixed order, so the result is
@@ -736,6 +840,7 @@ GS_EXPORT int gs_gemm_workspace(int K, int rows, int N, int n_batch, size_t *byt
     if (!c) return e;
     int ksb = 0;
     *bytes = rows == 0 ? 0 : gemm_part_bytes(gemm_slices(c, K, rows, N, n_batch, &ksb), rows, N, n_batch);
+    if (rows > 0 && N >= GS_GEMM_LIB_MIN_N) *bytes = std::max(*bytes, gemm_lib_bytes(K, rows, N));
     return 0;
 }
 

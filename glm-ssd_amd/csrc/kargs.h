@@ -63,6 +63,16 @@ struct QuantArgs {
     int64_t n_blocks;
 };
 
+// f32 rows -> compact f16 rows (round to nearest even): N rows of K values, source row stride
+// x_stride (elements), destination rows K apart (the GEMM library path's activations)
+struct CvtArgs {
+    const float *x;
+    uint16_t *y;
+    int64_t x_stride;
+    int K;    // a multiple of 8
+    int N;
+};
+
 struct EltArgs {
     const float *a;
     const float *b;

@@ -811,7 +811,12 @@ template <int QKB, int BB, void (*DEC)(const uint8_t *, int, float (&)[32])>
 __device__ __forceinline__ int dequant_unit(const uint8_t *src, int64_t u, int64_t n, float (&v)[32]) {
     if (QKB >= 32) {
         constexpr int UPB = QKB / 32;
-        DEC(src + (u / UPB) * BB, (int)(u % UPB), v);
+        const uint8_t *blk = src + (u / UPB) * BB;
+        // whole-dword reads (unaligned global loads) where a dword decoder exists: the same values
+        if constexpr (DEC == &exact::q8_0) exact::al::q8_0(blk, 0, v);
+        else if constexpr (DEC == &exact::q4_k) exact::al::q4_k(blk, (int)(u % UPB), v);
+        else if constexpr (DEC == &exact::q6_k) exact::al::q6_k(blk, (int)(u % UPB), v);
+        else DEC(blk, (int)(u % UPB), v);
         return 32;
     }
     const uint8_t *base = src + u * 32 * BB;
@@ -891,6 +896,18 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_axpy(EltArgs a) {   // y 
 extern "C" __global__ void __launch_bounds__(256) gs_k_f32_to_f16(EltArgs a) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < a.n) ((uint16_t *)a.y)[i] = (uint16_t)f2h(a.a[i]);
+}
+// 8 values per thread: two 16-byte loads, one 16-byte store (x rows 16-byte aligned, K % 8 == 0)
+extern "C" __global__ void __launch_bounds__(256) gs_k_rows_to_f16(CvtArgs a) {
+    typedef float f8 __attribute__((ext_vector_type(8)));
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    const int64_t per = a.K / 8, i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= per * a.N) return;
+    const int64_t n = i / per, c = i - n * per;
+    const float4 *src = (const float4 *)(a.x + n * a.x_stride + 8 * c);
+    const float4 u = src[0], v = src[1];
+    const f8 f = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+    *(h8 *)(a.y + n * a.K + 8 * c) = __builtin_convertvector(f, h8);
 }
 extern "C" __global__ void __launch_bounds__(256) gs_k_saxpy(EltArgs a) {  // y = s*x + y
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

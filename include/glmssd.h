@@ -134,13 +134,21 @@ int gs_axpy(float *y, const float *x, float a, int64_t n, void *s);
  * Like the reference, allocates nothing and never synchronizes. */
 int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
             int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs, void *s);
-/* Additive (no counterpart in the reference): gs_gemm with a caller-owned workspace. Problems with
- * few 128-row x 64-token tiles (small N, few rows) then split K across workgroups: each slice
- * writes its f32 partial tile into `work` and the slices are added in a fixed order (results are
- * reproducible; they differ from gs_gemm only in f32 summation order). gs_gemm_workspace gives the
- * bytes a problem needs on the current device (0: no split, `work` unused; at most CUs x 32 KB).
+/* Additive (no counterpart in the reference): gs_gemm with a caller-owned workspace, used two ways.
+ * (1) Problems with few 128-row x 64-token tiles (small N, few rows) split K across workgroups:
+ * each slice writes its f32 partial tile into `work` and the slices are added in a fixed order.
+ * (2) At N >= 384 tokens, for every weight type but Q8_0, F32 and BF16 and rows stored back to
+ * back (row_stride = bytes of a row), the weights are dequantized into `work` as f16 (F16 weights
+ * are used in place), X is converted to f16 there too, and the product runs as an f16 x f16 -> f32
+ * GEMM in hipBLASLt (the heuristic's first algorithm for the shape, so a shape always takes the
+ * same one). Both round the operands to f16 exactly as gs_gemm does and accumulate in f32; results
+ * repeat call to call and differ from gs_gemm only in f32 summation order. gs_gemm_workspace gives
+ * the bytes a problem needs on the current device (0: `work` unused; for (2) rows*K*2 + N*K*2
+ * rounded up to 256 each, plus 32 MiB of library workspace).
  * work: 16-byte aligned, >= that many bytes, not used by another call in flight; work == NULL
- * runs as gs_gemm. Allocates nothing and never synchronizes. */
+ * (or a smaller workspace) runs as gs_gemm. Never synchronizes; allocates nothing itself (the first
+ * call of kind (2) on a device creates that device's hipBLASLt handle, kept until the process
+ * ends). */
 int gs_gemm_workspace(int K, int rows, int N, int n_batch, size_t *bytes);
 int gs_gemm_ex(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
                int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs,

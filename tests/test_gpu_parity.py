@@ -397,7 +397,10 @@ def test_gemm_full_grid_and_k_split(stream):
     e = _gemm_case(T.Q8_0, 512, 2176, 512, stream, 21)
     say(f"gemm Q8_0 2176x512 N=512 (full grid): rel-L2 {e:.2e}")
     assert e <= GEMM_REL
-    assert G.ops.gemm_workspace(512, 2176, 512) == 0
+    # a full grid below the library path's token count needs no workspace; at N >= 384 the
+    # workspace holds the f16 operands of the library path
+    assert G.ops.gemm_workspace(512, 4352, 256) == 0
+    assert G.ops.gemm_workspace(512, 2176, 512) >= 2176 * 512 * 2 + 512 * 512 * 2
     ty, K, rows, N = T.IQ2_XXS, 4096, 1536, 64
     rb = G.row_bytes(ty, K)
     raw = O.Rng(22).random_blocks(ty, rows * K)
@@ -444,6 +447,62 @@ def test_gemm_ex_accumulate_and_batches(stream):
     got = dy.download(np.float32, nb * N * rows, stream).reshape(nb, N, rows).astype(np.float64) - y0
     for z in range(nb):
         assert rel_l2(got[z], wants[z]) <= GEMM_REL
+
+
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q5_K, T.Q6_K, T.IQ2_XXS, T.F16, T.Q8_0])
+def test_gemm_ex_library_path(ty, stream):
+    # N >= 384 tokens with the workspace gs_gemm_workspace asks for: the weights are dequantized
+    # to f16 in the workspace, X converted to f16, and the contraction runs in the GEMM library.
+    # Against the oracle's f16-operand product (f32 accumulation order differs) with accumulate,
+    # two batches, a strided Y; and two calls give the same bits. (Q8_0 keeps the tile kernel at
+    # every N: the same checks.)
+    K, rows, N, nb, ys = 512, 200, 400, 2, 203
+    rb = G.row_bytes(ty, K)
+    if ty == T.F16:
+        raw = np.random.default_rng(ty).standard_normal(nb * rows * K).astype(np.float16).view(np.uint8)
+    else:
+        raw = O.Rng(7 * ty).random_blocks(ty, nb * rows * K)
+    X = np.random.default_rng(ty + 1).standard_normal((nb, N, K)).astype(np.float32)
+    wants = [O.gemv(ty, raw[z * rows * rb:(z + 1) * rows * rb], rb, K, rows, X[z], B=N, act="f16", nthreads=8)
+             for z in range(nb)]
+    y0 = (np.random.default_rng(ty + 2).standard_normal((nb, N, ys)) * np.std(wants[0])).astype(np.float32)
+    need = G.ops.gemm_workspace(K, rows, N, nb)
+    assert need >= rows * K * 2 + N * K * 2   # holds the f16 operands
+    dw, dx, wk = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(need)
+    outs = []
+    for rep in range(2):
+        dy = G.DeviceBuffer.from_array(y0)
+        G.ops.gemm_ex(ty, dw, rb, K, rows, dx, K, dy, ys, N, True, nb, rows * rb, N * K, N * ys, wk, need, stream)
+        outs.append(dy.download(np.float32, nb * N * ys, stream).reshape(nb, N, ys))
+    assert np.array_equal(outs[0], outs[1])
+    got = outs[0]
+    assert np.array_equal(got[:, :, rows:], y0[:, :, rows:])   # padding columns untouched
+    for z in range(nb):
+        e = rel_l2(got[z, :, :rows].astype(np.float64) - y0[z, :, :rows], wants[z])
+        say(f"gemm_ex library path {G.TYPE_NAMES[ty]} batch {z}: rel-L2 {e:.2e}")
+        assert e <= GEMM_REL
+
+
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q6_K, T.IQ2_XXS, T.Q5_K, T.Q2_K, T.Q3_K, T.IQ4_XS, T.IQ3_XXS, T.IQ2_S])
+def test_gemm_ex_library_weights_bit_exact(ty, stream):
+    # the library path's weights: X = the identity (N = K = 512 tokens), so Y[n][r] is exactly
+    # the f16 rounding of weight (r, n), bit for bit against the oracle's dequantization
+    K, rows = 512, 70
+    rb = G.row_bytes(ty, K)
+    raw = O.Rng(3 * ty + 2).random_blocks(ty, rows * K)
+    with np.errstate(over="ignore", invalid="ignore"):
+        w16 = O.dequantize(ty, raw, rows * K).reshape(rows, K).astype(np.float16)
+    ok = np.all(np.isfinite(w16), axis=1)
+    assert ok.mean() > 0.5
+    X = np.eye(K, dtype=np.float32)
+    need = G.ops.gemm_workspace(K, rows, K, 1)
+    dw, dx, dy, wk = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(K * rows * 4), G.DeviceBuffer(need)
+    G.ops.gemm_ex(ty, dw, rb, K, rows, dx, K, dy, rows, K, False, 1, 0, 0, 0, wk, need, stream)
+    got = dy.download(np.float32, K * rows, stream).reshape(K, rows).T
+    want = w16.astype(np.float32) + np.float32(0)
+    bad = np.count_nonzero(got[ok].view(np.uint32) != want[ok].view(np.uint32))
+    say(f"gemm_ex library weights {G.TYPE_NAMES[ty]}: {ok.sum()} finite rows, {bad} mismatching elements")
+    assert bad == 0
 
 
 def test_gemm_accumulate_strides_and_partial_superblock(stream):
