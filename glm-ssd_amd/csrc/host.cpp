@@ -362,7 +362,7 @@ GS_EXPORT int gs_saxpy(int n, float a, const float *x, float *y, void *s) {
 static int dequant(int ty, const void *src, int64_t n, void *dst, void *s, const char *suffix) {
     int qk, bb;
     if (n <= 0 || n % 8 != 0 || !geometry(ty, qk, bb) || n % ggml_block_elems(ty) != 0) return hipErrorInvalidValue;
-    DequantArgs a{(const uint8_t *)src, dst, n, (n + 31) / 32, aligned16(dst)};
+    DequantArgs a{(const uint8_t *)src, dst, n, (n + 31) / 32, aligned16(dst), 0, nullptr, nullptr, 0, 0, 0};
     const std::string name = std::string("gs_k_dequant_") + suffix + "_" + std::to_string(ty);
     return launch(name, dim3((unsigned)((a.n_units + 255) / 256)), dim3(256), 0, (hipStream_t)s, a);
 }
@@ -731,16 +731,20 @@ int gemm_lib(DeviceCtx *c, int ty, const uint8_t *W, int K, int rows, const floa
     const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
     for (int z = 0; z < n_batch; z++) {
         const void *a16 = w16;
+        const int64_t xthr = (int64_t)N * (K / 4);   // activation pieces of 4 values
+        int e;
         if (ty == GS_F16) {   // already f16 (contiguous rows): the library reads it in place
             a16 = W + z * w_bs;
+            CvtArgs cv{X + z * x_bs, x16, x_stride, K, N};
+            e = launch("gs_k_rows_to_f16", dim3((unsigned)((xthr + 255) / 256)), dim3(256), 0, s, cv);
         } else {
-            const int e = dequant(ty, W + z * w_bs, (int64_t)rows * K, w16, s, "f16");
-            if (e != hipSuccess) return e;
+            // one launch: the weight units' blocks, then the activation conversion's blocks
+            const int64_t n = (int64_t)rows * K;
+            DequantArgs d{W + z * w_bs, w16, n, (n + 31) / 32, 1, 0, X + z * x_bs, x16, x_stride, K, N};
+            d.w_blocks = (int)((d.n_units + 255) / 256);
+            const std::string name = "gs_k_dequant_f16_" + std::to_string(ty);
+            e = launch(name, dim3((unsigned)(d.w_blocks + (xthr + 255) / 256)), dim3(256), 0, s, d);
         }
-        int e;
-        CvtArgs cv{X + z * x_bs, x16, x_stride, K, N};
-        const int64_t thr = (int64_t)N * (K / 8);
-        e = launch("gs_k_rows_to_f16", dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, cv);
         if (e != hipSuccess) return e;
         float *y = Y + z * y_bs;
         if (hipblasLtMatmul(c->lt, P->desc, &alpha, a16, P->la, x16, P->lb, &beta, y, P->lc, y, P->lc, &P->algo, lws,

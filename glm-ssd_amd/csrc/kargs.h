@@ -48,12 +48,20 @@ struct StreamArgs {
 };
 
 // Whole-tensor dequantization
+struct CvtArgs;
 struct DequantArgs {
     const uint8_t *src;
     void *dst;
     int64_t n;          // elements
     int64_t n_units;    // 32-element units (the last one may be partial for plain types)
     int aligned;        // dst is 16-byte aligned (vector stores)
+    // f16 only: blocks from w_blocks on convert f32 rows to f16 instead (the GEMM library path's
+    // activations, cvt_*: as CvtArgs); cvt_n == 0: none
+    int w_blocks;
+    const float *cvt_x;
+    uint16_t *cvt_y;
+    int64_t cvt_x_stride;
+    int cvt_K, cvt_n;
 };
 
 // q8_1 quantization of f32 rows: out = n/32 blocks of {f16 d; f16 s; int8 qs[32]}
@@ -69,7 +77,7 @@ struct CvtArgs {
     const float *x;
     uint16_t *y;
     int64_t x_stride;
-    int K;    // a multiple of 8
+    int K;    // a multiple of 4
     int N;
 };
 

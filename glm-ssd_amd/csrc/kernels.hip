@@ -830,6 +830,17 @@ __device__ __forceinline__ int dequant_unit(const uint8_t *src, int64_t u, int64
     }
     return cnt;
 }
+// piece i (4 values) of the f32 -> f16 row conversion: one 16-byte load, one 8-byte store, so the
+// lanes of a wave read 1 KB and write 512 bytes back to back (rows 16-byte aligned, K % 4 == 0)
+__device__ __forceinline__ void rows_to_f16(const float *x, uint16_t *y, int64_t x_stride, int K, int N, int64_t i) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const int64_t per = K / 4;
+    if (i >= per * N) return;
+    const int64_t n = i / per, c = i - n * per;
+    const f4v f = *(const f4v *)(x + n * x_stride + 4 * c);
+    *(h4 *)(y + n * K + 4 * c) = __builtin_convertvector(f, h4);
+}
 #define GS_DEQ_KERNEL(TY, QKB, BB, DEC)                                                          \
     extern "C" __global__ void __launch_bounds__(256) gs_k_dequant_f32_##TY(DequantArgs a) {    \
         const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;                        \
@@ -845,20 +856,43 @@ __device__ __forceinline__ int dequant_unit(const uint8_t *src, int64_t u, int64
         }                                                                                       \
     }                                                                                           \
     extern "C" __global__ void __launch_bounds__(256) gs_k_dequant_f16_##TY(DequantArgs a) {    \
+        __shared__ uint4 tr[256 * 4];   /* per wave 64 units x 64 bytes: the store transpose */    \
+        if (a.cvt_n && (int)blockIdx.x >= a.w_blocks) {   /* the activation blocks */            \
+            rows_to_f16(a.cvt_x, a.cvt_y, a.cvt_x_stride, a.cvt_K, a.cvt_n,                      \
+                        (int64_t)(blockIdx.x - a.w_blocks) * blockDim.x + threadIdx.x);          \
+            return;                                                                             \
+        }                                                                                       \
         const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;                        \
-        if (u >= a.n_units) return;                                                             \
+        const int lane = threadIdx.x & 63;                                                       \
+        const int64_t u0 = u - lane;   /* the wave's first unit */                               \
         float v[32];                                                                            \
-        const int cnt = dequant_unit<QKB, BB, DEC>(a.src, u, a.n, v);                           \
+        const int cnt = u < a.n_units ? dequant_unit<QKB, BB, DEC>(a.src, u, a.n, v) : 0;       \
         /* opaque to the optimizer: the f32 value (and the sign of a zero) reaches the single   \
            f32 -> f16 rounding unchanged */                                                     \
         for (int i = 0; i < 32; i++) asm volatile("" : "+v"(v[i]));                             \
+        uint4 h[4];                                                                             \
+        for (int i = 0; i < 4; i++)                                                             \
+            h[i] = make_uint4(f2h(v[8 * i]) | (f2h(v[8 * i + 1]) << 16), f2h(v[8 * i + 2]) | (f2h(v[8 * i + 3]) << 16), \
+                              f2h(v[8 * i + 4]) | (f2h(v[8 * i + 5]) << 16), f2h(v[8 * i + 6]) | (f2h(v[8 * i + 7]) << 16)); \
+        if (a.aligned && u0 + 64 <= a.n_units && (QKB >= 32 || 32 * (u0 + 64) <= a.n)) {        \
+            /* whole wave of full units: each lane's 64 bytes through LDS, then 16-byte pieces    \
+               in address order, so every store instruction writes 1 KB back to back */           \
+            uint4 *w = tr + (threadIdx.x >> 6) * 256;                                            \
+            for (int i = 0; i < 4; i++) w[4 * lane + ((i + lane) & 3)] = h[i];                  \
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");                      \
+            __builtin_amdgcn_wave_barrier();                                                    \
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");                      \
+            uint4 *d = (uint4 *)((uint16_t *)a.dst + 32 * u0);                                   \
+            for (int j = 0; j < 4; j++) {                                                       \
+                const int c = 64 * j + lane, src_lane = c >> 2, piece = c & 3;                   \
+                d[c] = w[4 * src_lane + ((piece + src_lane) & 3)];                              \
+            }                                                                                   \
+            return;                                                                             \
+        }                                                                                       \
+        if (cnt == 0) return;                                                                   \
         uint16_t *d = (uint16_t *)a.dst + 32 * u;                                               \
         if (cnt == 32 && a.aligned) {                                                           \
-            for (int i = 0; i < 4; i++)                                                         \
-                ((uint4 *)d)[i] = make_uint4(f2h(v[8 * i]) | (f2h(v[8 * i + 1]) << 16),           \
-                                             f2h(v[8 * i + 2]) | (f2h(v[8 * i + 3]) << 16),       \
-                                             f2h(v[8 * i + 4]) | (f2h(v[8 * i + 5]) << 16),       \
-                                             f2h(v[8 * i + 6]) | (f2h(v[8 * i + 7]) << 16));      \
+            for (int i = 0; i < 4; i++) ((uint4 *)d)[i] = h[i];                                   \
         } else {                                                                                \
             for (int i = 0; i < cnt; i++) d[i] = (uint16_t)f2h(v[i]);                           \
         }                                                                                       \
@@ -897,17 +931,8 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_f32_to_f16(EltArgs a) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < a.n) ((uint16_t *)a.y)[i] = (uint16_t)f2h(a.a[i]);
 }
-// 8 values per thread: two 16-byte loads, one 16-byte store (x rows 16-byte aligned, K % 8 == 0)
 extern "C" __global__ void __launch_bounds__(256) gs_k_rows_to_f16(CvtArgs a) {
-    typedef float f8 __attribute__((ext_vector_type(8)));
-    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-    const int64_t per = a.K / 8, i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= per * a.N) return;
-    const int64_t n = i / per, c = i - n * per;
-    const float4 *src = (const float4 *)(a.x + n * a.x_stride + 8 * c);
-    const float4 u = src[0], v = src[1];
-    const f8 f = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-    *(h8 *)(a.y + n * a.K + 8 * c) = __builtin_convertvector(f, h8);
+    rows_to_f16(a.x, a.y, a.x_stride, a.K, a.N, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 extern "C" __global__ void __launch_bounds__(256) gs_k_saxpy(EltArgs a) {  // y = s*x + y
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
