@@ -274,9 +274,10 @@ def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 
     return dict(ms=ms.value, bytes=raw.nbytes, gbps=raw.nbytes / (ms.value * 1e-3) / 1e9, copies=n)
 
 
-def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 << 20):
-    """gs_gemm_ex (f16 MFMA tiles; a workspace for the K split where the problem takes one) of N tokens
-    through a rows x K matrix, weight copies rotated."""
+def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 << 20, use_work=True):
+    """gs_gemm_ex of N tokens through a rows x K matrix, weight copies rotated, with the workspace
+    gs_gemm_workspace asks for (K split of small problems; at N >= 384 the f16 dequant + library
+    GEMM path); use_work=False: no workspace, i.e. plain gs_gemm's f16 MFMA tiles."""
     import glmssd as G
     rng = np.random.default_rng(seed)
     raw = make(rng, rows, K)
@@ -289,7 +290,7 @@ def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 
     ptrs = (C.c_void_p * n)(*[buf.p.value + i * raw.nbytes for i in range(n)])
     x = G.DeviceBuffer.from_array(rng.standard_normal(N * K).astype(np.float32), s)
     y = G.DeviceBuffer(N * rows * 4)
-    need = G.ops.gemm_workspace(K, rows, N)
+    need = G.ops.gemm_workspace(K, rows, N) if use_work else 0
     wk = G.DeviceBuffer(need) if need else None
     ms = C.c_float()
     G.check(L.bn_gemm(ty, C.cast(ptrs, C.c_void_p), n, G.row_bytes(ty, K), K, rows, x.p, y.p, N, steps, warmup,
@@ -439,10 +440,16 @@ def main():
             log(f"config1 B={B}: {rb['ms'] * 1e3:.2f} us, {rb['gbps']:.1f} GB/s")
         from glmssd import synth as S
         iq = lambda rng, rows, K: S.random_blocks(rng, G.GgmlType.IQ2_XXS, rows * K, 0.02, [0])
-        for name, ty, rows, K, N, mk in [("gemm_q4_k_k4096_rows12288_N512", G.GgmlType.Q4_K, 12288, 4096, 512, S.q4_k_matrix),
-                                         ("gemm_q8_0_k4096_rows4096_N512", G.GgmlType.Q8_0, 4096, 4096, 512, S.q8_0_matrix),
-                                         ("gemm_iq2_xxs_k4096_rows1536_N64", G.GgmlType.IQ2_XXS, 1536, 4096, 64, iq)]:
-            r = run_gemm(L, s, ty, rows, K, N, mk, max(20, args.steps // 5), max(5, args.warmup // 5), 9)
+        q6 = lambda rng, rows, K: S.q6_k_matrix(rng, rows, K)
+        for name, ty, rows, K, N, mk, uw in [
+                ("gemm_q4_k_k4096_rows12288_N512", G.GgmlType.Q4_K, 12288, 4096, 512, S.q4_k_matrix, True),
+                ("gemm_q4_k_k4096_rows12288_N512_tiles", G.GgmlType.Q4_K, 12288, 4096, 512, S.q4_k_matrix, False),
+                ("gemm_q6_k_k12288_rows4096_N512", G.GgmlType.Q6_K, 4096, 12288, 512, q6, True),
+                ("gemm_q8_0_k4096_rows4096_N512", G.GgmlType.Q8_0, 4096, 4096, 512, S.q8_0_matrix, True),
+                ("gemm_iq2_xxs_k4096_rows1536_N64", G.GgmlType.IQ2_XXS, 1536, 4096, 64, iq, True)]:
+            r = run_gemm(L, s, ty, rows, K, N, mk, max(20, args.steps // 5), max(5, args.warmup // 5), 9, use_work=uw)
+            r["path"] = ("f16 dequant + hipBLASLt" if uw and N >= 384 and ty != G.GgmlType.Q8_0 else
+                         "f16 MFMA tiles" + (" (K split)" if uw and N < 384 and r["workspace_bytes"] else ""))
             secondary[name] = r
             log(f"{name}: {r}")
         rc = run_read_ceiling(L, s, [17825792, 25952256, 28311552, 38928384, 41287680, 1 << 30], args.steps,
