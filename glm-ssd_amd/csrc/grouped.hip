@@ -633,11 +633,30 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_rows_f16(RowsQArgs a) {
     if (row >= a.nrows) return;
     const int n8 = a.K / 8;
     const float4 *src = (const float4 *)(a.x + (int64_t)row * a.x_stride);
+    uint4 *dst = (uint4 *)(a.out + (int64_t)row * a.K);
+    // rows of up to 64 x RQ 8-value pieces (K <= 4096) stay in registers between the max and the
+    // conversion, every load issued before the first is needed; longer rows are read twice
+    constexpr int RQ = 8;
+    float4 r0[RQ], r1[RQ];
     float amax = 0.f;
-    for (int u = lane; u < n8; u += 64) {
-        const float4 f0 = src[2 * u], f1 = src[2 * u + 1];
-        amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(f0.x), fabsf(f0.y)), fmaxf(fabsf(f0.z), fabsf(f0.w))),
-                                 fmaxf(fmaxf(fabsf(f1.x), fabsf(f1.y)), fmaxf(fabsf(f1.z), fabsf(f1.w)))));
+    const bool held = n8 <= 64 * RQ;
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RQ; i++) {
+            const int u = min(lane + 64 * i, n8 - 1);   // clamped: re-reads a valid piece
+            r0[i] = src[2 * u];
+            r1[i] = src[2 * u + 1];
+        }
+#pragma unroll
+        for (int i = 0; i < RQ; i++)
+            amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(r0[i].x), fabsf(r0[i].y)), fmaxf(fabsf(r0[i].z), fabsf(r0[i].w))),
+                                     fmaxf(fmaxf(fabsf(r1[i].x), fabsf(r1[i].y)), fmaxf(fabsf(r1[i].z), fabsf(r1[i].w)))));
+    } else {
+        for (int u = lane; u < n8; u += 64) {
+            const float4 f0 = src[2 * u], f1 = src[2 * u + 1];
+            amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(f0.x), fabsf(f0.y)), fmaxf(fabsf(f0.z), fabsf(f0.w))),
+                                     fmaxf(fmaxf(fabsf(f1.x), fabsf(f1.y)), fmaxf(fabsf(f1.z), fabsf(f1.w)))));
+        }
     }
     amax = wave_max(amax);
     int E = 0;
@@ -645,10 +664,15 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_rows_f16(RowsQArgs a) {
     E -= 15;
     const float down = ldexpf(1.f, -E);
     if (lane == 0) a.scale[row] = ldexpf(1.f, E);
-    uint4 *dst = (uint4 *)(a.out + (int64_t)row * a.K);
-    for (int u = lane; u < n8; u += 64) {
-        const float4 f0 = src[2 * u], f1 = src[2 * u + 1];
+    auto put = [&](int u, const float4 &f0, const float4 &f1) {
         dst[u] = make_uint4(f2h(f0.x * down) | (f2h(f0.y * down) << 16), f2h(f0.z * down) | (f2h(f0.w * down) << 16),
                             f2h(f1.x * down) | (f2h(f1.y * down) << 16), f2h(f1.z * down) | (f2h(f1.w * down) << 16));
+    };
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RQ; i++)
+            if (lane + 64 * i < n8) put(lane + 64 * i, r0[i], r1[i]);
+    } else {
+        for (int u = lane; u < n8; u += 64) put(u, src[2 * u], src[2 * u + 1]);
     }
 }
