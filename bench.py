@@ -448,8 +448,8 @@ def main():
                 ("gemm_q8_0_k4096_rows4096_N512", G.GgmlType.Q8_0, 4096, 4096, 512, S.q8_0_matrix, True),
                 ("gemm_iq2_xxs_k4096_rows1536_N64", G.GgmlType.IQ2_XXS, 1536, 4096, 64, iq, True)]:
             r = run_gemm(L, s, ty, rows, K, N, mk, max(20, args.steps // 5), max(5, args.warmup // 5), 9, use_work=uw)
-            r["path"] = ("f16 dequant + hipBLASLt" if uw and N >= 384 and ty != G.GgmlType.Q8_0 else
-                         "f16 MFMA tiles" + (" (K split)" if uw and N < 384 and r["workspace_bytes"] else ""))
+            r["path"] = ["f16 MFMA tiles", "f16 MFMA tiles (K split)", "f16 dequant + hipBLASLt"][
+                G.ops.gemm_path(ty, K, rows, N, G.row_bytes(ty, K), rows, r["workspace_bytes"])]
             secondary[name] = r
             log(f"{name}: {r}")
         rc = run_read_ceiling(L, s, [17825792, 25952256, 28311552, 38928384, 41287680, 1 << 30], args.steps,

@@ -5,8 +5,9 @@
 // hipModuleLaunchKernel, each with a single by-value argument block (kargs.h). Argument
 // validation mirrors the reference's (crates/cuda/kernels/quants.cu:223-256,378-409,
 // gemm.cu:107-152) and returns hipErrorInvalidValue without launching on bad input.
+#include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
-#include <hipblaslt/hipblaslt.h>
+#include <hipblaslt/hipblaslt.h>   // types only: the library is opened at run time (gemm_lib)
 
 #include <algorithm>
 #include <atomic>
@@ -678,6 +679,43 @@ size_t gemm_part_bytes(int nks, int rows, int N, int n_batch) {
 // than it saves. The algorithm is the library heuristic's first choice for the shape (fixed per
 // shape, so results repeat call to call).
 constexpr int GS_GEMM_LIB_MIN_N = 384;
+// hipBLASLt entry points, from libhipblaslt opened on first use (no link-time dependency: without
+// the library the tiles run every problem)
+struct LtApi {
+    decltype(&hipblasLtCreate) create = nullptr;
+    decltype(&hipblasLtMatmulDescCreate) desc_create = nullptr;
+    decltype(&hipblasLtMatmulDescSetAttribute) desc_set = nullptr;
+    decltype(&hipblasLtMatrixLayoutCreate) layout_create = nullptr;
+    decltype(&hipblasLtMatmulPreferenceCreate) pref_create = nullptr;
+    decltype(&hipblasLtMatmulPreferenceSetAttribute) pref_set = nullptr;
+    decltype(&hipblasLtMatmulPreferenceDestroy) pref_destroy = nullptr;
+    decltype(&hipblasLtMatmulAlgoGetHeuristic) heuristic = nullptr;
+    decltype(&hipblasLtMatmul) matmul = nullptr;
+};
+const LtApi *lt_api() {
+    static LtApi api;
+    static std::once_flag once;
+    static bool ok = false;
+    std::call_once(once, [] {
+        void *h = dlopen("libhipblaslt.so.1", RTLD_NOW | RTLD_LOCAL);
+        if (!h) h = dlopen("libhipblaslt.so", RTLD_NOW | RTLD_LOCAL);
+        if (!h) return;
+#define GS_LT_SYM(field, name) api.field = (decltype(api.field))dlsym(h, #name)
+        GS_LT_SYM(create, hipblasLtCreate);
+        GS_LT_SYM(desc_create, hipblasLtMatmulDescCreate);
+        GS_LT_SYM(desc_set, hipblasLtMatmulDescSetAttribute);
+        GS_LT_SYM(layout_create, hipblasLtMatrixLayoutCreate);
+        GS_LT_SYM(pref_create, hipblasLtMatmulPreferenceCreate);
+        GS_LT_SYM(pref_set, hipblasLtMatmulPreferenceSetAttribute);
+        GS_LT_SYM(pref_destroy, hipblasLtMatmulPreferenceDestroy);
+        GS_LT_SYM(heuristic, hipblasLtMatmulAlgoGetHeuristic);
+        GS_LT_SYM(matmul, hipblasLtMatmul);
+#undef GS_LT_SYM
+        ok = api.create && api.desc_create && api.desc_set && api.layout_create && api.pref_create && api.pref_set &&
+             api.pref_destroy && api.heuristic && api.matmul;
+    });
+    return ok ? &api : nullptr;
+}
 constexpr size_t GS_GEMM_LT_WS = (size_t)32 << 20;
 size_t a256(size_t n) { return (n + 255) & ~(size_t)255; }
 size_t gemm_lib_bytes(int K, int rows, int N) {
@@ -685,9 +723,11 @@ size_t gemm_lib_bytes(int K, int rows, int N) {
 }
 // the plan for this shape; nullptr if the library is unavailable (the caller then runs the tiles)
 DeviceCtx::LtPlan *lt_plan(DeviceCtx *c, int K, int rows, int N, int64_t y_stride) {
+    const LtApi *L = lt_api();
+    if (!L) return nullptr;
     std::lock_guard<std::mutex> lk(c->lt_mu);
     if (c->lt_failed) return nullptr;
-    if (!c->lt && hipblasLtCreate(&c->lt) != HIPBLAS_STATUS_SUCCESS) {
+    if (!c->lt && L->create(&c->lt) != HIPBLAS_STATUS_SUCCESS) {
         c->lt = nullptr;
         c->lt_failed = true;
         return nullptr;
@@ -698,26 +738,33 @@ DeviceCtx::LtPlan *lt_plan(DeviceCtx *c, int K, int rows, int N, int64_t y_strid
     // column-major view: Y (rows x N, ld y_stride) = W16^T (W16: K x rows, ld K) * X16 (K x N, ld K)
     DeviceCtx::LtPlan P;
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    bool ok = hipblasLtMatmulDescCreate(&P.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatmulDescSetAttribute(P.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatrixLayoutCreate(&P.la, HIP_R_16F, K, rows, K) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatrixLayoutCreate(&P.lb, HIP_R_16F, K, N, K) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatrixLayoutCreate(&P.lc, HIP_R_32F, rows, N, y_stride) == HIPBLAS_STATUS_SUCCESS;
+    const hipblasStatus_t S = HIPBLAS_STATUS_SUCCESS;
+    bool ok = L->desc_create(&P.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == S;
+    ok = ok && L->desc_set(P.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == S;
+    ok = ok && L->desc_set(P.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == S;
+    ok = ok && L->layout_create(&P.la, HIP_R_16F, K, rows, K) == S;
+    ok = ok && L->layout_create(&P.lb, HIP_R_16F, K, N, K) == S;
+    ok = ok && L->layout_create(&P.lc, HIP_R_32F, rows, N, y_stride) == S;
     hipblasLtMatmulPreference_t pref = nullptr;
     size_t ws = GS_GEMM_LT_WS;
-    ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) ==
-                   HIPBLAS_STATUS_SUCCESS;
+    ok = ok && L->pref_create(&pref) == S;
+    ok = ok && L->pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) == S;
     hipblasLtMatmulHeuristicResult_t r;
     int nr = 0;
-    ok = ok && hipblasLtMatmulAlgoGetHeuristic(c->lt, P.desc, P.la, P.lb, P.lc, P.lc, pref, 1, &r, &nr) ==
-                   HIPBLAS_STATUS_SUCCESS && nr > 0;
-    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    ok = ok && L->heuristic(c->lt, P.desc, P.la, P.lb, P.lc, P.lc, pref, 1, &r, &nr) == S && nr > 0;
+    if (pref) L->pref_destroy(pref);
     (void)hipGetLastError();
     if (!ok) return nullptr;   // no algorithm for this shape: the tiles run it
     P.algo = r.algo;
     return &(c->lt_plans[key] = P);
+}
+// the library path's conditions (gs_gemm_ex; gs_gemm_path reports them)
+bool gemm_lib_eligible(int ty, int K, int rows, int N, int64_t row_stride, int64_t y_stride, size_t work_bytes) {
+    int qk, bb;
+    if (!geometry(ty, qk, bb)) return false;
+    const bool lib_ty = ty != GS_Q8_0 && ty != GS_F32 && ty != GS_BF16;
+    return lib_ty && N >= GS_GEMM_LIB_MIN_N && rows > 0 && row_stride == (int64_t)(K / qk) * bb && y_stride >= rows &&
+           work_bytes >= gemm_lib_bytes(K, rows, N);
 }
 // -1: not taken (the tile kernel runs the problem); otherwise the HIP status of the launches
 int gemm_lib(DeviceCtx *c, int ty, const uint8_t *W, int K, int rows, const float *X, int64_t x_stride, float *Y,
@@ -747,7 +794,7 @@ int gemm_lib(DeviceCtx *c, int ty, const uint8_t *W, int K, int rows, const floa
         }
         if (e != hipSuccess) return e;
         float *y = Y + z * y_bs;
-        if (hipblasLtMatmul(c->lt, P->desc, &alpha, a16, P->la, x16, P->lb, &beta, y, P->lc, y, P->lc, &P->algo, lws,
+        if (lt_api()->matmul(c->lt, P->desc, &alpha, a16, P->la, x16, P->lb, &beta, y, P->lc, y, P->lc, &P->algo, lws,
                             GS_GEMM_LT_WS, s) != HIPBLAS_STATUS_SUCCESS)
             return hipErrorLaunchFailure;
     }
@@ -801,9 +848,7 @@ int gemm_impl(int ty, const void *W, int64_t row_stride, int K, int rows, const 
     // the block formats whose tile decode costs more than a dequant pass, and F16 weights as they
     // are; Q8_0's tile decode is cheap enough that the tile kernel stays faster: 46 against 49 us
     // at 4096 x 4096 x 512)
-    const bool lib_ty = ty != GS_Q8_0 && ty != GS_F32 && ty != GS_BF16;
-    if (work && lib_ty && N >= GS_GEMM_LIB_MIN_N && row_stride == (int64_t)(K / qk) * bb && y_stride >= rows &&
-        work_bytes >= gemm_lib_bytes(K, rows, N) && aligned16(work)) {
+    if (work && aligned16(work) && gemm_lib_eligible(ty, K, rows, N, row_stride, y_stride, work_bytes)) {
         const int r = gemm_lib(c, ty, (const uint8_t *)W, K, rows, X, x_stride, Y, y_stride, N, accumulate, n_batch, w_bs,
                                x_bs, y_bs, work, (hipStream_t)s);
         if (r >= 0) return r;
@@ -846,6 +891,19 @@ GS_EXPORT int gs_gemm_workspace(int K, int rows, int N, int n_batch, size_t *byt
     *bytes = rows == 0 ? 0 : gemm_part_bytes(gemm_slices(c, K, rows, N, n_batch, &ksb), rows, N, n_batch);
     if (rows > 0 && N >= GS_GEMM_LIB_MIN_N) *bytes = std::max(*bytes, gemm_lib_bytes(K, rows, N));
     return 0;
+}
+
+GS_EXPORT int gs_gemm_path(int ty, int K, int rows, int N, int64_t row_stride, int64_t y_stride, size_t work_bytes) {
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return -(int)e;
+    if (gemm_lib_eligible(ty, K, rows, N, row_stride, y_stride, work_bytes) && lt_plan(c, K, rows, N, y_stride))
+        return 2;
+    int ksb = 0;
+    return work_bytes > 0 && gemm_slices(c, K, rows, N, 1, &ksb) > 1 &&
+                   work_bytes >= gemm_part_bytes(gemm_slices(c, K, rows, N, 1, &ksb), rows, N, 1)
+               ? 1
+               : 0;
 }
 
 GS_EXPORT int gs_gemm_ex(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride,

@@ -88,6 +88,7 @@ SIGNATURES = {
     "gs_gemm": [C.c_int, _P, _I64, C.c_int, C.c_int, _P, _I64, _P, _I64, C.c_int, C.c_int, C.c_int, _I64, _I64, _I64,
                 _P],
     "gs_gemm_workspace": [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_size_t)],
+    "gs_gemm_path": [C.c_int, C.c_int, C.c_int, C.c_int, _I64, _I64, C.c_size_t],
     "gs_gemm_ex": [C.c_int, _P, _I64, C.c_int, C.c_int, _P, _I64, _P, _I64, C.c_int, C.c_int, C.c_int, _I64, _I64,
                    _I64, _P, C.c_size_t, _P],
     "gs_wait_status": [_P],
@@ -305,10 +306,19 @@ class ops:
 
     @staticmethod
     def gemm_workspace(k, rows, n, n_batch=1):
-        """gs_gemm_workspace: bytes of K-split scratch gs_gemm_ex would use (0: no split)."""
+        """gs_gemm_workspace: bytes of workspace gs_gemm_ex would use (K-split partials, or the f16
+        operands of the library path at N >= 384; 0: none)."""
         b = C.c_size_t()
         check(lib().gs_gemm_workspace(k, rows, n, n_batch, C.byref(b)))
         return b.value
+
+    @staticmethod
+    def gemm_path(ty, k, rows, n, row_stride, y_stride, work_bytes):
+        """gs_gemm_path: 0 f16 MFMA tiles, 1 tiles with the K split, 2 f16 dequant + hipBLASLt."""
+        r = lib().gs_gemm_path(int(ty), k, rows, n, row_stride, y_stride, work_bytes)
+        if r < 0:
+            check(-r)
+        return r
 
     @staticmethod
     def gemm_ex(ty, w, row_stride, k, rows, x, x_stride, y, y_stride, n, accumulate=False, n_batch=1, w_bs=0, x_bs=0,

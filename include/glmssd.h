@@ -150,6 +150,11 @@ int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const fl
  * call of kind (2) on a device creates that device's hipBLASLt handle, kept until the process
  * ends). */
 int gs_gemm_workspace(int K, int rows, int N, int n_batch, size_t *bytes);
+/* Additive (no counterpart in the reference): the path gs_gemm_ex takes for a problem (one batch)
+ * on the current device with a workspace of work_bytes: 0 the f16 MFMA tiles, 1 the tiles with the
+ * K split, 2 the f16 dequant + hipBLASLt path (the library opens and has an algorithm for the
+ * shape); a negative HIP error code if the device cannot run the library at all. */
+int gs_gemm_path(int ty, int K, int rows, int N, int64_t row_stride, int64_t y_stride, size_t work_bytes);
 int gs_gemm_ex(int ty, const void *W, int64_t row_stride, int K, int rows, const float *X, int64_t x_stride, float *Y,
                int64_t y_stride, int N, int accumulate, int n_batch, int64_t w_bs, int64_t x_bs, int64_t y_bs,
                void *work, size_t work_bytes, void *s);

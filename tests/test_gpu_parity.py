@@ -468,6 +468,9 @@ def test_gemm_ex_library_path(ty, stream):
     y0 = (np.random.default_rng(ty + 2).standard_normal((nb, N, ys)) * np.std(wants[0])).astype(np.float32)
     need = G.ops.gemm_workspace(K, rows, N, nb)
     assert need >= rows * K * 2 + N * K * 2   # holds the f16 operands
+    assert G.ops.gemm_path(ty, K, rows, N, rb, ys, need) == (1 if ty == T.Q8_0 else 2)
+    assert G.ops.gemm_path(ty, K, rows, N, rb + 2, ys, need) != 2   # padded rows: the tiles
+    assert G.ops.gemm_path(ty, K, rows, N, rb, ys, 0) == 0   # no workspace: plain tiles
     dw, dx, wk = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(need)
     outs = []
     for rep in range(2):
@@ -496,6 +499,7 @@ def test_gemm_ex_library_weights_bit_exact(ty, stream):
     assert ok.mean() > 0.5
     X = np.eye(K, dtype=np.float32)
     need = G.ops.gemm_workspace(K, rows, K, 1)
+    assert G.ops.gemm_path(ty, K, rows, K, rb, rows, need) == 2
     dw, dx, dy, wk = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(K * rows * 4), G.DeviceBuffer(need)
     G.ops.gemm_ex(ty, dw, rb, K, rows, dx, K, dy, rows, K, False, 1, 0, 0, 0, wk, need, stream)
     got = dy.download(np.float32, K * rows, stream).reshape(K, rows).T
