@@ -38,13 +38,18 @@ MFMA_F16_PEAK_TFLOPS = 2500.0   # dense f16 MFMA (the grouped GEMM's operand typ
 GATEUP_KERNEL = "gs_k_stream_16_1_1_4_w"   # the kernel gs_moe_gateup launches for config 2
 
 
-def traffic_bytes(kernel):
-    """HBM bytes per launch from the committed rocprofv3 counter summary, if it covers `kernel`."""
+def profile_entry(kernel, key):
+    """`key` of `kernel` in the committed rocprofv3 counter summary, if it covers them."""
     try:
         with open(os.path.join(ROOT, "profiles", "stream_kernels_traffic.json")) as f:
-            return json.load(f)["kernels"][kernel]["traffic_bytes"]
+            return json.load(f)["kernels"][kernel][key]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def traffic_bytes(kernel):
+    """HBM bytes per launch from the committed rocprofv3 counter summary."""
+    return profile_entry(kernel, "traffic_bytes")
 
 
 def log(*a):
@@ -310,6 +315,13 @@ def config5_roofline(r):
     if not r:
         return None
     tr = [traffic_bytes(k) for k in GROUPED_KERNELS]
+    ctr = [profile_entry(k, "counters") for k in GROUPED_KERNELS]
+    busy = None
+    if all(c is not None for c in ctr):
+        busy = {"gate_up": ctr[0]["mfma_busy_frac"], "down": ctr[1]["mfma_busy_frac"],
+                "valu_active": [c["valu_active_frac"] for c in ctr],
+                "source": "profiles/stream_kernels_traffic.json (rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / 4 / "
+                          "SQ_BUSY_CU_CYCLES per kernel, padded token slots included)"}
     return {"bound": "hbm", "achieved": r["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(r["GBps"] / HBM_PEAK_GBPS, 4),
             "traffic": sum(tr) if all(t is not None for t in tr) else None,
@@ -317,7 +329,8 @@ def config5_roofline(r):
                               "WRITE_SIZE, calibrated on a 1 GiB device copy)",
             "algorithmic_bytes_per_step": r["weight_bytes"], "us_per_step": r["us_per_step"],
             "mfma": {"achieved": r["TFLOPs"], "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": r["frac_mfma_f16_peak"], "dtype": "f16 x f16 -> f32 (v_mfma_f32_16x16x32_f16)"}}
+                     "frac": r["frac_mfma_f16_peak"], "dtype": "f16 x f16 -> f32 (v_mfma_f32_16x16x32_f16)",
+                     "busy": busy}}
 
 
 def cpu_model():
