@@ -676,3 +676,56 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_rows_f16(RowsQArgs a) {
         for (int u = lane; u < n8; u += 64) put(u, src[2 * u], src[2 * u + 1]);
     }
 }
+
+// The same conversion with one 256-thread workgroup per row, for few long rows (the prompt's
+// tokens: 512 rows of 4096 gave 128 four-row blocks, half the CUs and 16 loads in a row per lane).
+// The row's largest magnitude is a max, so the result is the one-wave kernel's bit for bit.
+extern "C" __global__ void __launch_bounds__(256) gs_k_rows_f16_wg(RowsQArgs a) {
+    __shared__ float wmax[4];
+    const int t = threadIdx.x, row = blockIdx.x;
+    const int n8 = a.K / 8;
+    const float4 *src = (const float4 *)(a.x + (int64_t)row * a.x_stride);
+    uint4 *dst = (uint4 *)(a.out + (int64_t)row * a.K);
+    constexpr int RQ = 4;   // rows of up to 256 x RQ 8-value pieces (K <= 8192) stay in registers
+    float4 r0[RQ], r1[RQ];
+    float amax = 0.f;
+    const bool held = n8 <= 256 * RQ;
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RQ; i++) {
+            const int u = min(t + 256 * i, n8 - 1);   // clamped: re-reads a valid piece
+            r0[i] = src[2 * u];
+            r1[i] = src[2 * u + 1];
+        }
+#pragma unroll
+        for (int i = 0; i < RQ; i++)
+            amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(r0[i].x), fabsf(r0[i].y)), fmaxf(fabsf(r0[i].z), fabsf(r0[i].w))),
+                                     fmaxf(fmaxf(fabsf(r1[i].x), fabsf(r1[i].y)), fmaxf(fabsf(r1[i].z), fabsf(r1[i].w)))));
+    } else {
+        for (int u = t; u < n8; u += 256) {
+            const float4 f0 = src[2 * u], f1 = src[2 * u + 1];
+            amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(f0.x), fabsf(f0.y)), fmaxf(fabsf(f0.z), fabsf(f0.w))),
+                                     fmaxf(fmaxf(fabsf(f1.x), fabsf(f1.y)), fmaxf(fabsf(f1.z), fabsf(f1.w)))));
+        }
+    }
+    amax = wave_max(amax);
+    if ((t & 63) == 0) wmax[t >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int E = 0;
+    if (amax > 0.f && amax <= 3.4e38f) (void)frexpf(amax, &E);   // amax < 2^E
+    E -= 15;
+    const float down = ldexpf(1.f, -E);
+    if (t == 0) a.scale[row] = ldexpf(1.f, E);
+    auto put = [&](int u, const float4 &f0, const float4 &f1) {
+        dst[u] = make_uint4(f2h(f0.x * down) | (f2h(f0.y * down) << 16), f2h(f0.z * down) | (f2h(f0.w * down) << 16),
+                            f2h(f1.x * down) | (f2h(f1.y * down) << 16), f2h(f1.z * down) | (f2h(f1.w * down) << 16));
+    };
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RQ; i++)
+            if (t + 256 * i < n8) put(t + 256 * i, r0[i], r1[i]);
+    } else {
+        for (int u = t; u < n8; u += 256) put(u, src[2 * u], src[2 * u + 1]);
+    }
+}

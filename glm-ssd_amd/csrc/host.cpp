@@ -970,6 +970,13 @@ GroupedWork grouped_layout(int n_tok, int n_pairs, int K, int n_ff) {
 hipError_t rows_f16(const float *x, int64_t x_stride, int K, int nrows, uint16_t *out, float *scale, hipStream_t s) {
     if (nrows <= 0) return hipSuccess;
     RowsQArgs a{x, x_stride, out, scale, K, nrows};
+    // one wave per row while that fills the chip (four rows per block); fewer, long rows take a
+    // workgroup each (same result)
+    hipError_t e;
+    DeviceCtx *c = ctx(&e);
+    if (!c) return e;
+    if (K >= 2048 && nrows < 4 * c->cu_count)
+        return launch("gs_k_rows_f16_wg", dim3(nrows), dim3(256), 0, s, a);
     return launch("gs_k_rows_f16", dim3((nrows + 3) / 4), dim3(256), 0, s, a);
 }
 
