@@ -281,7 +281,7 @@ def run_gemv(L, s, ty, rows, K, make, steps, warmup, seed, min_rot_bytes=640 << 
 
 def run_gemm(L, s, ty, rows, K, N, make, steps, warmup, seed, min_rot_bytes=640 << 20, use_work=True):
     """gs_gemm_ex of N tokens through a rows x K matrix, weight copies rotated, with the workspace
-    gs_gemm_workspace asks for (K split of small problems; at N >= 384 the f16 dequant + library
+    gs_gemm_workspace asks for (K split of small problems; from N = 256 the f16 dequant + library
     GEMM path); use_work=False: no workspace, i.e. plain gs_gemm's f16 MFMA tiles."""
     import glmssd as G
     rng = np.random.default_rng(seed)
@@ -457,6 +457,8 @@ def main():
         for name, ty, rows, K, N, mk, uw in [
                 ("gemm_q4_k_k4096_rows12288_N512", G.GgmlType.Q4_K, 12288, 4096, 512, S.q4_k_matrix, True),
                 ("gemm_q4_k_k4096_rows12288_N512_tiles", G.GgmlType.Q4_K, 12288, 4096, 512, S.q4_k_matrix, False),
+                ("gemm_q4_k_k4096_rows12288_N192", G.GgmlType.Q4_K, 12288, 4096, 192, S.q4_k_matrix, True),
+                ("gemm_q4_k_k4096_rows12288_N192_tiles", G.GgmlType.Q4_K, 12288, 4096, 192, S.q4_k_matrix, False),
                 ("gemm_q6_k_k12288_rows4096_N512", G.GgmlType.Q6_K, 4096, 12288, 512, q6, True),
                 ("gemm_q8_0_k4096_rows4096_N512", G.GgmlType.Q8_0, 4096, 4096, 512, S.q8_0_matrix, True),
                 ("gemm_iq2_xxs_k4096_rows1536_N64", G.GgmlType.IQ2_XXS, 1536, 4096, 64, iq, True)]:

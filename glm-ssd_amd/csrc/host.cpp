@@ -54,7 +54,7 @@ struct DeviceCtx {
     hipError_t init_err = hipSuccess;
     std::map<std::pair<std::string, int>, int> occ;  // (kernel, lds) -> blocks per CU
     std::vector<void *> wait_flags;   // gs_wait_expired of each code object that has one
-    // GEMM library path (gs_gemm_ex at N >= GS_GEMM_LIB_MIN_N): the device's hipBLASLt handle,
+    // GEMM library path (gs_gemm_ex with many tokens): the device's hipBLASLt handle,
     // created on first use, and one plan per problem shape
     std::mutex lt_mu;
     hipblasLtHandle_t lt = nullptr;
@@ -671,14 +671,20 @@ size_t gemm_part_bytes(int nks, int rows, int N, int n_batch) {
 }
 
 // ---- library path: dequantize to f16, convert X to f16, contract on hipBLASLt -----------------
-// At N >= GS_GEMM_LIB_MIN_N tokens, with a workspace, gs_gemm_ex writes the weights once as f16
+// With enough tokens (gemm_lib_tokens) and a workspace, gs_gemm_ex writes the weights once as f16
 // (the same f16(dequant) values the tile kernel rounds to), converts X to f16 (same rounding) and
 // runs the contraction as a plain f16 x f16 -> f32 GEMM (f32 accumulation) in hipBLASLt: Q4_K
 // 12288 x 4096 x 512 tokens 126 us in the tile kernel against about 82 us this way (dequant
-// pass ~24 us, conversion ~3 us, library GEMM ~55 us). Below that N the dequant pass costs more
-// than it saves. The algorithm is the library heuristic's first choice for the shape (fixed per
-// shape, so results repeat call to call).
-constexpr int GS_GEMM_LIB_MIN_N = 384;
+// pass ~24 us, conversion ~3 us, library GEMM ~55 us). The algorithm is the library heuristic's
+// first choice for the shape (fixed per shape, so results repeat call to call).
+// Token counts where the library path wins (measured, one MI355X): from 192 tokens for matrices of
+// 2^25 weights and more (Q4_K 12288 x 4096: 65 against 82 us at N = 192, where the tiles pass 256
+// CUs and need a second round; Q6_K 4096 x 12288 at N = 320: 75 against 131 us), from 256 tokens
+// otherwise (Q4_K 4096 x 4096: even at 256, 38 against 43 us at 320); below that the fixed dequant
+// pass costs more than the tiles lose.
+bool gemm_lib_tokens(int K, int rows, int N) {
+    return N >= 256 || (N >= 192 && (int64_t)rows * K >= ((int64_t)1 << 25));
+}
 // hipBLASLt entry points, from libhipblaslt opened on first use (no link-time dependency: without
 // the library the tiles run every problem)
 struct LtApi {
@@ -763,7 +769,7 @@ bool gemm_lib_eligible(int ty, int K, int rows, int N, int64_t row_stride, int64
     int qk, bb;
     if (!geometry(ty, qk, bb)) return false;
     const bool lib_ty = ty != GS_Q8_0 && ty != GS_F32 && ty != GS_BF16;
-    return lib_ty && N >= GS_GEMM_LIB_MIN_N && rows > 0 && row_stride == (int64_t)(K / qk) * bb && y_stride >= rows &&
+    return lib_ty && rows > 0 && gemm_lib_tokens(K, rows, N) && row_stride == (int64_t)(K / qk) * bb && y_stride >= rows &&
            work_bytes >= gemm_lib_bytes(K, rows, N);
 }
 // -1: not taken (the tile kernel runs the problem); otherwise the HIP status of the launches
@@ -889,7 +895,7 @@ GS_EXPORT int gs_gemm_workspace(int K, int rows, int N, int n_batch, size_t *byt
     if (!c) return e;
     int ksb = 0;
     *bytes = rows == 0 ? 0 : gemm_part_bytes(gemm_slices(c, K, rows, N, n_batch, &ksb), rows, N, n_batch);
-    if (rows > 0 && N >= GS_GEMM_LIB_MIN_N) *bytes = std::max(*bytes, gemm_lib_bytes(K, rows, N));
+    if (rows > 0 && gemm_lib_tokens(K, rows, N)) *bytes = std::max(*bytes, gemm_lib_bytes(K, rows, N));
     return 0;
 }
 

@@ -397,10 +397,12 @@ def test_gemm_full_grid_and_k_split(stream):
     e = _gemm_case(T.Q8_0, 512, 2176, 512, stream, 21)
     say(f"gemm Q8_0 2176x512 N=512 (full grid): rel-L2 {e:.2e}")
     assert e <= GEMM_REL
-    # a full grid below the library path's token count needs no workspace; at N >= 384 the
+    # a full grid below the library path's token count needs no workspace (204 tiles, 4.5 M
+    # weights at 192 tokens); from 256 tokens, or 192 for matrices of 2^25 weights and more, the
     # workspace holds the f16 operands of the library path
-    assert G.ops.gemm_workspace(512, 4352, 256) == 0
-    assert G.ops.gemm_workspace(512, 2176, 512) >= 2176 * 512 * 2 + 512 * 512 * 2
+    assert G.ops.gemm_workspace(512, 8704, 192) == 0
+    assert G.ops.gemm_workspace(512, 2176, 256) >= 2176 * 512 * 2 + 256 * 512 * 2
+    assert G.ops.gemm_workspace(4096, 8192, 192) >= 8192 * 4096 * 2 + 192 * 4096 * 2
     ty, K, rows, N = T.IQ2_XXS, 4096, 1536, 64
     rb = G.row_bytes(ty, K)
     raw = O.Rng(22).random_blocks(ty, rows * K)
@@ -451,7 +453,7 @@ def test_gemm_ex_accumulate_and_batches(stream):
 
 @pytest.mark.parametrize("ty", [T.Q4_K, T.Q5_K, T.Q6_K, T.IQ2_XXS, T.F16, T.Q8_0])
 def test_gemm_ex_library_path(ty, stream):
-    # N >= 384 tokens with the workspace gs_gemm_workspace asks for: the weights are dequantized
+    # N = 400 tokens with the workspace gs_gemm_workspace asks for: the weights are dequantized
     # to f16 in the workspace, X converted to f16, and the contraction runs in the GEMM library.
     # Against the oracle's f16-operand product (f32 accumulation order differs) with accumulate,
     # two batches, a strided Y; and two calls give the same bits. (Q8_0 keeps the tile kernel at
