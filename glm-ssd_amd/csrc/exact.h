@@ -199,6 +199,10 @@ __device__ __forceinline__ void iq4_xs(const uint8_t *b, int u, float (&y)[32]) 
 namespace al {
 __device__ __forceinline__ uint32_t w32(const uint8_t *p, int off) { return *(const uint32_t *)(p + off); }
 __device__ __forceinline__ float h16(uint32_t w, int hi) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? w >> 16 : w)); }
+// the f16 at byte `off` (2-byte aligned) by itself: no byte past it is read
+__device__ __forceinline__ float h16_at(const uint8_t *p, int off) {
+    return (float)__builtin_bit_cast(_Float16, *(const uint16_t *)(p + off));
+}
 __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)(int)(int8_t)(w >> (8 * i)); }
 __device__ __forceinline__ float ubyte(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
 // a value whose bits the compiler must not track: byte i of it then converts with one
@@ -239,11 +243,23 @@ __device__ __forceinline__ void q4_k(const uint8_t *p, int u, float (&y)[32]) {
     }
 }
 
-// Q6_K: unit u = quarter k = u % 4 of half n = u / 4; ql, qh, the int8 scales and d all start on
-// dwords
+// Q8_0 block in global memory (34 bytes, 2-byte aligned): d as 16 bits, the 32 quants as the 8
+// dwords at bytes 2..33 (unaligned loads). Reads no byte past the block, so the last block of an
+// allocation is safe where q8_0 above, made for a dword-aligned LDS group, reads on to byte 35.
+__device__ __forceinline__ void q8_0_block(const uint8_t *b, float (&y)[32]) {
+    const float d = h16_at(b, 0);
+    for (int k = 0; k < 8; k++) {
+        const uint32_t q = w32(b, 2 + 4 * k);
+        for (int i = 0; i < 4; i++) y[4 * k + i] = sbyte(q, i) * d;
+    }
+}
+
+// Q6_K: unit u = quarter k = u % 4 of half n = u / 4; ql, qh and the int8 scales start on dwords;
+// d (bytes 208-209, the block's last) is read as 16 bits, so nothing past the 210-byte block is
+// read (the decoder also runs on blocks in global memory)
 __device__ __forceinline__ void q6_k(const uint8_t *p, int u, float (&y)[32]) {
     const int n = u >> 2, k = u & 3;
-    const float d = h16(w32(p, 208), 0);
+    const float d = h16_at(p, 208);
     // scale bytes 2k and 2k + 1 of the half (elements 0..15, 16..31), in the dword at 4 (k >> 1)
     const uint32_t scw = w32(p, 192 + 8 * n + 4 * (k >> 1));
     const float s0 = d * sbyte(scw, 2 * (k & 1)), s1 = d * sbyte(scw, 2 * (k & 1) + 1);

@@ -768,7 +768,7 @@ DeviceCtx::LtPlan *lt_plan(DeviceCtx *c, int K, int rows, int N, int64_t y_strid
 bool gemm_lib_eligible(int ty, int K, int rows, int N, int64_t row_stride, int64_t y_stride, size_t work_bytes) {
     int qk, bb;
     if (!geometry(ty, qk, bb)) return false;
-    const bool lib_ty = ty != GS_Q8_0 && ty != GS_F32 && ty != GS_BF16;
+    const bool lib_ty = ty != GS_F32 && ty != GS_BF16;   // float weights: not measured this way
     return lib_ty && rows > 0 && gemm_lib_tokens(K, rows, N) && row_stride == (int64_t)(K / qk) * bb && y_stride >= rows &&
            work_bytes >= gemm_lib_bytes(K, rows, N);
 }
@@ -851,9 +851,8 @@ int gemm_impl(int ty, const void *W, int64_t row_stride, int K, int rows, const 
     DeviceCtx *c = ctx(&e);
     if (!c) return e;
     // many tokens and a workspace for the f16 operands: dequantize + library GEMM (contiguous rows;
-    // the block formats whose tile decode costs more than a dequant pass, and F16 weights as they
-    // are; Q8_0's tile decode is cheap enough that the tile kernel stays faster: 46 against 49 us
-    // at 4096 x 4096 x 512)
+    // every block format, and F16 weights as they are: Q8_0 too, whose tile decode is the cheapest,
+    // 42 against 50 us at 4096 x 4096 x 512 and 82 against 137 us at 12288 x 4096 x 512)
     if (work && aligned16(work) && gemm_lib_eligible(ty, K, rows, N, row_stride, y_stride, work_bytes)) {
         const int r = gemm_lib(c, ty, (const uint8_t *)W, K, rows, X, x_stride, Y, y_stride, N, accumulate, n_batch, w_bs,
                                x_bs, y_bs, work, (hipStream_t)s);

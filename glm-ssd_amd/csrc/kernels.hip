@@ -812,8 +812,9 @@ __device__ __forceinline__ int dequant_unit(const uint8_t *src, int64_t u, int64
     if (QKB >= 32) {
         constexpr int UPB = QKB / 32;
         const uint8_t *blk = src + (u / UPB) * BB;
-        // whole-dword reads (unaligned global loads) where a dword decoder exists: the same values
-        if constexpr (DEC == &exact::q8_0) exact::al::q8_0(blk, 0, v);
+        // whole-dword reads (unaligned global loads) where a dword decoder exists: the same values,
+        // and no byte past the block is read (the last block may end the allocation)
+        if constexpr (DEC == &exact::q8_0) exact::al::q8_0_block(blk, v);
         else if constexpr (DEC == &exact::q4_k) exact::al::q4_k(blk, (int)(u % UPB), v);
         else if constexpr (DEC == &exact::q6_k) exact::al::q6_k(blk, (int)(u % UPB), v);
         else DEC(blk, (int)(u % UPB), v);

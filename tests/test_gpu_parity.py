@@ -59,6 +59,29 @@ def test_dequant_bit_exact(ty, stream):
     assert bad.size == 0
 
 
+@pytest.mark.parametrize("ty", [T.Q8_0, T.Q4_K, T.Q6_K])
+def test_dequant_blocks_ending_the_allocation(ty, stream):
+    # the formats decoded with whole-dword reads: the last blocks of an allocation whose size is a
+    # multiple of 2 MiB (no slack after it), so a read past the final block would leave the
+    # allocation; the decoders read only the block's own bytes
+    say("dequant at the allocation's end", G.TYPE_NAMES[ty])
+    qk, bb = G.block(ty)
+    total = int(np.lcm(bb, 2 << 20))
+    nb = 96
+    raw = O.Rng(0x5EED + ty).random_blocks(ty, nb * qk)
+    buf = G.DeviceBuffer(total)
+    buf.upload(raw, stream, total - raw.nbytes)
+    n = nb * qk
+    want = O.dequantize(ty, raw, n)
+    dy, dh = G.DeviceBuffer(n * 4), G.DeviceBuffer(n * 2)
+    G.ops.dequant_f32(ty, buf.ptr(total - raw.nbytes), n, dy, stream)
+    G.ops.dequant_f16(ty, buf.ptr(total - raw.nbytes), n, dh, stream)
+    assert np.array_equal(dy.download(np.float32, n, stream).view(np.uint32), want.view(np.uint32))
+    with np.errstate(over="ignore"):
+        wh = want.astype(np.float16).view(np.uint16)
+    assert np.array_equal(dh.download(np.uint16, n, stream), wh)
+
+
 def test_quant_q8_1_bit_exact(stream):
     say("quant_q8_1")
     rng = np.random.default_rng(5)
@@ -456,8 +479,7 @@ def test_gemm_ex_library_path(ty, stream):
     # N = 400 tokens with the workspace gs_gemm_workspace asks for: the weights are dequantized
     # to f16 in the workspace, X converted to f16, and the contraction runs in the GEMM library.
     # Against the oracle's f16-operand product (f32 accumulation order differs) with accumulate,
-    # two batches, a strided Y; and two calls give the same bits. (Q8_0 keeps the tile kernel at
-    # every N: the same checks.)
+    # two batches, a strided Y; and two calls give the same bits.
     K, rows, N, nb, ys = 512, 200, 400, 2, 203
     rb = G.row_bytes(ty, K)
     if ty == T.F16:
@@ -470,7 +492,7 @@ def test_gemm_ex_library_path(ty, stream):
     y0 = (np.random.default_rng(ty + 2).standard_normal((nb, N, ys)) * np.std(wants[0])).astype(np.float32)
     need = G.ops.gemm_workspace(K, rows, N, nb)
     assert need >= rows * K * 2 + N * K * 2   # holds the f16 operands
-    assert G.ops.gemm_path(ty, K, rows, N, rb, ys, need) == (1 if ty == T.Q8_0 else 2)
+    assert G.ops.gemm_path(ty, K, rows, N, rb, ys, need) == 2
     assert G.ops.gemm_path(ty, K, rows, N, rb + 2, ys, need) != 2   # padded rows: the tiles
     assert G.ops.gemm_path(ty, K, rows, N, rb, ys, 0) == 0   # no workspace: plain tiles
     dw, dx, wk = G.DeviceBuffer.from_array(raw), G.DeviceBuffer.from_array(X), G.DeviceBuffer(need)
@@ -488,7 +510,8 @@ def test_gemm_ex_library_path(ty, stream):
         assert e <= GEMM_REL
 
 
-@pytest.mark.parametrize("ty", [T.Q4_K, T.Q6_K, T.IQ2_XXS, T.Q5_K, T.Q2_K, T.Q3_K, T.IQ4_XS, T.IQ3_XXS, T.IQ2_S])
+@pytest.mark.parametrize("ty", [T.Q4_K, T.Q6_K, T.IQ2_XXS, T.Q5_K, T.Q2_K, T.Q3_K, T.IQ4_XS, T.IQ3_XXS, T.IQ2_S,
+                                T.Q8_0])
 def test_gemm_ex_library_weights_bit_exact(ty, stream):
     # the library path's weights: X = the identity (N = K = 512 tokens), so Y[n][r] is exactly
     # the f16 rounding of weight (r, n), bit for bit against the oracle's dequantization
