@@ -756,7 +756,9 @@ struct FIQ2_S : UnitGeom<256, 82> {
         w.a = m.u32(o + 2 + 4 * (uint32_t)j);
         w.sg = m.u32(o + 34 + 4 * (uint32_t)j);
         w.qh = m.u16(o + 66 + (uint32_t)j);
-        w.sc = m.u16(o + 74 + (uint32_t)j);
+        // the scale byte 74 + j as the high byte of the u16 before it: unit 7's u16 at 74 + j would
+        // end past the 82-byte block (the last block of an allocation)
+        w.sc = m.u16(o + 73 + (uint32_t)j) >> 8;
     }
     // units j, j+1 of one block (j even): d once, both units' bytes in 8-byte and 2-byte reads
     static constexpr bool PAIR = true;

@@ -182,6 +182,28 @@ def test_gemv_matches_oracle(ty, rows, K, stream):
         assert _gemv_case(ty, rows, K, B, stream, seed=1000 * ty + rows + B) <= (REL_L2_F32 if ty in FLOAT else REL_L2)
 
 
+@pytest.mark.parametrize("ty", [t for t in ALL if t != T.BF16])
+@pytest.mark.parametrize("K", [4096, 1536, 2816])
+def test_gemv_matrix_ending_the_allocation(ty, K, stream):
+    # the matrix's last byte is the last byte of an allocation whose size is a multiple of 2 MiB
+    # (no slack after it): the streaming loads of the last row read only its blocks' bytes
+    # (48 rows: every type's matrix is then a multiple of 16 bytes, so it starts 16-byte aligned)
+    rows = 48
+    rb = G.row_bytes(ty, K)
+    raw = O.Rng(77 * ty + K).random_blocks(ty, rows * K)
+    total = -(-raw.nbytes // (2 << 20)) * (2 << 20)
+    buf = G.DeviceBuffer(total)
+    off = total - raw.nbytes
+    buf.upload(raw, stream, off)
+    x = np.random.default_rng(K + ty).standard_normal((3, K)).astype(np.float32)
+    want = O.gemv(ty, raw, rb, K, rows, x, B=3, act="f32" if ty in FLOAT else "q8_1")
+    dx, dy = G.DeviceBuffer.from_array(x), G.DeviceBuffer(3 * rows * 4)
+    for B in (1, 3):
+        G.ops.gemv(ty, buf.ptr(off), rb, K, rows, dx, K, dy, rows, B, False, stream)
+        got = dy.download(np.float32, B * rows, stream).reshape(B, rows)
+        assert rel_l2(got, want[:B]) <= (REL_L2_F32 if ty in FLOAT else REL_L2)
+
+
 # BF16 with finite blocks: bf16 bit patterns of N(0,1) values (the reference harness skips BF16
 # because its random bytes hold NaN/Inf; a real BF16 matrix is finite)
 @pytest.mark.parametrize("rows,K", [(101, 4096), (513, 1536)])
