@@ -786,7 +786,7 @@ int gemm_lib(DeviceCtx *c, int ty, const uint8_t *W, int K, int rows, const floa
         const void *a16 = w16;
         const int64_t xthr = (int64_t)N * (K / 4);   // activation pieces of 4 values
         int e;
-        if (ty == GS_F16) {   // already f16 (contiguous rows): the library reads it in place
+        if (ty == GS_F16 && aligned16(W + z * w_bs)) {   // already f16, contiguous and 16-byte aligned: in place
             a16 = W + z * w_bs;
             CvtArgs cv{X + z * x_bs, x16, x_stride, K, N};
             e = launch("gs_k_rows_to_f16", dim3((unsigned)((xthr + 255) / 256)), dim3(256), 0, s, cv);

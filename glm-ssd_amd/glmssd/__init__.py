@@ -323,7 +323,8 @@ class ops:
     @staticmethod
     def gemm_ex(ty, w, row_stride, k, rows, x, x_stride, y, y_stride, n, accumulate=False, n_batch=1, w_bs=0, x_bs=0,
                 y_bs=0, work=None, work_bytes=0, s=None):
-        """gs_gemm_ex: gs_gemm with a caller workspace for the K split."""
+        """gs_gemm_ex: gs_gemm with a caller workspace (K split of small problems, or the f16
+        operands of the dequant + library GEMM path at many tokens; gemm_path says which)."""
         check(lib().gs_gemm_ex(ty, _p(w), row_stride, k, rows, _p(x), x_stride, _p(y), y_stride, n,
                                1 if accumulate else 0, n_batch, w_bs, x_bs, y_bs, _p(work), work_bytes, _raw(s)))
 

@@ -532,6 +532,25 @@ def test_gemm_ex_library_path(ty, stream):
         assert e <= GEMM_REL
 
 
+def test_gemm_ex_library_path_f16_unaligned(stream):
+    # F16 weights 2 bytes past a 16-byte boundary: the library path copies them (the dequant
+    # pass) instead of handing the library a misaligned operand; same product as aligned
+    ty, K, rows, N = T.F16, 512, 96, 320
+    rb = G.row_bytes(ty, K)
+    raw = np.random.default_rng(41).standard_normal(rows * K).astype(np.float16).view(np.uint8)
+    X = np.random.default_rng(42).standard_normal((N, K)).astype(np.float32)
+    want = O.gemv(ty, raw, rb, K, rows, X, B=N, act="f16", nthreads=8)
+    dw = G.DeviceBuffer(raw.nbytes + 16)
+    dw.upload(raw, stream, 2)
+    dx, dy = G.DeviceBuffer.from_array(X), G.DeviceBuffer(N * rows * 4)
+    need = G.ops.gemm_workspace(K, rows, N, 1)
+    assert G.ops.gemm_path(ty, K, rows, N, rb, rows, need) == 2
+    wk = G.DeviceBuffer(need)
+    G.ops.gemm_ex(ty, dw.ptr(2), rb, K, rows, dx, K, dy, rows, N, False, 1, 0, 0, 0, wk, need, stream)
+    got = dy.download(np.float32, N * rows, stream).reshape(N, rows)
+    assert rel_l2(got, want) <= GEMM_REL
+
+
 @pytest.mark.parametrize("ty", [T.Q4_K, T.Q6_K, T.IQ2_XXS, T.Q5_K, T.Q2_K, T.Q3_K, T.IQ4_XS, T.IQ3_XXS, T.IQ2_S,
                                 T.Q8_0])
 def test_gemm_ex_library_weights_bit_exact(ty, stream):
