@@ -677,13 +677,14 @@ size_t gemm_part_bytes(int nks, int rows, int N, int n_batch) {
 // 12288 x 4096 x 512 tokens 126 us in the tile kernel against about 82 us this way (dequant
 // pass ~24 us, conversion ~3 us, library GEMM ~55 us). The algorithm is the library heuristic's
 // first choice for the shape (fixed per shape, so results repeat call to call).
-// Token counts where the library path wins (measured, one MI355X): from 192 tokens for matrices of
-// 2^25 weights and more (Q4_K 12288 x 4096: 65 against 82 us at N = 192, where the tiles pass 256
-// CUs and need a second round; Q6_K 4096 x 12288 at N = 320: 75 against 131 us), from 256 tokens
-// otherwise (Q4_K 4096 x 4096: even at 256, 38 against 43 us at 320); below that the fixed dequant
-// pass costs more than the tiles lose.
+// Token counts where the library path wins (measured, one MI355X): above 128 tokens for matrices
+// of 2^25 weights and more (Q4_K 12288 x 4096: 58 against 84 us at N = 136, where the tiles pass
+// 256 CUs and need a second round, 44 against 62 us the other way at N = 128; Q6_K 4096 x 12288:
+// 59 against 77 us at 136, 75 against 131 us at 320), from 256 tokens otherwise (Q4_K 4096 x 4096:
+// even at 256, 38 against 43 us at 320); below that the fixed dequant pass costs more than the
+// tiles lose.
 bool gemm_lib_tokens(int K, int rows, int N) {
-    return N >= 256 || (N >= 192 && (int64_t)rows * K >= ((int64_t)1 << 25));
+    return N >= 256 || (N > 128 && (int64_t)rows * K >= ((int64_t)1 << 25));
 }
 // hipBLASLt entry points, from libhipblaslt opened on first use (no link-time dependency: without
 // the library the tiles run every problem)

@@ -307,7 +307,7 @@ class ops:
     @staticmethod
     def gemm_workspace(k, rows, n, n_batch=1):
         """gs_gemm_workspace: bytes of workspace gs_gemm_ex would use (K-split partials, or the f16
-        operands of the library path from N = 256, or 192 at rows*K >= 2^25; 0: none)."""
+        operands of the library path from N = 256, or above 128 at rows*K >= 2^25; 0: none)."""
         b = C.c_size_t()
         check(lib().gs_gemm_workspace(k, rows, n, n_batch, C.byref(b)))
         return b.value

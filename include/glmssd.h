@@ -137,7 +137,7 @@ int gs_gemm(int ty, const void *W, int64_t row_stride, int K, int rows, const fl
 /* Additive (no counterpart in the reference): gs_gemm with a caller-owned workspace, used two ways.
  * (1) Problems with few 128-row x 64-token tiles (small N, few rows) split K across workgroups:
  * each slice writes its f32 partial tile into `work` and the slices are added in a fixed order.
- * (2) From N = 256 tokens (N = 192 for matrices of rows*K >= 2^25 weights), for every weight
+ * (2) From N = 256 tokens (N > 128 for matrices of rows*K >= 2^25 weights), for every weight
  * type but F32 and BF16 and rows stored back to back (row_stride = bytes of a row), the weights are dequantized into `work` as f16 (F16 weights
  * are used in place), X is converted to f16 there too, and the product runs as an f16 x f16 -> f32
  * GEMM in hipBLASLt (the heuristic's first algorithm for the shape, so a shape always takes the

@@ -443,11 +443,12 @@ def test_gemm_full_grid_and_k_split(stream):
     say(f"gemm Q8_0 2176x512 N=512 (full grid): rel-L2 {e:.2e}")
     assert e <= GEMM_REL
     # a full grid below the library path's token count needs no workspace (204 tiles, 4.5 M
-    # weights at 192 tokens); from 256 tokens, or 192 for matrices of 2^25 weights and more, the
-    # workspace holds the f16 operands of the library path
+    # weights at 192 tokens); from 256 tokens, or above 128 for matrices of 2^25 weights and
+    # more, the workspace holds the f16 operands of the library path
     assert G.ops.gemm_workspace(512, 8704, 192) == 0
     assert G.ops.gemm_workspace(512, 2176, 256) >= 2176 * 512 * 2 + 256 * 512 * 2
-    assert G.ops.gemm_workspace(4096, 8192, 192) >= 8192 * 4096 * 2 + 192 * 4096 * 2
+    assert G.ops.gemm_workspace(4096, 8192, 136) >= 8192 * 4096 * 2 + 136 * 4096 * 2
+    assert G.ops.gemm_path(T.Q4_K, 4096, 8192, 128, G.row_bytes(T.Q4_K, 4096), 8192, 1 << 30) != 2
     ty, K, rows, N = T.IQ2_XXS, 4096, 1536, 64
     rb = G.row_bytes(ty, K)
     raw = O.Rng(22).random_blocks(ty, rows * K)
