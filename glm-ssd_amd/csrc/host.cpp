@@ -413,6 +413,18 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
         a.accumulate = accumulate;
         return stream_any(0, ty, a, n_batch, (hipStream_t)s);
     }
+    // Q8_0 with 4..8 vectors: one pass on int8 MFMA, every weight read once for all vectors
+    // (gs_k_mv_q8_0: 16 rows and the vectors' q8_1 units in LDS; rows of whole 16-byte chunks,
+    // K % 256 == 0, up to K = 4096; 16-byte aligned rows and activations). 4096 x 4096: 8.9 us
+    // for 4 vectors, 10.3 for 8, against 9.1 and 12.4 in the streaming kernels (which read the
+    // weights twice from 5 vectors on); at 2 vectors the streaming kernel stays faster (7.1
+    // against 8.3 us: it overlaps the contraction with the weight stream)
+    if (ty == GS_Q8_0 && B >= 4 && n_batch == 1 && nv_tail == 0 && K % 256 == 0 && K <= 4096 && aligned16(x) &&
+        x_stride % 4 == 0 && aligned16(W) && row_stride % 16 == 0) {
+        MvArgs m{(const uint8_t *)W, row_stride, x, x_stride, y, y_stride, K, rows, B, accumulate};
+        const size_t U = K / 32, lds = 16 * (34 * U + 16) + 288 * U + 8 * 64 * 16;
+        return launch("gs_k_mv_q8_0", dim3((unsigned)((rows + 15) / 16)), dim3(512), lds, (hipStream_t)s, m);
+    }
     // more than 4 vectors whose units do not fit 8-vector registers (K > 2048): groups of 4 vectors
     // over the whole K instead of K slices of 8 vectors (8 x 4096 Q8_0: 14 us against 28 us), both
     // groups in one launch (blockIdx.y; the second holds B - 4 vectors), reading the same weights

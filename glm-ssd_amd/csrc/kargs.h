@@ -71,6 +71,17 @@ struct QuantArgs {
     int64_t n_blocks;
 };
 
+// multi-vector Q8_0 GEMV on int8 MFMA (gs_gemv with 2..8 vectors): y[t][r] (+)= W[r] . q8_1(x[t])
+struct MvArgs {
+    const uint8_t *w;
+    int64_t row_stride;   // bytes
+    const float *x;
+    int64_t x_stride;     // floats
+    float *y;
+    int64_t y_stride;     // floats
+    int K, rows, nv, accumulate;
+};
+
 // f32 rows -> compact f16 rows (round to nearest even): N rows of K values, source row stride
 // x_stride (elements), destination rows K apart (the GEMM library path's activations)
 struct CvtArgs {

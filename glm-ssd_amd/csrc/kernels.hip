@@ -918,6 +918,149 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_quant_q8_1(QuantArgs a) {
 }
 
 // =============================================================================================
+// Q8_0 GEMV of 2..8 vectors on int8 MFMA (quants.cu:53-256 semantics: y[t][r] (+)= W[r] . x[t])
+//
+// A 32-element Q8_0 block is one v_mfma_i32_16x16x32_i8 step: weights int8 as they are stored,
+// activations the q8_1 quantization of x (the streaming kernels' arithmetic, so the same int8
+// values and f16-rounded scales). The MFMA gives the exact int32 dot of every (vector, row) pair
+// of the block for 16 rows at once; d_w * d_x then scales it into the f32 sum, as the streaming
+// kernels do per block. So each weight is read once for all vectors (the streaming kernels keep
+// at most 4 vectors' activations in registers and read the weights twice for 5..8).
+// Workgroup: 16 rows. Their bytes are copied to LDS with 16-byte loads (1 KB per wave load, where
+// fragment-shaped loads would touch 16 rows' lines per instruction), rows 16 bytes apart beyond
+// their length so the 16 rows of a fragment read sit in different banks; the vectors' q8_1 units
+// in LDS unit-major ([unit][vector][32 B]: a lane's 8 bytes for one MFMA are one conflict-free
+// read). 8 waves split the blocks of the row; their partial sums are added in wave order.
+// Rows: K % 256 == 0 (whole 16-byte chunks, nothing read past a row), K <= 4096.
+// =============================================================================================
+typedef int mv_v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t mv_u4 __attribute__((ext_vector_type(4)));   // a native vector: the chunk array stays in VGPRs
+extern "C" __global__ void __launch_bounds__(512) gs_k_mv_q8_0(MvArgs a) {
+    extern __shared__ __align__(16) uint8_t mv_lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int U = a.K / 32, nv = a.nv;
+    const int rbytes = 34 * U, RS = rbytes + 16;               // row bytes, LDS row pitch
+    uint8_t *wl = mv_lds;                                       // [16][RS] raw rows
+    uint8_t *xq = mv_lds + 16 * (size_t)RS;                     // [U][8][32] int8
+    float *xd = (float *)(xq + 256 * (size_t)U);                // [U][8] f16-rounded scales
+    float *red = xd + 8 * (size_t)U;                            // [8 waves][64 lanes][4]
+    const int r0 = blockIdx.x * 16;
+
+    // loads: the activations (8 floats per thread and task, 4 threads per unit), then the rows
+    const int ntask = nv * U * 4;
+    const int cpr = rbytes / 16, nchunk = 16 * cpr;            // 16-byte chunks per row, per tile
+    constexpr int XC = 8, WC = 9;                               // per thread: tasks, chunks (K <= 4096)
+    float f[XC][8];
+#pragma unroll
+    for (int c = 0; c < XC; c++) {
+        // passes past the last task re-read a valid piece (uniform; no early exit, so the array
+        // stays in registers)
+        const int t = min(512 * c + tid, ntask - 1);
+        const int sub = t & 3, vu = t >> 2, v = vu / U, u = vu - v * U;
+        const float4 *src = (const float4 *)(a.x + (int64_t)v * a.x_stride + 32 * u + 8 * sub);
+        const float4 p0 = src[0], p1 = src[1];
+        f[c][0] = p0.x; f[c][1] = p0.y; f[c][2] = p0.z; f[c][3] = p0.w;
+        f[c][4] = p1.x; f[c][5] = p1.y; f[c][6] = p1.z; f[c][7] = p1.w;
+    }
+    mv_u4 wc[WC];
+    int wdst[WC];   // LDS byte offset of the chunk (-1: none)
+#pragma unroll
+    for (int c = 0; c < WC; c++) {
+        const int z = min(512 * c + tid, nchunk - 1), rr = z / cpr, cc = z - rr * cpr;
+        const uint8_t *row = a.w + (int64_t)min(r0 + rr, a.rows - 1) * a.row_stride;   // tail rows: clamped, dropped
+        wc[c] = *(const mv_u4 *)(row + 16 * cc);
+        wdst[c] = 512 * c + tid < nchunk ? rr * RS + 16 * cc : -1;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < XC; c++) {
+        if (512 * c >= ntask) continue;                         // uniform; quads are in or out together
+        const int t = 512 * c + tid;
+        float amax = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(f[c][e]));
+        uint32_t ab = __builtin_bit_cast(uint32_t, amax);
+        ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0xB1>(__builtin_bit_cast(float, ab))));
+        ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0x4E>(__builtin_bit_cast(float, ab))));
+        amax = __builtin_bit_cast(float, ab);
+        const float d = q8_div127(amax);
+        float id = d != 0.f ? 1.0f / d : 0.f;
+        id = id <= 3.40282347e38f ? id : 0.f;   // d < 2^-128: q = 0, as quant_unit
+        uint32_t w[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int qv[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) qv[b] = q8_round_mul(f[c][4 * h + b], id);
+            w[h] = __builtin_amdgcn_perm((uint32_t)qv[1], (uint32_t)qv[0], 0x0c0c0400u) |
+                   __builtin_amdgcn_perm((uint32_t)qv[3], (uint32_t)qv[2], 0x04000c0cu);
+        }
+        if (t < ntask) {
+            const int sub = t & 3, vu = t >> 2, v = vu / U, u = vu - v * U;
+            *(uint2 *)(xq + 256 * (size_t)u + 32 * v + 8 * sub) = make_uint2(w[0], w[1]);
+            if (sub == 0) xd[8 * u + v] = h2f(f2h(d));
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < WC; c++)
+        if (wdst[c] >= 0) *(mv_u4 *)(wl + wdst[c]) = wc[c];
+    __syncthreads();
+
+    // contraction: this wave's blocks of the 16 rows
+    const int j = lane & 15, q = lane >> 4;
+    const int ta = j & 7;                 // the lane's A row (vector); rows 8..15 repeat 0..7, dropped
+    const int tq = 4 * (q & 1);           // first vector of the lane's four D rows (q >= 2: dropped)
+    const uint8_t *wrow = wl + (size_t)j * RS;
+    const int upw = (U + 7) / 8, u0 = wave * upw, u1 = min(U, u0 + upw);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    // four blocks per step: their LDS reads and MFMAs overlap instead of each waiting on the last
+    constexpr int US = 4;
+    for (int ub = u0; ub < u1; ub += US) {
+        uint64_t wb[US], xa[US];
+        float dw[US];
+        float4 dx[US];
+#pragma unroll
+        for (int i = 0; i < US; i++) {
+            const int u = min(ub + i, u1 - 1);   // past the wave's last block: re-read it, dropped below
+            const uint32_t o = 34u * (uint32_t)u + 2u + 8u * (uint32_t)q, oa = o & ~3u, sh = o & 3u;
+            const uint32_t w0 = *(const uint32_t *)(wrow + oa), w1 = *(const uint32_t *)(wrow + oa + 4),
+                           w2 = *(const uint32_t *)(wrow + oa + 8);
+            wb[i] = (uint64_t)__builtin_amdgcn_alignbyte(w1, w0, sh) |
+                    ((uint64_t)__builtin_amdgcn_alignbyte(w2, w1, sh) << 32);
+            xa[i] = *(const uint64_t *)(xq + 256 * (size_t)u + 32 * ta + 8 * q);
+            dw[i] = h2f(*(const uint16_t *)(wrow + 34 * u));
+            dx[i] = *(const float4 *)(xd + 8 * u + tq);
+        }
+        mv_v4i dot[US];
+#pragma unroll
+        for (int i = 0; i < US; i++)
+            dot[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xa[i], (long)wb[i], mv_v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < US; i++) {
+            if (ub + i < u1) {   // uniform
+                acc[0] += (float)dot[i][0] * (dw[i] * dx[i].x);
+                acc[1] += (float)dot[i][1] * (dw[i] * dx[i].y);
+                acc[2] += (float)dot[i][2] * (dw[i] * dx[i].z);
+                acc[3] += (float)dot[i][3] * (dw[i] * dx[i].w);
+            }
+        }
+    }
+    *(float4 *)(red + 4 * (64 * wave + lane)) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();
+    if (tid < 16 * 8) {
+        const int t = tid >> 4, jj = tid & 15, r = r0 + jj;
+        const int src = 16 * (t >> 2) + jj, i = t & 3;   // the lane that holds D[t][jj]
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; w++) sum += red[4 * (64 * w + src) + i];
+        if (t < nv && r < a.rows) {
+            float *dst = a.y + (int64_t)t * a.y_stride + r;
+            *dst = a.accumulate ? *dst + sum : sum;
+        }
+    }
+}
+
+// =============================================================================================
 // Element-wise and row kernels of the MoE glue (ops.cu:101-125, gemm.cu:125-163)
 // =============================================================================================
 extern "C" __global__ void __launch_bounds__(256) gs_k_swiglu(EltArgs a) {

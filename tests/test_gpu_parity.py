@@ -182,6 +182,20 @@ def test_gemv_matches_oracle(ty, rows, K, stream):
         assert _gemv_case(ty, rows, K, B, stream, seed=1000 * ty + rows + B) <= (REL_L2_F32 if ty in FLOAT else REL_L2)
 
 
+@pytest.mark.parametrize("rows,K", [(37, 256), (200, 1024), (1000, 4096), (45, 96), (64, 8192)])
+def test_gemv_q8_0_vectors_on_mfma(rows, K, stream):
+    # Q8_0 with 4..8 vectors and K % 256 == 0 up to 4096 runs as one int8-MFMA pass (16-row
+    # tiles, a tail tile in each shape; K = 256 gives each of the 8 waves one block); 2..3
+    # vectors, K = 96 and 8192 take the streaming kernels: every vector count, strided
+    # activations, rows padded by 16 bytes (and by 2, which takes the streaming kernels too) and
+    # accumulate, against the oracle
+    for B in range(2, 9):
+        pad = 16 * (B % 2) if B % 4 else 2
+        e = _gemv_case(T.Q8_0, rows, K, B, stream, seed=7 * K + B, x_stride=K + 4 * (B % 3),
+                       accumulate=B % 2 == 1, row_stride=G.row_bytes(T.Q8_0, K) + pad)
+        assert e <= REL_L2
+
+
 @pytest.mark.parametrize("ty", [t for t in ALL if t != T.BF16])
 @pytest.mark.parametrize("K", [4096, 1536, 2816])
 def test_gemv_matrix_ending_the_allocation(ty, K, stream):
