@@ -89,7 +89,10 @@ int gs_dequant_f32(int ty, const void *src, int64_t n, float *dst, void *s);
 int gs_dequant_f16(int ty, const void *src, int64_t n, void *dst, void *s); /* lib.rs:53 */
 
 /* y[b*y_stride + r] (+)= W[r] . x[b*x_stride + :], b < B (1..8); W: rows rows of K elements,
- * row_stride bytes apart (lib.rs:54-57; quants.cu:223-243) */
+ * row_stride bytes apart (lib.rs:54-57; quants.cu:223-243). Quantized formats take q8_1
+ * activations, as in every matrix-vector path here; Q8_0 with 4..8 vectors (K % 256 == 0, K <= 4096,
+ * 16-byte aligned rows and x) contracts all vectors in one int8-MFMA pass (same int8 operands and
+ * per-block scales; only the f32 summation order differs from the streaming kernels). */
 int gs_gemv(int ty, const void *W, int64_t row_stride, int K, int rows, const float *x, int64_t x_stride, float *y,
             int64_t y_stride, int B, int accumulate, void *s);
 
