@@ -451,6 +451,15 @@ def main():
                 "GB/s": round(rb["gbps"], 1), "us_per_call": round(rb["ms"] * 1e3, 2),
                 "frac_hbm_peak": round(rb["gbps"] / HBM_PEAK_GBPS, 4), "weight_bytes": rb["bytes"], "vectors": B}
             log(f"config1 B={B}: {rb['ms'] * 1e3:.2f} us, {rb['gbps']:.1f} GB/s")
+        # config 3's matrices with several vectors (multi-token decode: MTP verify)
+        for name, ty, rows, K, mk in (("config3_q4_k_gemv_k4096_rows12288", G.GgmlType.Q4_K, 12288, 4096, synth.q4_k_matrix),
+                                      ("config3_q6_k_gemv_k12288_rows4096", G.GgmlType.Q6_K, 4096, 12288, synth.q6_k_matrix)):
+            for B in (4, 8):
+                rb = run_gemv(L, s, ty, rows, K, mk, args.steps, args.warmup, 3, B=B)
+                secondary[f"{name}_B{B}"] = {
+                    "GB/s": round(rb["gbps"], 1), "us_per_call": round(rb["ms"] * 1e3, 2),
+                    "frac_hbm_peak": round(rb["gbps"] / HBM_PEAK_GBPS, 4), "weight_bytes": rb["bytes"], "vectors": B}
+                log(f"{name} B={B}: {rb['ms'] * 1e3:.2f} us")
         from glmssd import synth as S
         iq = lambda rng, rows, K: S.random_blocks(rng, G.GgmlType.IQ2_XXS, rows * K, 0.02, [0])
         q6 = lambda rng, rows, K: S.q6_k_matrix(rng, rows, K)

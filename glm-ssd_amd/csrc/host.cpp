@@ -413,17 +413,33 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
         a.accumulate = accumulate;
         return stream_any(0, ty, a, n_batch, (hipStream_t)s);
     }
-    // Q8_0 with 4..8 vectors: one pass on int8 MFMA, every weight read once for all vectors
-    // (gs_k_mv_q8_0: 16 rows and the vectors' q8_1 units in LDS; rows of whole 16-byte chunks,
-    // K % 256 == 0, up to K = 4096; 16-byte aligned rows and activations). 4096 x 4096: 8.9 us
-    // for 4 vectors, 10.3 for 8, against 9.1 and 12.4 in the streaming kernels (which read the
-    // weights twice from 5 vectors on); at 2 vectors the streaming kernel stays faster (7.1
-    // against 8.3 us: it overlaps the contraction with the weight stream)
-    if (ty == GS_Q8_0 && B >= 4 && n_batch == 1 && nv_tail == 0 && K % 256 == 0 && K <= 4096 && aligned16(x) &&
-        x_stride % 4 == 0 && aligned16(W) && row_stride % 16 == 0) {
-        MvArgs m{(const uint8_t *)W, row_stride, x, x_stride, y, y_stride, K, rows, B, accumulate};
-        const size_t U = K / 32, lds = 16 * (34 * U + 16) + 288 * U + 8 * 64 * 16;
-        return launch("gs_k_mv_q8_0", dim3((unsigned)((rows + 15) / 16)), dim3(512), lds, (hipStream_t)s, m);
+    // Vectors of Q8_0 / Q4_K / Q6_K in one pass on int8 MFMA, every weight read once for all
+    // vectors (gs_k_mv_<ty>_<0|1>: 16 rows per workgroup, the row in chunks of up to 4096 elements
+    // in LDS with the vectors' q8_1 units). Rows: whole chunks of whole 16-byte pieces, 16-byte
+    // aligned rows and activations. Taken where it beats the streaming kernels (measured, one
+    // MI355X, 4096 x 4096, 12288 x 4096, 4096 x 12288): from 5 vectors, where they read the
+    // matrix twice (Q4_K 12288 x 4096 x 8 vectors: 20.2 against 24.5 us, Q8_0 19.6 against 25.2),
+    // from 3 when rows are longer than their register plan (K > 4096: one vector per slice; Q6_K
+    // 4096 x 12288 x 4 vectors: 28.3 against 30.3 us), and for Q8_0 from 4 (4096 x 4096: 8.5
+    // against 9.1 us); below that they stay faster (they overlap the dot products with the weight
+    // stream, where this kernel waits for a tile's bytes).
+    const int mv_min = ty == GS_Q8_0 ? 4 : K > 4096 ? 3 : 5;
+    if ((ty == GS_Q8_0 || ty == GS_Q4_K || ty == GS_Q6_K) && B >= mv_min && n_batch == 1 && nv_tail == 0 &&
+        aligned16(x) && x_stride % 4 == 0 && aligned16(W) && row_stride % 16 == 0) {
+        const int ck = std::min(K, 4096);
+        const int64_t rbytes = (int64_t)(ck / qk) * bb;
+        if (K % ck == 0 && ck % qk == 0 && rbytes % 16 == 0 && rbytes <= 4352) {
+            MvArgs m{(const uint8_t *)W, row_stride, x, x_stride, y, y_stride, K, rows, B, accumulate};
+            const size_t U = ck / 32, lds = 16 * ((size_t)rbytes + 16) + 320 * U + 8 * 64 * 16;
+            // one workgroup per CU at most (its LDS), each walking tiles of 16 rows
+            hipError_t e;
+            DeviceCtx *c = ctx(&e);
+            if (!c) return e;
+            const int ntile = (rows + 15) / 16, grid = std::min(ntile, c->cu_count);
+            const bool multi = ntile > grid || K > ck;
+            return launch("gs_k_mv_" + std::to_string(ty) + (multi ? "_1" : "_0"), dim3((unsigned)grid), dim3(512), lds,
+                          (hipStream_t)s, m);
+        }
     }
     // more than 4 vectors whose units do not fit 8-vector registers (K > 2048): groups of 4 vectors
     // over the whole K instead of K slices of 8 vectors (8 x 4096 Q8_0: 14 us against 28 us), both

@@ -918,147 +918,269 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_quant_q8_1(QuantArgs a) {
 }
 
 // =============================================================================================
-// Q8_0 GEMV of 2..8 vectors on int8 MFMA (quants.cu:53-256 semantics: y[t][r] (+)= W[r] . x[t])
+// Quantized GEMV of 2..8 vectors on int8 MFMA (quants.cu:53-256 semantics: y[t][r] (+)= W[r] . x[t])
 //
-// A 32-element Q8_0 block is one v_mfma_i32_16x16x32_i8 step: weights int8 as they are stored,
-// activations the q8_1 quantization of x (the streaming kernels' arithmetic, so the same int8
-// values and f16-rounded scales). The MFMA gives the exact int32 dot of every (vector, row) pair
-// of the block for 16 rows at once; d_w * d_x then scales it into the f32 sum, as the streaming
-// kernels do per block. So each weight is read once for all vectors (the streaming kernels keep
-// at most 4 vectors' activations in registers and read the weights twice for 5..8).
-// Workgroup: 16 rows. Their bytes are copied to LDS with 16-byte loads (1 KB per wave load, where
-// fragment-shaped loads would touch 16 rows' lines per instruction), rows 16 bytes apart beyond
-// their length so the 16 rows of a fragment read sit in different banks; the vectors' q8_1 units
-// in LDS unit-major ([unit][vector][32 B]: a lane's 8 bytes for one MFMA are one conflict-free
-// read). 8 waves split the blocks of the row; their partial sums are added in wave order.
-// Rows: K % 256 == 0 (whole 16-byte chunks, nothing read past a row), K <= 4096.
+// A 32-element unit is one v_mfma_i32_16x16x32_i8 step: the format's integer weights (Q8_0 int8,
+// Q4_K nibbles, Q6_K 6-bit values - 32) against the vectors' q8_1 int8 values (quantized in the
+// workgroup with the streaming kernels' arithmetic: the same int8 values, f16-rounded scales and
+// sums). The MFMA gives the exact int32 dot of every (vector, row) pair of the unit for 16 rows at
+// once; the unit's scales then take it into the f32 sum, as the streaming kernels do per unit:
+//   Q8_0  d * d_x * dot;   Q4_K  (d*sc) * d_x * dot - (dmin*m) * s_x  (s_x = d_x * sum q_x);
+//   Q6_K  the unit's two 16-element halves have their own scales: two MFMAs, each with the other
+//         half's weight bytes zero, (d*sc_h) * d_x * dot_h summed.
+// So each weight is read once for all vectors, where the streaming kernels hold at most 4 vectors'
+// activations in registers (5..8: the matrix read twice) and, for rows beyond that register plan
+// (Q6_K K = 12288), run one vector per slice.
+// Workgroup: 16 rows, the row walked in chunks of 4096 elements. Per chunk the 16 rows' bytes go
+// to LDS with 16-byte loads (1 KB per wave load; fragment-shaped loads touched 16 rows' lines per
+// instruction), rows 16 bytes apart beyond their length so a fragment's 16 rows sit in different
+// banks; the vectors' q8_1 units in LDS unit-major ([unit][vector][32 B]: a lane's 8 bytes for one
+// MFMA are one conflict-free read). The next chunk's loads are issued before this chunk's
+// contraction. 8 waves split a chunk's units; their partial sums are added in wave order.
 // =============================================================================================
 typedef int mv_v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t mv_u4 __attribute__((ext_vector_type(4)));   // a native vector: the chunk array stays in VGPRs
-extern "C" __global__ void __launch_bounds__(512) gs_k_mv_q8_0(MvArgs a) {
+
+// 8 bytes at a 2-byte aligned LDS offset: three aligned dwords, shifted into place
+__device__ __forceinline__ uint64_t mv_ld8(const uint8_t *r, uint32_t o) {
+    const uint32_t oa = o & ~3u, sh = o & 3u;
+    const uint32_t w0 = *(const uint32_t *)(r + oa), w1 = *(const uint32_t *)(r + oa + 4), w2 = *(const uint32_t *)(r + oa + 8);
+    return (uint64_t)__builtin_amdgcn_alignbyte(w1, w0, sh) | ((uint64_t)__builtin_amdgcn_alignbyte(w2, w1, sh) << 32);
+}
+// unit u of a chunk row in LDS, lane quarter q (elements 8q .. 8q+7): the weights as int8 (b0; b1
+// the second half for HALVES formats, each with the other half zero) and the scales
+struct MvUnit {
+    uint64_t b0, b1;
+    float s0, s1, mn;
+};
+struct MvQ8_0 {
+    static constexpr int TY = GS_Q8_0, QK = 32, BB = 34;
+    static constexpr bool MIN = false, HALVES = false;
+    __device__ static __forceinline__ void unit(const uint8_t *r, int u, int q, MvUnit &m) {
+        const uint32_t blk = 34u * (uint32_t)u;
+        m.b0 = mv_ld8(r, blk + 2u + 8u * (uint32_t)q);
+        m.s0 = h2f(*(const uint16_t *)(r + blk));
+    }
+};
+struct MvQ4_K {   // lib.rs:204-218 with scale_min_k4 (lib.rs:87-93)
+    static constexpr int TY = GS_Q4_K, QK = 256, BB = 144;
+    static constexpr bool MIN = true, HALVES = false;
+    __device__ static __forceinline__ void unit(const uint8_t *r, int u, int q, MvUnit &m) {
+        const uint32_t b = (uint32_t)u >> 3, uu = (uint32_t)u & 7u, blk = 144u * b;
+        const uint64_t raw = *(const uint64_t *)(r + blk + 16u + 32u * (uu >> 1) + 8u * (uint32_t)q);
+        m.b0 = (raw >> (4u * (uu & 1u))) & 0x0f0f0f0f0f0f0f0full;
+        const uint32_t dd = *(const uint32_t *)(r + blk), sh = 8u * (uu & 3u);
+        const uint32_t b1 = (*(const uint32_t *)(r + blk + 4) >> sh) & 0xffu, b2 = (*(const uint32_t *)(r + blk + 8) >> sh) & 0xffu,
+                       b3 = (*(const uint32_t *)(r + blk + 12) >> sh) & 0xffu;
+        const uint32_t sc = uu < 4 ? (b1 & 63u) : ((b3 & 0xfu) | ((b1 >> 6) << 4));
+        const uint32_t mi = uu < 4 ? (b2 & 63u) : ((b3 >> 4) | ((b2 >> 6) << 4));
+        m.s0 = h2f(dd & 0xffffu) * (float)sc;
+        m.mn = h2f(dd >> 16) * (float)mi;
+    }
+};
+struct MvQ6_K {   // lib.rs:243-262
+    static constexpr int TY = GS_Q6_K, QK = 256, BB = 210;
+    static constexpr bool MIN = false, HALVES = true;
+    __device__ static __forceinline__ void unit(const uint8_t *r, int u, int q, MvUnit &m) {
+        const uint32_t b = (uint32_t)u >> 3, uu = (uint32_t)u & 7u, n = uu >> 2, g = uu & 3u, blk = 210u * b;
+        const uint64_t ql = mv_ld8(r, blk + 64u * n + 32u * (g & 1u) + 8u * (uint32_t)q);
+        const uint64_t qh = mv_ld8(r, blk + 128u + 32u * n + 8u * (uint32_t)q);
+        uint64_t v = ((ql >> (4u * (g >> 1))) & 0x0f0f0f0f0f0f0f0full) | (((qh >> (2u * g)) & 0x0303030303030303ull) << 4);
+        // v - 32 per byte without borrows between bytes (values 0..63)
+        v = ((v | 0x8080808080808080ull) - 0x2020202020202020ull) ^ 0x8080808080808080ull;
+        m.b0 = q < 2 ? v : 0ull;
+        m.b1 = q < 2 ? 0ull : v;
+        const float d = h2f(*(const uint16_t *)(r + blk + 208));
+        const uint32_t scw = *(const uint16_t *)(r + blk + 192u + 8u * n + 2u * g);   // the two halves' int8 scales
+        m.s0 = d * (float)(int)(int8_t)(scw & 0xffu);
+        m.s1 = d * (float)(int)(int8_t)(scw >> 8);
+    }
+};
+
+template <class F, bool MULTI>
+__device__ __forceinline__ void mv_body(const MvArgs &a) {
     extern __shared__ __align__(16) uint8_t mv_lds[];
+    constexpr int CK = 4096;                                    // elements per chunk (at most)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int U = a.K / 32, nv = a.nv;
-    const int rbytes = 34 * U, RS = rbytes + 16;               // row bytes, LDS row pitch
-    uint8_t *wl = mv_lds;                                       // [16][RS] raw rows
+    const int ck = a.K < CK ? a.K : CK, nch = a.K / ck;         // the host checks a.K % ck == 0
+    const int U = ck / 32, nv = a.nv;                           // units per chunk
+    const int rbytes = ck / F::QK * F::BB, RS = rbytes + 16;    // chunk row bytes (16-byte multiple), LDS pitch
+    uint8_t *wl = mv_lds;                                       // [16][RS] raw rows of the chunk
     uint8_t *xq = mv_lds + 16 * (size_t)RS;                     // [U][8][32] int8
     float *xd = (float *)(xq + 256 * (size_t)U);                // [U][8] f16-rounded scales
-    float *red = xd + 8 * (size_t)U;                            // [8 waves][64 lanes][4]
+    float *xs = xd + 8 * (size_t)U;                             // [U][8] scale * sum of q (MIN formats)
+    float *red = xs + 8 * (size_t)U;                            // [8 waves][64 lanes][4]
     const int r0 = blockIdx.x * 16;
+    const int ntask = nv * U * 4;                               // 8 floats per task, 4 tasks per unit
+    const int cpr = rbytes / 16, nchunk = 16 * cpr;             // 16-byte pieces per row, per tile
+    constexpr int XC = 8, WC = 9;                               // per thread: tasks, pieces (<= 4352 B rows)
 
-    // loads: the activations (8 floats per thread and task, 4 threads per unit), then the rows
-    const int ntask = nv * U * 4;
-    const int cpr = rbytes / 16, nchunk = 16 * cpr;            // 16-byte chunks per row, per tile
-    constexpr int XC = 8, WC = 9;                               // per thread: tasks, chunks (K <= 4096)
     float f[XC][8];
-#pragma unroll
-    for (int c = 0; c < XC; c++) {
-        // passes past the last task re-read a valid piece (uniform; no early exit, so the array
-        // stays in registers)
-        const int t = min(512 * c + tid, ntask - 1);
-        const int sub = t & 3, vu = t >> 2, v = vu / U, u = vu - v * U;
-        const float4 *src = (const float4 *)(a.x + (int64_t)v * a.x_stride + 32 * u + 8 * sub);
-        const float4 p0 = src[0], p1 = src[1];
-        f[c][0] = p0.x; f[c][1] = p0.y; f[c][2] = p0.z; f[c][3] = p0.w;
-        f[c][4] = p1.x; f[c][5] = p1.y; f[c][6] = p1.z; f[c][7] = p1.w;
-    }
     mv_u4 wc[WC];
-    int wdst[WC];   // LDS byte offset of the chunk (-1: none)
+    int wdst[WC];   // LDS byte offset of the piece (-1: none)
+    // divisions by U and cpr through their reciprocals (exact below 2^21), and a scheduling
+    // barrier after each load: the loads then go out as their addresses are ready, instead of
+    // after every address of the step (which the compiler otherwise computes first: ~1 us later)
+    const float rU = 1.0f / (float)U, rcpr = 1.0f / (float)cpr;
+    auto issue_x = [&](int c) __attribute__((always_inline)) {
+        const int k0 = c * ck;
 #pragma unroll
-    for (int c = 0; c < WC; c++) {
-        const int z = min(512 * c + tid, nchunk - 1), rr = z / cpr, cc = z - rr * cpr;
-        const uint8_t *row = a.w + (int64_t)min(r0 + rr, a.rows - 1) * a.row_stride;   // tail rows: clamped, dropped
-        wc[c] = *(const mv_u4 *)(row + 16 * cc);
-        wdst[c] = 512 * c + tid < nchunk ? rr * RS + 16 * cc : -1;
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int c = 0; c < XC; c++) {
-        if (512 * c >= ntask) continue;                         // uniform; quads are in or out together
-        const int t = 512 * c + tid;
-        float amax = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(f[c][e]));
-        uint32_t ab = __builtin_bit_cast(uint32_t, amax);
-        ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0xB1>(__builtin_bit_cast(float, ab))));
-        ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0x4E>(__builtin_bit_cast(float, ab))));
-        amax = __builtin_bit_cast(float, ab);
-        const float d = q8_div127(amax);
-        float id = d != 0.f ? 1.0f / d : 0.f;
-        id = id <= 3.40282347e38f ? id : 0.f;   // d < 2^-128: q = 0, as quant_unit
-        uint32_t w[2];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int qv[4];
-#pragma unroll
-            for (int b = 0; b < 4; b++) qv[b] = q8_round_mul(f[c][4 * h + b], id);
-            w[h] = __builtin_amdgcn_perm((uint32_t)qv[1], (uint32_t)qv[0], 0x0c0c0400u) |
-                   __builtin_amdgcn_perm((uint32_t)qv[3], (uint32_t)qv[2], 0x04000c0cu);
+        for (int i = 0; i < XC; i++) {
+            // passes past the last task re-read a valid piece (uniform; no early exit, so the array
+            // stays in registers)
+            const int t = min(512 * i + tid, ntask - 1);
+            const int sub = t & 3, vu = t >> 2, v = udiv_small(vu, rU), u = vu - v * U;
+            const float4 *src = (const float4 *)(a.x + (int64_t)v * a.x_stride + k0 + 32 * u + 8 * sub);
+            const float4 p0 = src[0], p1 = src[1];
+            f[i][0] = p0.x; f[i][1] = p0.y; f[i][2] = p0.z; f[i][3] = p0.w;
+            f[i][4] = p1.x; f[i][5] = p1.y; f[i][6] = p1.z; f[i][7] = p1.w;
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (t < ntask) {
-            const int sub = t & 3, vu = t >> 2, v = vu / U, u = vu - v * U;
-            *(uint2 *)(xq + 256 * (size_t)u + 32 * v + 8 * sub) = make_uint2(w[0], w[1]);
-            if (sub == 0) xd[8 * u + v] = h2f(f2h(d));
-        }
-    }
+    };
+    auto issue_w = [&](int tile, int c) __attribute__((always_inline)) {
+        const int64_t wk0 = (int64_t)(c * ck / F::QK) * F::BB;
 #pragma unroll
-    for (int c = 0; c < WC; c++)
-        if (wdst[c] >= 0) *(mv_u4 *)(wl + wdst[c]) = wc[c];
-    __syncthreads();
+        for (int i = 0; i < WC; i++) {
+            const int z = min(512 * i + tid, nchunk - 1), rr = udiv_small(z, rcpr), cc = z - rr * cpr;
+            const uint8_t *row = a.w + (int64_t)min(16 * tile + rr, a.rows - 1) * a.row_stride + wk0;   // tail rows: clamped, dropped
+            wc[i] = *(const mv_u4 *)(row + 16 * cc);
+            wdst[i] = 512 * i + tid < nchunk ? rr * RS + 16 * cc : -1;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto stage_x = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < XC; i++) {
+            if (512 * i >= ntask) continue;                      // uniform; quads are in or out together
+            const int t = 512 * i + tid;
+            float amax = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(f[i][e]));
+            uint32_t ab = __builtin_bit_cast(uint32_t, amax);
+            ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0xB1>(__builtin_bit_cast(float, ab))));
+            ab = max(ab, __builtin_bit_cast(uint32_t, quad_swap<0x4E>(__builtin_bit_cast(float, ab))));
+            amax = __builtin_bit_cast(float, ab);
+            const float d = q8_div127(amax);
+            float id = d != 0.f ? 1.0f / d : 0.f;
+            id = id <= 3.40282347e38f ? id : 0.f;   // d < 2^-128: q = 0, as quant_unit
+            uint32_t w[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                int qv[4];
+#pragma unroll
+                for (int b = 0; b < 4; b++) qv[b] = q8_round_mul(f[i][4 * h + b], id);
+                w[h] = __builtin_amdgcn_perm((uint32_t)qv[1], (uint32_t)qv[0], 0x0c0c0400u) |
+                       __builtin_amdgcn_perm((uint32_t)qv[3], (uint32_t)qv[2], 0x04000c0cu);
+            }
+            int sum = 0;
+            if (F::MIN) {   // the unit's sum of q: this thread's 8, then the quad's
+                sum = __builtin_amdgcn_sdot4((int)w[1], 0x01010101, __builtin_amdgcn_sdot4((int)w[0], 0x01010101, 0, false), false);
+                sum += __builtin_bit_cast(int, quad_swap<0xB1>(__builtin_bit_cast(float, sum)));
+                sum += __builtin_bit_cast(int, quad_swap<0x4E>(__builtin_bit_cast(float, sum)));
+            }
+            if (t < ntask) {
+                const int sub = t & 3, vu = t >> 2, v = udiv_small(vu, rU), u = vu - v * U;
+                *(uint2 *)(xq + 256 * (size_t)u + 32 * v + 8 * sub) = make_uint2(w[0], w[1]);
+                if (sub == 0) {
+                    const float dh = h2f(f2h(d));
+                    xd[8 * u + v] = dh;
+                    if (F::MIN) xs[8 * u + v] = dh * (float)sum;
+                }
+            }
+        }
+    };
 
-    // contraction: this wave's blocks of the 16 rows
     const int j = lane & 15, q = lane >> 4;
     const int ta = j & 7;                 // the lane's A row (vector); rows 8..15 repeat 0..7, dropped
     const int tq = 4 * (q & 1);           // first vector of the lane's four D rows (q >= 2: dropped)
     const uint8_t *wrow = wl + (size_t)j * RS;
     const int upw = (U + 7) / 8, u0 = wave * upw, u1 = min(U, u0 + upw);
+    // the workgroup's (tile, chunk) steps, tiles blockIdx.x, blockIdx.x + gridDim.x, ...; with one
+    // chunk per row the activations are staged once for every tile
+    // (MULTI = false: the host launched one step per workgroup, so no load is issued during a
+    // contraction and the load registers are free there)
+    const int ntile = (a.rows + 15) / 16;
+    const int nstep = MULTI ? ((ntile - 1 - (int)blockIdx.x) / (int)gridDim.x + 1) * nch : 1;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    // four blocks per step: their LDS reads and MFMAs overlap instead of each waiting on the last
-    constexpr int US = 4;
-    for (int ub = u0; ub < u1; ub += US) {
-        uint64_t wb[US], xa[US];
-        float dw[US];
-        float4 dx[US];
+    issue_x(0);
+    issue_w(blockIdx.x, 0);
+    for (int k = 0; k < nstep; k++) {
+        const int tile = blockIdx.x + (k / nch) * gridDim.x, c = k % nch;
+        __builtin_amdgcn_sched_barrier(0);
+        if (k == 0 || nch > 1) stage_x();
 #pragma unroll
-        for (int i = 0; i < US; i++) {
-            const int u = min(ub + i, u1 - 1);   // past the wave's last block: re-read it, dropped below
-            const uint32_t o = 34u * (uint32_t)u + 2u + 8u * (uint32_t)q, oa = o & ~3u, sh = o & 3u;
-            const uint32_t w0 = *(const uint32_t *)(wrow + oa), w1 = *(const uint32_t *)(wrow + oa + 4),
-                           w2 = *(const uint32_t *)(wrow + oa + 8);
-            wb[i] = (uint64_t)__builtin_amdgcn_alignbyte(w1, w0, sh) |
-                    ((uint64_t)__builtin_amdgcn_alignbyte(w2, w1, sh) << 32);
-            xa[i] = *(const uint64_t *)(xq + 256 * (size_t)u + 32 * ta + 8 * q);
-            dw[i] = h2f(*(const uint16_t *)(wrow + 34 * u));
-            dx[i] = *(const float4 *)(xd + 8 * u + tq);
+        for (int i = 0; i < WC; i++)
+            if (wdst[i] >= 0) *(mv_u4 *)(wl + wdst[i]) = wc[i];
+        __syncthreads();
+        if (MULTI && k + 1 < nstep) {   // in flight during this step's contraction
+            const int k1 = k + 1;
+            if (nch > 1) issue_x(k1 % nch);
+            issue_w(blockIdx.x + (k1 / nch) * gridDim.x, k1 % nch);
         }
-        mv_v4i dot[US];
+        // four units per step: their LDS reads and MFMAs overlap
+        constexpr int US = 4;
+        for (int ub = u0; ub < u1; ub += US) {
+            MvUnit m[US];
+            uint64_t xa[US];
+            float4 dx[US], sx[US];
 #pragma unroll
-        for (int i = 0; i < US; i++)
-            dot[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xa[i], (long)wb[i], mv_v4i{0, 0, 0, 0}, 0, 0, 0);
+            for (int i = 0; i < US; i++) {
+                const int u = min(ub + i, u1 - 1);   // past the wave's last unit: re-read it, dropped below
+                F::unit(wrow, u, q, m[i]);
+                xa[i] = *(const uint64_t *)(xq + 256 * (size_t)u + 32 * ta + 8 * q);
+                dx[i] = *(const float4 *)(xd + 8 * u + tq);
+                if (F::MIN) sx[i] = *(const float4 *)(xs + 8 * u + tq);
+            }
+            mv_v4i dot0[US], dot1[US];
 #pragma unroll
-        for (int i = 0; i < US; i++) {
-            if (ub + i < u1) {   // uniform
-                acc[0] += (float)dot[i][0] * (dw[i] * dx[i].x);
-                acc[1] += (float)dot[i][1] * (dw[i] * dx[i].y);
-                acc[2] += (float)dot[i][2] * (dw[i] * dx[i].z);
-                acc[3] += (float)dot[i][3] * (dw[i] * dx[i].w);
+            for (int i = 0; i < US; i++) {
+                dot0[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xa[i], (long)m[i].b0, mv_v4i{0, 0, 0, 0}, 0, 0, 0);
+                if (F::HALVES)
+                    dot1[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xa[i], (long)m[i].b1, mv_v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < US; i++) {
+                if (ub + i >= u1) continue;   // uniform
+                const float e[4] = {dx[i].x, dx[i].y, dx[i].z, dx[i].w};
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    if (F::HALVES) acc[kk] += ((float)dot0[i][kk] * m[i].s0 + (float)dot1[i][kk] * m[i].s1) * e[kk];
+                    else acc[kk] += (float)dot0[i][kk] * (m[i].s0 * e[kk]);
+                }
+                if (F::MIN) {
+                    acc[0] -= m[i].mn * sx[i].x;
+                    acc[1] -= m[i].mn * sx[i].y;
+                    acc[2] -= m[i].mn * sx[i].z;
+                    acc[3] -= m[i].mn * sx[i].w;
+                }
             }
         }
-    }
-    *(float4 *)(red + 4 * (64 * wave + lane)) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    __syncthreads();
-    if (tid < 16 * 8) {
-        const int t = tid >> 4, jj = tid & 15, r = r0 + jj;
-        const int src = 16 * (t >> 2) + jj, i = t & 3;   // the lane that holds D[t][jj]
-        float sum = 0.f;
+        if (c == nch - 1) {   // the tile's last chunk: the waves' partial sums, in wave order
+            *(float4 *)(red + 4 * (64 * wave + lane)) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            acc[0] = acc[1] = acc[2] = acc[3] = 0.f;
+            __syncthreads();
+            if (tid < 16 * 8) {
+                const int t = tid >> 4, jj = tid & 15, r = 16 * tile + jj;
+                const int src = 16 * (t >> 2) + jj, i = t & 3;   // the lane that holds D[t][jj]
+                float sum = 0.f;
 #pragma unroll
-        for (int w = 0; w < 8; w++) sum += red[4 * (64 * w + src) + i];
-        if (t < nv && r < a.rows) {
-            float *dst = a.y + (int64_t)t * a.y_stride + r;
-            *dst = a.accumulate ? *dst + sum : sum;
+                for (int w = 0; w < 8; w++) sum += red[4 * (64 * w + src) + i];
+                if (t < nv && r < a.rows) {
+                    float *dst = a.y + (int64_t)t * a.y_stride + r;
+                    *dst = a.accumulate ? *dst + sum : sum;
+                }
+            }
         }
+        __syncthreads();   // every wave is done with this step's LDS before the next is stored
     }
 }
+// _0: one (tile, chunk) step per workgroup; _1: a walk over several
+#define GS_MV_KERNELS(TY, F)                                                                     \
+    extern "C" __global__ void __launch_bounds__(512) gs_k_mv_##TY##_0(MvArgs a) { mv_body<F, false>(a); } \
+    extern "C" __global__ void __launch_bounds__(512) gs_k_mv_##TY##_1(MvArgs a) { mv_body<F, true>(a); }
+GS_MV_KERNELS(8, MvQ8_0)
+GS_MV_KERNELS(12, MvQ4_K)
+GS_MV_KERNELS(14, MvQ6_K)
 
 // =============================================================================================
 // Element-wise and row kernels of the MoE glue (ops.cu:101-125, gemm.cu:125-163)

@@ -182,17 +182,21 @@ def test_gemv_matches_oracle(ty, rows, K, stream):
         assert _gemv_case(ty, rows, K, B, stream, seed=1000 * ty + rows + B) <= (REL_L2_F32 if ty in FLOAT else REL_L2)
 
 
-@pytest.mark.parametrize("rows,K", [(37, 256), (200, 1024), (1000, 4096), (45, 96), (64, 8192)])
-def test_gemv_q8_0_vectors_on_mfma(rows, K, stream):
-    # Q8_0 with 4..8 vectors and K % 256 == 0 up to 4096 runs as one int8-MFMA pass (16-row
-    # tiles, a tail tile in each shape; K = 256 gives each of the 8 waves one block); 2..3
-    # vectors, K = 96 and 8192 take the streaming kernels: every vector count, strided
-    # activations, rows padded by 16 bytes (and by 2, which takes the streaming kernels too) and
+@pytest.mark.parametrize("ty,rows,K", [(T.Q8_0, 37, 256), (T.Q8_0, 200, 1024), (T.Q8_0, 1000, 4096), (T.Q8_0, 45, 96),
+                                        (T.Q8_0, 64, 8192), (T.Q4_K, 37, 256), (T.Q4_K, 300, 4096), (T.Q4_K, 61, 12288),
+                                        (T.Q6_K, 33, 2048), (T.Q6_K, 200, 4096), (T.Q6_K, 61, 12288), (T.Q6_K, 40, 256)])
+def test_gemv_vectors_on_mfma(ty, rows, K, stream):
+    # Q8_0 (from 4 vectors) and Q4_K / Q6_K (from 5, from 3 with K > 4096) run as one int8-MFMA
+    # pass, fewer vectors on the streaming kernels (both checked here): 16-row tiles (a
+    # tail tile in each shape), the row in chunks of up to 4096 elements (K = 8192 and 12288: two
+    # and three chunks; K = 256 gives each of the 8 waves at most one unit). Q8_0 with K = 96 and
+    # Q6_K with K = 256 (rows not whole 16-byte pieces) take the streaming kernels, as do rows
+    # padded by 2 bytes: every vector count, strided activations, rows padded by 16 bytes and
     # accumulate, against the oracle
     for B in range(2, 9):
         pad = 16 * (B % 2) if B % 4 else 2
-        e = _gemv_case(T.Q8_0, rows, K, B, stream, seed=7 * K + B, x_stride=K + 4 * (B % 3),
-                       accumulate=B % 2 == 1, row_stride=G.row_bytes(T.Q8_0, K) + pad)
+        e = _gemv_case(ty, rows, K, B, stream, seed=7 * K + B + 100 * ty, x_stride=K + 4 * (B % 3),
+                       accumulate=B % 2 == 1, row_stride=G.row_bytes(ty, K) + pad)
         assert e <= REL_L2
 
 
