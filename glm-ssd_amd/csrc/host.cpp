@@ -413,7 +413,7 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
         a.accumulate = accumulate;
         return stream_any(0, ty, a, n_batch, (hipStream_t)s);
     }
-    // Vectors of Q8_0 / Q4_K / Q6_K in one pass on int8 MFMA, every weight read once for all
+    // Vectors of Q8_0 / Q4_K / Q5_K / Q6_K in one pass on int8 MFMA, every weight read once for all
     // vectors (gs_k_mv_<ty>_<0|1>: 16 rows per workgroup, the row in chunks of up to 4096 elements
     // in LDS with the vectors' q8_1 units). Rows: whole chunks of whole 16-byte pieces, 16-byte
     // aligned rows and activations. Taken where it beats the streaming kernels (measured, one
@@ -424,7 +424,7 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
     // against 9.1 us); below that they stay faster (they overlap the dot products with the weight
     // stream, where this kernel waits for a tile's bytes).
     const int mv_min = ty == GS_Q8_0 ? 4 : K > 4096 ? 3 : 5;
-    if ((ty == GS_Q8_0 || ty == GS_Q4_K || ty == GS_Q6_K) && B >= mv_min && n_batch == 1 && nv_tail == 0 &&
+    if ((ty == GS_Q8_0 || ty == GS_Q4_K || ty == GS_Q5_K || ty == GS_Q6_K) && B >= mv_min && n_batch == 1 && nv_tail == 0 &&
         aligned16(x) && x_stride % 4 == 0 && aligned16(W) && row_stride % 16 == 0) {
         const int ck = std::min(K, 4096);
         const int64_t rbytes = (int64_t)(ck / qk) * bb;

@@ -921,11 +921,11 @@ extern "C" __global__ void __launch_bounds__(256) gs_k_quant_q8_1(QuantArgs a) {
 // Quantized GEMV of 2..8 vectors on int8 MFMA (quants.cu:53-256 semantics: y[t][r] (+)= W[r] . x[t])
 //
 // A 32-element unit is one v_mfma_i32_16x16x32_i8 step: the format's integer weights (Q8_0 int8,
-// Q4_K nibbles, Q6_K 6-bit values - 32) against the vectors' q8_1 int8 values (quantized in the
+// Q4_K nibbles, Q5_K 5-bit values, Q6_K 6-bit values - 32) against the vectors' q8_1 int8 values (quantized in the
 // workgroup with the streaming kernels' arithmetic: the same int8 values, f16-rounded scales and
 // sums). The MFMA gives the exact int32 dot of every (vector, row) pair of the unit for 16 rows at
 // once; the unit's scales then take it into the f32 sum, as the streaming kernels do per unit:
-//   Q8_0  d * d_x * dot;   Q4_K  (d*sc) * d_x * dot - (dmin*m) * s_x  (s_x = d_x * sum q_x);
+//   Q8_0  d * d_x * dot;   Q4_K, Q5_K  (d*sc) * d_x * dot - (dmin*m) * s_x  (s_x = d_x * sum q_x);
 //   Q6_K  the unit's two 16-element halves have their own scales: two MFMAs, each with the other
 //         half's weight bytes zero, (d*sc_h) * d_x * dot_h summed.
 // So each weight is read once for all vectors, where the streaming kernels hold at most 4 vectors'
@@ -969,6 +969,23 @@ struct MvQ4_K {   // lib.rs:204-218 with scale_min_k4 (lib.rs:87-93)
         const uint32_t b = (uint32_t)u >> 3, uu = (uint32_t)u & 7u, blk = 144u * b;
         const uint64_t raw = *(const uint64_t *)(r + blk + 16u + 32u * (uu >> 1) + 8u * (uint32_t)q);
         m.b0 = (raw >> (4u * (uu & 1u))) & 0x0f0f0f0f0f0f0f0full;
+        const uint32_t dd = *(const uint32_t *)(r + blk), sh = 8u * (uu & 3u);
+        const uint32_t b1 = (*(const uint32_t *)(r + blk + 4) >> sh) & 0xffu, b2 = (*(const uint32_t *)(r + blk + 8) >> sh) & 0xffu,
+                       b3 = (*(const uint32_t *)(r + blk + 12) >> sh) & 0xffu;
+        const uint32_t sc = uu < 4 ? (b1 & 63u) : ((b3 & 0xfu) | ((b1 >> 6) << 4));
+        const uint32_t mi = uu < 4 ? (b2 & 63u) : ((b3 >> 4) | ((b2 >> 6) << 4));
+        m.s0 = h2f(dd & 0xffffu) * (float)sc;
+        m.mn = h2f(dd >> 16) * (float)mi;
+    }
+};
+struct MvQ5_K {   // lib.rs:221-240: Q4_K's nibbles and scales, bit u of qh[l] as the fifth bit
+    static constexpr int TY = GS_Q5_K, QK = 256, BB = 176;
+    static constexpr bool MIN = true, HALVES = false;
+    __device__ static __forceinline__ void unit(const uint8_t *r, int u, int q, MvUnit &m) {
+        const uint32_t b = (uint32_t)u >> 3, uu = (uint32_t)u & 7u, blk = 176u * b;
+        const uint64_t raw = *(const uint64_t *)(r + blk + 48u + 32u * (uu >> 1) + 8u * (uint32_t)q);
+        const uint64_t qh = *(const uint64_t *)(r + blk + 16u + 8u * (uint32_t)q);
+        m.b0 = ((raw >> (4u * (uu & 1u))) & 0x0f0f0f0f0f0f0f0full) | (((qh >> uu) & 0x0101010101010101ull) << 4);
         const uint32_t dd = *(const uint32_t *)(r + blk), sh = 8u * (uu & 3u);
         const uint32_t b1 = (*(const uint32_t *)(r + blk + 4) >> sh) & 0xffu, b2 = (*(const uint32_t *)(r + blk + 8) >> sh) & 0xffu,
                        b3 = (*(const uint32_t *)(r + blk + 12) >> sh) & 0xffu;
@@ -1180,6 +1197,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &a) {
     extern "C" __global__ void __launch_bounds__(512) gs_k_mv_##TY##_1(MvArgs a) { mv_body<F, true>(a); }
 GS_MV_KERNELS(8, MvQ8_0)
 GS_MV_KERNELS(12, MvQ4_K)
+GS_MV_KERNELS(13, MvQ5_K)
 GS_MV_KERNELS(14, MvQ6_K)
 
 // =============================================================================================
