@@ -420,10 +420,10 @@ static int gemv_impl(int ty, const void *W, int64_t row_stride, int K, int rows,
     // MI355X, 4096 x 4096, 12288 x 4096, 4096 x 12288): from 5 vectors, where they read the
     // matrix twice (Q4_K 12288 x 4096 x 8 vectors: 20.2 against 24.5 us, Q8_0 19.6 against 25.2),
     // from 3 when rows are longer than their register plan (K > 4096: one vector per slice; Q6_K
-    // 4096 x 12288 x 4 vectors: 28.3 against 30.3 us), and for Q8_0 from 4 (4096 x 4096: 8.5
-    // against 9.1 us); below that they stay faster (they overlap the dot products with the weight
-    // stream, where this kernel waits for a tile's bytes).
-    const int mv_min = ty == GS_Q8_0 ? 4 : K > 4096 ? 3 : 5;
+    // 4096 x 12288 x 4 vectors: 26.4 against 30.3 us), and for Q8_0 from 3 (4096 x 4096: 7.8 against
+    // 8.5 us at 3 vectors, 7.9 against 9.2 at 4); below that they stay faster (they overlap the dot
+    // products with the weight stream, where this kernel waits for a tile's bytes).
+    const int mv_min = ty == GS_Q8_0 || K > 4096 ? 3 : 5;
     if ((ty == GS_Q8_0 || ty == GS_Q4_K || ty == GS_Q5_K || ty == GS_Q6_K) && B >= mv_min && n_batch == 1 && nv_tail == 0 &&
         aligned16(x) && x_stride % 4 == 0 && aligned16(W) && row_stride % 16 == 0) {
         const int ck = std::min(K, 4096);

@@ -90,7 +90,7 @@ int gs_dequant_f16(int ty, const void *src, int64_t n, void *dst, void *s); /* l
 
 /* y[b*y_stride + r] (+)= W[r] . x[b*x_stride + :], b < B (1..8); W: rows rows of K elements,
  * row_stride bytes apart (lib.rs:54-57; quants.cu:223-243). Quantized formats take q8_1
- * activations, as in every matrix-vector path here. Several vectors of Q8_0 (from 4), Q4_K, Q5_K
+ * activations, as in every matrix-vector path here. Several vectors of Q8_0 (from 3), Q4_K, Q5_K
  * and Q6_K (from 5, from 3 when K > 4096) contract in one int8-MFMA pass when rows are whole 4096-element
  * chunks (or one shorter chunk) of whole 16-byte pieces and rows and x are 16-byte aligned: the
  * same int8 operands and per-unit scales, only the f32 summation order differs. */

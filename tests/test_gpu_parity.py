@@ -187,7 +187,7 @@ def test_gemv_matches_oracle(ty, rows, K, stream):
                                         (T.Q6_K, 33, 2048), (T.Q6_K, 200, 4096), (T.Q6_K, 61, 12288), (T.Q6_K, 40, 256),
                                         (T.Q5_K, 77, 4096), (T.Q5_K, 30, 8192)])
 def test_gemv_vectors_on_mfma(ty, rows, K, stream):
-    # Q8_0 (from 4 vectors) and Q4_K / Q5_K / Q6_K (from 5, from 3 with K > 4096) run as one int8-MFMA
+    # Q8_0 (from 3 vectors) and Q4_K / Q5_K / Q6_K (from 5, from 3 with K > 4096) run as one int8-MFMA
     # pass, fewer vectors on the streaming kernels (both checked here): 16-row tiles (a
     # tail tile in each shape), the row in chunks of up to 4096 elements (K = 8192 and 12288: two
     # and three chunks; K = 256 gives each of the 8 waves at most one unit). Q8_0 with K = 96 and
