@@ -1112,27 +1112,30 @@ __device__ __forceinline__ void mv_body(const MvArgs &a) {
     const int tq = 4 * (q & 1);           // first vector of the lane's four D rows (q >= 2: dropped)
     const uint8_t *wrow = wl + (size_t)j * RS;
     const int upw = (U + 7) / 8, u0 = wave * upw, u1 = min(U, u0 + upw);
-    // the workgroup's (tile, chunk) steps, tiles blockIdx.x, blockIdx.x + gridDim.x, ...; with one
-    // chunk per row the activations are staged once for every tile
+    // the workgroup's (chunk, tile) steps, chunk-major over its tiles blockIdx.x, blockIdx.x +
+    // gridDim.x, ...: the activations of a chunk are staged once for all the workgroup's tiles, and
+    // with several tiles each step adds its chunk's partial sums into y (chunk 0 stores them), in
+    // chunk order; a single tile keeps them in registers until its last chunk
     // (MULTI = false: the host launched one step per workgroup, so no load is issued during a
     // contraction and the load registers are free there)
     const int ntile = (a.rows + 15) / 16;
-    const int nstep = MULTI ? ((ntile - 1 - (int)blockIdx.x) / (int)gridDim.x + 1) * nch : 1;
+    const int ntw = MULTI ? (ntile - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 1;   // tiles of this workgroup
+    const int nstep = MULTI ? ntw * nch : 1;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     issue_x(0);
     issue_w(blockIdx.x, 0);
     for (int k = 0; k < nstep; k++) {
-        const int tile = blockIdx.x + (k / nch) * gridDim.x, c = k % nch;
+        const int c = k / ntw, ti = k - c * ntw, tile = blockIdx.x + ti * gridDim.x;
         __builtin_amdgcn_sched_barrier(0);
-        if (k == 0 || nch > 1) stage_x();
+        if (ti == 0) stage_x();
 #pragma unroll
         for (int i = 0; i < WC; i++)
             if (wdst[i] >= 0) *(mv_u4 *)(wl + wdst[i]) = wc[i];
         __syncthreads();
         if (MULTI && k + 1 < nstep) {   // in flight during this step's contraction
-            const int k1 = k + 1;
-            if (nch > 1) issue_x(k1 % nch);
-            issue_w(blockIdx.x + (k1 / nch) * gridDim.x, k1 % nch);
+            const int k1 = k + 1, c1 = k1 / ntw, t1 = k1 - c1 * ntw;
+            if (t1 == 0) issue_x(c1);
+            issue_w(blockIdx.x + t1 * gridDim.x, c1);
         }
         // four units per step: their LDS reads and MFMAs overlap
         constexpr int US = 4;
@@ -1172,7 +1175,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &a) {
                 }
             }
         }
-        if (c == nch - 1) {   // the tile's last chunk: the waves' partial sums, in wave order
+        if (ntw > 1 || c == nch - 1) {   // the waves' partial sums, in wave order
             *(float4 *)(red + 4 * (64 * wave + lane)) = make_float4(acc[0], acc[1], acc[2], acc[3]);
             acc[0] = acc[1] = acc[2] = acc[3] = 0.f;
             __syncthreads();
@@ -1184,7 +1187,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &a) {
                 for (int w = 0; w < 8; w++) sum += red[4 * (64 * w + src) + i];
                 if (t < nv && r < a.rows) {
                     float *dst = a.y + (int64_t)t * a.y_stride + r;
-                    *dst = a.accumulate ? *dst + sum : sum;
+                    *dst = a.accumulate || (ntw > 1 && c > 0) ? *dst + sum : sum;
                 }
             }
         }

@@ -186,11 +186,13 @@ def test_gemv_matches_oracle(ty, rows, K, stream):
                                         (T.Q8_0, 64, 8192), (T.Q4_K, 37, 256), (T.Q4_K, 300, 4096), (T.Q4_K, 61, 12288),
                                         (T.Q6_K, 33, 2048), (T.Q6_K, 200, 4096), (T.Q6_K, 61, 12288), (T.Q6_K, 40, 256),
                                         (T.Q5_K, 77, 4096), (T.Q5_K, 30, 8192),
-                                        (T.Q4_K, 4200, 4096), (T.Q6_K, 4111, 2048), (T.Q5_K, 4113, 1024)])
+                                        (T.Q4_K, 4200, 4096), (T.Q6_K, 4111, 2048), (T.Q5_K, 4113, 1024),
+                                        (T.Q4_K, 4200, 8192), (T.Q6_K, 4111, 12288)])
 def test_gemv_vectors_on_mfma(ty, rows, K, stream):
     # Q8_0 (from 3 vectors) and Q4_K / Q5_K / Q6_K (from 5, from 3 with K > 4096) run as one
     # int8-MFMA pass, fewer vectors on the streaming kernels (both checked here; the ~4100-row shapes
-    # have more 16-row tiles than CUs, so each workgroup walks several): 16-row tiles (a
+    # have more 16-row tiles than CUs, so each workgroup walks several, with K > 4096 over every
+    # chunk of the row): 16-row tiles (a
     # tail tile in each shape), the row in chunks of up to 4096 elements (K = 8192 and 12288: two
     # and three chunks; K = 256 gives each of the 8 waves at most one unit). Q8_0 with K = 96 and
     # Q6_K with K = 256 (rows not whole 16-byte pieces) take the streaming kernels, as do rows
