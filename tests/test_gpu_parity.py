@@ -187,7 +187,8 @@ def test_gemv_matches_oracle(ty, rows, K, stream):
                                         (T.Q6_K, 33, 2048), (T.Q6_K, 200, 4096), (T.Q6_K, 61, 12288), (T.Q6_K, 40, 256),
                                         (T.Q5_K, 77, 4096), (T.Q5_K, 30, 8192),
                                         (T.Q4_K, 4200, 4096), (T.Q6_K, 4111, 2048), (T.Q5_K, 4113, 1024),
-                                        (T.Q4_K, 4200, 8192), (T.Q6_K, 4111, 12288)])
+                                        (T.Q4_K, 4200, 8192), (T.Q6_K, 4111, 12288),
+                                        (T.Q8_0, 4200, 2048), (T.Q5_K, 4113, 2048)])
 def test_gemv_vectors_on_mfma(ty, rows, K, stream):
     # Q8_0 (from 3 vectors) and Q4_K / Q5_K / Q6_K (from 5, from 3 with K > 4096) run as one
     # int8-MFMA pass, fewer vectors on the streaming kernels (both checked here; the ~4100-row shapes
