@@ -619,39 +619,6 @@ __device__ __forceinline__ void signed_dot8x4(const uint2 (&g_)[4], const uint2 
     }
 }
 
-// A unit decoded ahead of its activations (the one-token down pass does this while its activation
-// staging is in flight): grid bytes with the signs applied, 2s+1 and the block scale. dot_pre is then
-// the integer dot and scaling of signed_dot8x4<NV, false>, operation for operation (same result).
-struct PreUnit {
-    uint2 g[4];
-    int m;
-    float dh;
-};
-__device__ __forceinline__ void pre_unit(const uint2 (&g)[4], const uint2 (&s)[4], float dh, int m, PreUnit &p) {
-#pragma unroll
-    for (int l = 0; l < 4; l++) {
-        p.g[l].x = __builtin_amdgcn_perm(0x01010100u - g[l].x, g[l].x, s[l].x);
-        p.g[l].y = __builtin_amdgcn_perm(0x01010100u - g[l].y, g[l].y, s[l].y);
-    }
-    p.m = m;
-    p.dh = dh;
-}
-template <int NV>
-__device__ __forceinline__ void dot_pre(const PreUnit &p, const XU (&x)[NV], int nv, float (&r)[NV]) {
-#pragma unroll
-    for (int t = 0; t < NV; t++) {
-        if (NV == 1 || t < nv) {
-            int acc = 0;
-#pragma unroll
-            for (int l = 0; l < 4; l++) {
-                acc = l == 0 ? sdot4_0(p.g[l].x, x[t].q[2 * l]) : __builtin_amdgcn_sdot4((int)p.g[l].x, (int)x[t].q[2 * l], acc, false);
-                acc = __builtin_amdgcn_sdot4((int)p.g[l].y, (int)x[t].q[2 * l + 1], acc, false);
-            }
-            r[t] += (p.dh * x[t].D) * (float)__mul24(acc, p.m);
-        }
-    }
-}
-
 struct FIQ2_XXS : UnitGeom<256, 66> {
     static constexpr int TYPE = GS_IQ2_XXS, QK = 256, BB = 66, TAB = 0, RAW = 3;
     static constexpr bool NEG_X = true;
@@ -693,12 +660,6 @@ struct FIQ2_XXS : UnitGeom<256, 66> {
         }
 #pragma unroll
         for (int l = 0; l < 4; l++) e.s[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_sel_lds + sofs[l]);
-    }
-    static constexpr bool PRE = true;
-    __device__ static __forceinline__ void predecode(const Raw &w, PreUnit &p) {
-        Dec e;
-        fetch(w, e);
-        pre_unit(e.g, e.s, h2f(w.d), (int)((w.a.y >> 27) | 1u), p);
     }
     template <int NV, bool XNEG = true>
     __device__ static __forceinline__ void dot2(const Raw &w, const Dec &e, const XU (&x)[NV], int nv, float (&r)[NV]) {
@@ -877,12 +838,6 @@ struct FIQ3_XXS : UnitGeom<256, 98> {
         const uint32_t sofs[4] = {sel_off<0>(w.s), sel_off<1>(w.s), sel_off<2>(w.s), sel_off<3>(w.s)};
 #pragma unroll
         for (int l = 0; l < 4; l++) e.s[l] = *(const uint2 *)((const uint8_t *)gs_iq2xxs_sel_lds + sofs[l]);
-    }
-    static constexpr bool PRE = true;
-    __device__ static __forceinline__ void predecode(const Raw &w, PreUnit &p) {
-        Dec e;
-        fetch(w, e);
-        pre_unit(e.g, e.s, h2f(w.d), (int)((w.s >> 27) | 1u), p);
     }
     template <int NV, bool XNEG = true>
     __device__ static __forceinline__ void dot2(const Raw &w, const Dec &e, const XU (&x)[NV], int nv, float (&r)[NV]) {

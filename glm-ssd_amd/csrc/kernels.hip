@@ -263,11 +263,6 @@ __device__ __forceinline__ int udiv_small(int u, float rd) { return (int)(((floa
 // one 16-byte read for both units' indices, half the vector-memory instructions of two loads
 // (Paired, declared with pf_depth above).
 
-// Formats whose units can be decoded ahead of the activations (PreUnit, predecode, dot_pre)
-template <class A, class B> struct is_same_t { static constexpr bool value = false; };
-template <class A> struct is_same_t<A, A> { static constexpr bool value = true; };
-template <class F, class = void> struct HasPre { static constexpr bool value = false; };
-template <class F> struct HasPre<F, decltype((void)F::PRE, void())> { static constexpr bool value = F::PRE; };
 
 template <bool B> struct BoolC { static constexpr bool value = B; };
 
@@ -317,10 +312,6 @@ struct StreamPass {
     typename F::TabReg treg;
     typename F::Raw R[PF][UMAX];
     float wtl[NV];   // DOWN: lane i holds vector t's combine weight for expert i
-    // one-token 64-lane down with an IQ format: the batch's units decoded ahead of the activations
-    // (at most 12 units: 10 registers each)
-    static constexpr bool PRE = KIND == 2 && LP == 64 && NV == 1 && !XNEG && HasPre<F>::value && PF * UX <= 12;
-    PreUnit P[PRE ? PF : 1][PRE ? UX : 1];
 
     // geometry of this pass; issues no memory access except the pointer-table load (DOWN/GATEUP)
     __device__ __forceinline__ StreamPass(const StreamArgs &a_, uint8_t *smem) : a(a_) {
@@ -571,25 +562,14 @@ struct StreamPass {
         }
     }
 
-    // PRE: decode the first batch's units (waits for their weights; the tables must be staged)
-    __device__ __forceinline__ void predecode() {
-        if constexpr (PRE) {
-#pragma unroll
-            for (int p = 0; p < PF; p++)
-#pragma unroll
-                for (int j = 0; j < UX; j++) F::predecode(R[p][j], P[p][j]);
-        }
-    }
-    // whether this wave's rows fit one batch (then run_rows<true> can use the predecoded units)
+    // whether this wave's rows fit one batch
     __device__ __forceinline__ bool single_batch() const {
         return __builtin_amdgcn_readfirstlane(gid) + PF * ngroups >= nrow;
     }
 
     // activation units from LDS into registers, then every batch of rows (the first batch is
-    // already loaded) with the results stored. USE_PRE: one batch whose units predecode() decoded.
-    template <bool USE_PRE = false>
+    // already loaded) with the results stored.
     __device__ __forceinline__ void run_rows() {
-        static_assert(!USE_PRE || PRE, "predecoded rows need a PRE pass");
         const uint32_t *xm = (const uint32_t *)(xq + (size_t)nxv * K);
         XU xr[UX][NV];
 #pragma unroll
@@ -629,17 +609,13 @@ struct StreamPass {
             // units of the batch in order (row p, unit j), each one's table reads issued one unit
             // ahead (reads of rows past the end fetch valid table entries and are unused)
             typename TP::Dec dec[2];
-            if (!USE_PRE) TP::fetch(R[0][0], dec[0]);
+            TP::fetch(R[0][0], dec[0]);
 #pragma unroll
             for (int p = 0; p < PF; p++) {
                 float acc0[NV], acc1[NV];
 #pragma unroll
                 for (int t = 0; t < NV; t++) acc0[t] = acc1[t] = 0.f;
                 if (base + p * ngroups < nrow) {   // no loads inside: the waits stay exact
-                    if constexpr (USE_PRE) {
-#pragma unroll
-                        for (int j = 0; j < UX; j++) dot_pre<NV>(P[PRE ? p : 0][PRE ? j : 0], xr[j], nv, acc0);
-                    } else
 #pragma unroll
                     for (int j = 0; j < UMAX; j++) {
                         const int i = p * UMAX + j;
@@ -659,7 +635,7 @@ struct StreamPass {
                         else
                             TP::template dot<NV, XNEG>(R[p][j], dec[i & 1], usub[jx], tab, xr[jx], nv, acc0);
                     }
-                } else if (!USE_PRE && p + 1 < PF) {
+                } else if (p + 1 < PF) {
                     TP::fetch(R[p + 1][0], dec[((p + 1) * UMAX) & 1]);
                 }
                 if (ISSUE) {   // kept after the slot's last use: hoisted above it, the loads would
@@ -719,7 +695,7 @@ struct StreamPass {
                 }
             }
         };
-        if (USE_PRE || (RING && single_batch())) {   // one batch: no refills
+        if (RING && single_batch()) {   // one batch: no refills
             if (gid < nrow) batch(gid, BoolC<false>{});
             return;
         }
