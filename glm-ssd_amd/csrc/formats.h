@@ -155,6 +155,56 @@ struct FQ8_0 : UnitGeom<32, 34>, NoTable {
     }
 };
 
+// Q8_0 with aligned loads (FQ8_0A: the one-vector GEMV over many rows). The 34-byte blocks put
+// every other block's quants at a 2-byte aligned address, and 16-byte loads there stream about a
+// third slower than 4-byte aligned ones (measured: 4.9 against 6.5 TB/s over 1 GiB). A lane's unit
+// pair (two consecutive blocks) therefore reads each unit's 32 quant bytes as the 36-byte
+// dword-aligned window around them (two 16-byte loads and one 4-byte load) and shifts them into
+// place (v_alignbyte); the shift (0 or 2 bytes) rides in the high half of the scale word. That
+// costs 8 more VALU per unit and 8 load instructions per pair instead of 6, so a GEMV with few
+// rows per wave (4096 x 4096) stays on FQ8_0. Nothing past the pair's 68 bytes is read but the
+// rest of the dword holding its last two bytes (4-byte aligned, so never on another page); a
+// window whose last dword is not needed (no shift) repeats the one before it instead.
+struct FQ8_0A : UnitGeom<32, 34>, NoTable {
+    static constexpr int TYPE = GS_Q8_0, QK = 32, BB = 34, TAB = 0, RAW = 10;
+    struct Raw { uint4 lo, hi; uint32_t x8, d; };   // d: f16 scale | byte shift << 16
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int, Raw &w) {
+        w.d = m.u16(o);
+        w.lo = m.u128(o + 2);
+        w.hi = m.u128(o + 18);
+        w.x8 = 0;
+    }
+    static constexpr bool PAIR = true;
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int, Raw &w0, Raw &w1) {
+        const uint32_t a = (uint32_t)(uintptr_t)m.ptr(o) & 3u;   // 0 or 2: rows are 2-byte aligned
+        const uint32_t s0 = (a + 2u) & 3u, s1 = a;                 // shifts of the quants at o+2, o+36
+        const uint32_t o0 = o + 2u - s0, o1 = o + 36u - s1;        // their 4-byte aligned windows
+        w0.d = m.u16(o) | (s0 << 16);
+        w1.d = m.u16(o + 34u) | (s1 << 16);
+        w0.lo = m.u128(o0);
+        w0.hi = m.u128(o0 + 16u);
+        w0.x8 = m.u32(o0 + (s0 ? 32u : 28u));
+        w1.lo = m.u128(o1);
+        w1.hi = m.u128(o1 + 16u);
+        w1.x8 = m.u32(o1 + (s1 ? 32u : 28u));
+    }
+    template <int NV, bool XNEG = false>
+    __device__ static __forceinline__ void dot(const Raw &w, int, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const float d = h2f(w.d & 0xffffu);
+        const uint32_t sh = w.d >> 16;
+        const uint32_t dw[9] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w, w.hi.x, w.hi.y, w.hi.z, w.hi.w, w.x8};
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = __builtin_amdgcn_alignbyte(dw[i + 1], dw[i], sh);
+#pragma unroll
+        for (int t = 0; t < NV; t++)
+            if (NV == 1 || t < nv) r[t] += (d * x[t].D) * (float)dot8(q, x[t].q);
+    }
+};
+
 struct FQ4_K : UnitGeom<256, 144>, NoTable {
     static constexpr int TYPE = GS_Q4_K, QK = 256, BB = 144, TAB = 0, RAW = 12;
     struct Raw { uint4 hd, lo, hi; };   // bytes 0..15 (d, dmin, scales[12]); 32 quant bytes

@@ -206,6 +206,41 @@ def test_gemv_vectors_on_mfma(ty, rows, K, stream):
         assert e <= REL_L2
 
 
+@pytest.mark.parametrize("rows,K,pad,acc", [(8200, 4096, 0, False), (8200, 4096, 2, True), (9000, 2048, 2, False),
+                                          (8192, 8192, 2, False)])
+def test_gemv_q8_0_aligned_pairs(rows, K, pad, acc, stream):
+    # one Q8_0 vector over at least 4 rows per wave takes the aligned-pair kernel (_wa): each
+    # unit's quants from a dword-aligned window, shifted into place; with rows 2 bytes past a
+    # multiple of 4 apart (pad 2) rows start alternately at 0 and 2 mod 4, so both shifts run
+    e = _gemv_case(T.Q8_0, rows, K, 1, stream, seed=rows + K + pad, accumulate=acc,
+                   row_stride=G.row_bytes(T.Q8_0, K) + pad)
+    assert e <= REL_L2
+
+
+@pytest.mark.parametrize("pad", [0, 2])
+def test_gemv_q8_0_aligned_pairs_ending_the_allocation(pad, stream):
+    # the aligned-pair kernel on a matrix whose last row ends at the end of an allocation (a
+    # multiple of 2 MiB, minus `pad`): no load reaches past the allocation
+    rows, K = 8192, 4096
+    rb = G.row_bytes(T.Q8_0, K)
+    rs = rb + 2
+    raw = O.Rng(5150 + pad).random_blocks(T.Q8_0, rows * K)
+    nbytes = (rows - 1) * rs + rb
+    big = np.zeros(nbytes, dtype=np.uint8)
+    for r in range(rows):
+        big[r * rs:r * rs + rb] = raw[r * rb:(r + 1) * rb]
+    total = -(-(nbytes + pad) // (2 << 20)) * (2 << 20)
+    buf = G.DeviceBuffer(total)
+    off = total - pad - nbytes
+    buf.upload(big, stream, off)
+    x = np.random.default_rng(pad).standard_normal(K).astype(np.float32)
+    want = O.gemv(T.Q8_0, big, rs, K, rows, x, B=1)
+    dx, dy = G.DeviceBuffer.from_array(x), G.DeviceBuffer(rows * 4)
+    G.ops.gemv(T.Q8_0, buf.ptr(off), rs, K, rows, dx, K, dy, rows, 1, False, stream)
+    got = dy.download(np.float32, rows, stream)
+    assert rel_l2(got[None], want[:1]) <= REL_L2
+
+
 @pytest.mark.parametrize("ty", [t for t in ALL if t != T.BF16])
 @pytest.mark.parametrize("K", [4096, 1536, 2816])
 def test_gemv_matrix_ending_the_allocation(ty, K, stream):
