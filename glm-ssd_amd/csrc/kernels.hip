@@ -772,13 +772,18 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
 // the kernels below.
 #if defined(GS_STREAM_F)
 GS_STREAM_ALL(GS_STREAM_F, GS_STREAM_ID)
-#if GS_STREAM_ID == 8   // Q8_0 one-vector GEMV with aligned pair loads (suffix _wa; FQ8_0A)
-#define GS_STREAM_KERNEL_WA(UM)                                                                   \
-    extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE))) \
-        gs_k_stream_8_0_1_##UM##_wa(StreamArgs a) {                                             \
-        stream_body<FQ8_0A, 0, 1, UM, 64>(a);                                                   \
-    }
-GS_STREAM_KERNEL_WA(2) GS_STREAM_KERNEL_WA(4)
+// one-vector GEMV with aligned pair loads (suffix _wa): Q8_0 (FQ8_0A), Q6_K (FQ6_KA)
+#if GS_STREAM_ID == 8
+extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))
+gs_k_stream_8_0_1_2_wa(StreamArgs a) { stream_body<FQ8_0A, 0, 1, 2, 64>(a); }
+extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))
+gs_k_stream_8_0_1_4_wa(StreamArgs a) { stream_body<FQ8_0A, 0, 1, 4, 64>(a); }
+#endif
+#if GS_STREAM_ID == 14
+extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))
+gs_k_stream_14_0_1_2_wa(StreamArgs a) { stream_body<FQ6_KA, 0, 1, 2, 64>(a); }
+extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))
+gs_k_stream_14_0_1_4_wa(StreamArgs a) { stream_body<FQ6_KA, 0, 1, 4, 64>(a); }
 #endif
 #endif
 

@@ -217,6 +217,17 @@ def test_gemv_q8_0_aligned_pairs(rows, K, pad, acc, stream):
     assert e <= REL_L2
 
 
+@pytest.mark.parametrize("rows,K,pad,acc", [(8200, 4096, 0, False), (8200, 4096, 4, True), (8192, 8192, 0, False),
+                                          (8300, 2048, 2, False)])
+def test_gemv_q6_k_aligned_pairs(rows, K, pad, acc, stream):
+    # one Q6_K vector over at least 4 rows per wave with 4-byte aligned rows takes the
+    # aligned-pair kernel (_wa: odd super-blocks start 2 bytes past a multiple of 4, so both shifts
+    # run); rows 2 bytes apart from a multiple of 4 (pad 2) keep the plain loads
+    e = _gemv_case(T.Q6_K, rows, K, 1, stream, seed=rows + K + pad + 1, accumulate=acc,
+                   row_stride=G.row_bytes(T.Q6_K, K) + pad)
+    assert e <= REL_L2
+
+
 @pytest.mark.parametrize("pad", [0, 2])
 def test_gemv_q8_0_aligned_pairs_ending_the_allocation(pad, stream):
     # the aligned-pair kernel on a matrix whose last row ends at the end of an allocation (a
