@@ -462,6 +462,18 @@ def main():
                 log(f"{name} B={B}: {rb['ms'] * 1e3:.2f} us")
         from glmssd import synth as S
         iq = lambda rng, rows, K: S.random_blocks(rng, G.GgmlType.IQ2_XXS, rows * K, 0.02, [0])
+        # sustained rate: one vector through a matrix of 262144 x 4096 (0.3-0.9 GB, an LM-head-sized
+        # GEMV), two rotated copies, where launch ramp and drain no longer dominate
+        q80 = lambda rng, rows, K: S.random_blocks(rng, G.GgmlType.Q8_0, rows * K, 1 / 127, [0])
+        for name, ty, mk in (("q4_k", G.GgmlType.Q4_K, S.q4_k_matrix), ("q8_0", G.GgmlType.Q8_0, q80),
+                             ("q6_k", G.GgmlType.Q6_K, S.q6_k_matrix), ("iq2_xxs", G.GgmlType.IQ2_XXS, iq)):
+            rb = run_gemv(L, s, ty, 262144, 4096, mk, max(10, args.steps // 20), max(3, args.warmup // 10), 5,
+                          min_rot_bytes=1 << 30)
+            secondary[f"sustained_gemv_{name}_262144x4096"] = {
+                "GB/s": round(rb["gbps"], 1), "us_per_call": round(rb["ms"] * 1e3, 2),
+                "frac_hbm_peak": round(rb["gbps"] / HBM_PEAK_GBPS, 4), "weight_bytes": rb["bytes"],
+                "rotated_copies": rb["copies"]}
+            log(f"sustained {name}: {rb['ms'] * 1e3:.1f} us, {rb['gbps']:.1f} GB/s")
         q6 = lambda rng, rows, K: S.q6_k_matrix(rng, rows, K)
         for name, ty, rows, K, N, mk, uw in [
                 ("gemm_q4_k_k4096_rows12288_N512", G.GgmlType.Q4_K, 12288, 4096, 512, S.q4_k_matrix, True),
