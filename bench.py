@@ -235,7 +235,7 @@ def run_moe_per_token(L, s, layer, n_tok, steps, warmup, seed, n_rout=4, k=8):
 
 
 def run_read_ceiling(L, s, sizes, steps, warmup, ramp_ms, min_pool=768 << 20):
-    """Plain HBM read (bench_kernels.hip bn_k_read) of each byte count, the start address rotated
+    """Plain HBM read (bench_kernels.hip bn_k_read_*, the best of its read shapes) of each byte count, the start address rotated
     over a pool of at least 768 MB so no call is served from the last-level cache: the achievable
     ceiling the streaming kernels are compared with at the same byte count. The warm-up floor
     applies before the first size only (the sizes follow each other with no idle time between
