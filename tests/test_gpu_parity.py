@@ -228,6 +228,13 @@ def test_gemv_q6_k_aligned_pairs(rows, K, pad, acc, stream):
     assert e <= REL_L2
 
 
+@pytest.mark.parametrize("rows,K,acc", [(8200, 4096, False), (8192, 8192, True)])
+def test_gemv_iq2_xxs_many_rows(rows, K, acc, stream):
+    # one IQ2_XXS vector over several row batches per wave (the row ring's refills)
+    e = _gemv_case(T.IQ2_XXS, rows, K, 1, stream, seed=rows + K + 7, accumulate=acc)
+    assert e <= REL_L2
+
+
 @pytest.mark.parametrize("pad", [0, 2])
 def test_gemv_q8_0_aligned_pairs_ending_the_allocation(pad, stream):
     # the aligned-pair kernel on a matrix whose last row ends at the end of an allocation (a
