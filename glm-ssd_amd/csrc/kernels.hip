@@ -1183,7 +1183,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &a) {
         __syncthreads();   // every wave is done with this step's LDS before the next is stored
     }
 }
-// _0: one (tile, chunk) step per workgroup; _1: a walk over several
+// _0: one (chunk, tile) step per workgroup; _1: a walk over several (chunk-major over its tiles)
 #define GS_MV_KERNELS(TY, F)                                                                     \
     extern "C" __global__ void __launch_bounds__(512) gs_k_mv_##TY##_0(MvArgs a) { mv_body<F, false>(a); } \
     extern "C" __global__ void __launch_bounds__(512) gs_k_mv_##TY##_1(MvArgs a) { mv_body<F, true>(a); }
