@@ -205,6 +205,62 @@ struct FQ8_0A : UnitGeom<32, 34>, NoTable {
     }
 };
 
+// Q8_0 over rows that start 4-byte aligned (FQ8_0A4): a lane's unit pair then always starts
+// aligned (68 bytes per pair), so the pair is read as 17 aligned dwords (four 16-byte loads and
+// one 4-byte load, where FQ8_0 issues six loads, four of them 2-byte aligned): unit 0 (sub 0)
+// keeps dwords 0..8 (its scale in the low half of dword 0, its quants 2 bytes in, shifted into
+// place with v_alignbyte), unit 1 dwords 9..16 (its quants aligned) and dword 8 (its scale in the
+// high half). No byte outside the pair is read.
+struct FQ8_0A4 : UnitGeom<32, 34>, NoTable {
+    static constexpr int TYPE = GS_Q8_0, QK = 32, BB = 34, TAB = 0, RAW = 9;
+    struct Raw { uint4 lo, hi; uint32_t x8; };
+    __device__ static __forceinline__ int sub(int u) { return u & 1; }   // the unit's place in its pair
+    template <class M>
+    __device__ static __forceinline__ void load(const M &m, uint32_t o, int s, Raw &w) {
+        if (s == 0) {   // o 4-byte aligned
+            w.lo = m.u128(o);
+            w.hi = m.u128(o + 16);
+            w.x8 = m.u32(o + 32);
+        } else {        // o 2 bytes past a multiple of 4: quants at o+2 aligned, scale to the high half
+            w.lo = m.u128(o + 2);
+            w.hi = m.u128(o + 18);
+            w.x8 = m.u16(o) << 16;
+        }
+    }
+    static constexpr bool PAIR = true;
+    template <class M>
+    __device__ static __forceinline__ void load2(const M &m, uint32_t o, int, Raw &w0, Raw &w1) {
+        w0.lo = m.u128(o);
+        w0.hi = m.u128(o + 16);
+        const uint4 c = m.u128(o + 32);
+        w1.hi = m.u128(o + 48);
+        const uint32_t e = m.u32(o + 64);
+        w0.x8 = c.x;
+        w1.x8 = c.x;
+        w1.lo = make_uint4(c.y, c.z, c.w, w1.hi.x);
+        w1.hi = make_uint4(w1.hi.y, w1.hi.z, w1.hi.w, e);
+    }
+    template <int NV, bool XNEG = false>
+    __device__ static __forceinline__ void dot(const Raw &w, int s, const uint8_t *, const XU (&x)[NV], int nv,
+                                               float (&r)[NV]) {
+        const uint32_t dw[9] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w, w.hi.x, w.hi.y, w.hi.z, w.hi.w, w.x8};
+        uint32_t q[8];
+        float d;
+        if (s == 0) {
+            d = h2f(w.lo.x & 0xffffu);
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[i] = __builtin_amdgcn_alignbyte(dw[i + 1], dw[i], 2);
+        } else {
+            d = h2f(w.x8 >> 16);
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[i] = dw[i];
+        }
+#pragma unroll
+        for (int t = 0; t < NV; t++)
+            if (NV == 1 || t < nv) r[t] += (d * x[t].D) * (float)dot8(q, x[t].q);
+    }
+};
+
 struct FQ4_K : UnitGeom<256, 144>, NoTable {
     static constexpr int TYPE = GS_Q4_K, QK = 256, BB = 144, TAB = 0, RAW = 12;
     struct Raw { uint4 hd, lo, hi; };   // bytes 0..15 (d, dmin, scales[12]); 32 quant bytes

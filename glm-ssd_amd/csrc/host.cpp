@@ -232,20 +232,24 @@ hipError_t stream(int kind, int ty, StreamArgs &a, hipStream_t s, int n_batch = 
     const int NVt = a.nvec <= 1 ? 1 : a.nvec <= 2 ? 2 : a.nvec <= 4 ? 4 : 8;
     // one token with 64-lane groups: the variant with the group width fixed at compile time
     const bool w64 = a.lpr == 64 && NVt == 1 && (kind != 2 || a.wlo != nullptr);
-    // Q8_0 / Q6_K GEMV with at least 4 rows per wave and rows up to 8192 elements: the aligned-load
-    // variants (formats.h FQ8_0A, FQ6_KA). Measured, Q8_0: 8192 x 4096 10.1 -> 8.9 us, 12288 x 4096
-    // 13.9 -> 11.7, 262144 x 4096 245 -> 196, 65536 x 8192 123 -> 118; but 4096 x 4096 6.3 -> 6.6
-    // and 16384 x 12288 47.5 -> 48.4, so fewer rows and longer rows keep the plain loads. Q6_K:
-    // 12288 x 4096 11.6 -> 10.7 us, 16384 x 8192 25.9 -> 24.7, 262144 x 4096 186 -> 159 (its
-    // K = 12288 variant spills).
+    // One-vector GEMV variants with aligned loads (formats.h). Q8_0 rows of an even number of
+    // blocks up to 8192 elements (a lane's unit pair never crosses the row end): rows that start
+    // 4-byte aligned read each pair as 17 aligned dwords (_w4, FQ8_0A4; measured 4096 x 4096
+    // 6.2-7.7 -> 6.3-6.6 us across processes, 12288 x 4096 11.6 -> 11.0, 16384 x 8192 31.7 ->
+    // 24.4); other rows, from 4 rows per wave, shift each unit's quants out of an aligned window
+    // (_wa, FQ8_0A; 262144 x 4096 245 -> 196 us; with fewer rows the plain loads stay faster).
+    // Q6_K from 4 rows per wave, rows 4-byte aligned (its windows start 2 bytes before odd
+    // blocks), up to 8192 elements (the K = 12288 variant spills): _wa, FQ6_KA (12288 x 4096
+    // 11.6 -> 10.7 us, 16384 x 8192 25.9 -> 24.7, 262144 x 4096 186 -> 159).
+    const bool one_vec = w64 && kind == 0 && n_batch == 1 && P.um <= 4;
     const bool many_rows = (int64_t)a.rows >= 4 * (int64_t)c->cu_count * (GS_WG / 64);
-    const bool wa = w64 && kind == 0 && n_batch == 1 && many_rows &&
-                    ((ty == GS_Q8_0 && P.um <= 4) ||
-                     // Q6_K (formats.h FQ6_KA): its windows start 2 bytes before odd blocks, so
-                     // every row must start 4-byte aligned
-                     (ty == GS_Q6_K && P.um <= 4 && a.row_stride % 4 == 0 && ((uintptr_t)a.w0[0] & 3) == 0));
+    const bool rows4 = a.row_stride % 4 == 0 && ((uintptr_t)a.w0[0] & 3) == 0;
+    const bool q8_pairs = one_vec && ty == GS_Q8_0 && a.K % 64 == 0;
+    const bool w4 = q8_pairs && rows4;
+    const bool wa = one_vec && many_rows && ((q8_pairs && !rows4) || (ty == GS_Q6_K && rows4));
     const std::string name = "gs_k_stream_" + std::to_string(ty) + "_" + std::to_string(kind) + "_" +
-                             std::to_string(NVt) + "_" + std::to_string(P.um) + (w64 ? (wa ? "_wa" : "_w") : "");
+                             std::to_string(NVt) + "_" + std::to_string(P.um) +
+                             (w64 ? (w4 ? "_w4" : wa ? "_wa" : "_w") : "");
     hipFunction_t f;
     if ((e = get_fn(c, name, &f)) != hipSuccess) return e;
     const int G = GS_WG / a.lpr;

@@ -772,12 +772,17 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a) {
 // the kernels below.
 #if defined(GS_STREAM_F)
 GS_STREAM_ALL(GS_STREAM_F, GS_STREAM_ID)
-// one-vector GEMV with aligned pair loads (suffix _wa): Q8_0 (FQ8_0A), Q6_K (FQ6_KA)
+// one-vector GEMV variants with aligned loads: _w4 (Q8_0, rows 4-byte aligned: FQ8_0A4) and _wa
+// (Q8_0 other rows: FQ8_0A; Q6_K: FQ6_KA)
 #if GS_STREAM_ID == 8
 extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))
 gs_k_stream_8_0_1_2_wa(StreamArgs a) { stream_body<FQ8_0A, 0, 1, 2, 64>(a); }
 extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))
 gs_k_stream_8_0_1_4_wa(StreamArgs a) { stream_body<FQ8_0A, 0, 1, 4, 64>(a); }
+extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))
+gs_k_stream_8_0_1_2_w4(StreamArgs a) { stream_body<FQ8_0A4, 0, 1, 2, 64>(a); }
+extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))
+gs_k_stream_8_0_1_4_w4(StreamArgs a) { stream_body<FQ8_0A4, 0, 1, 4, 64>(a); }
 #endif
 #if GS_STREAM_ID == 14
 extern "C" __global__ void __launch_bounds__(GS_WG) __attribute__((amdgpu_waves_per_eu(GS_WPE)))

@@ -207,11 +207,13 @@ def test_gemv_vectors_on_mfma(ty, rows, K, stream):
 
 
 @pytest.mark.parametrize("rows,K,pad,acc", [(8200, 4096, 0, False), (8200, 4096, 2, True), (9000, 2048, 2, False),
-                                          (8192, 8192, 2, False)])
+                                          (8192, 8192, 2, False), (8192, 8192, 0, True), (600, 4096, 0, True),
+                                          (8200, 1056, 0, False)])
 def test_gemv_q8_0_aligned_pairs(rows, K, pad, acc, stream):
-    # one Q8_0 vector over at least 4 rows per wave takes the aligned-pair kernel (_wa): each
-    # unit's quants from a dword-aligned window, shifted into place; with rows 2 bytes past a
-    # multiple of 4 apart (pad 2) rows start alternately at 0 and 2 mod 4, so both shifts run
+    # one Q8_0 vector: rows 4-byte aligned (pad 0) read each unit pair as 17 aligned dwords (_w4);
+    # other rows (pad 2: rows start alternately at 0 and 2 mod 4), from 4 rows per wave, shift
+    # each unit's quants out of an aligned window (_wa, both shifts); an odd number of blocks per
+    # row (K = 1056) keeps the plain loads (a pair would cross the row end)
     e = _gemv_case(T.Q8_0, rows, K, 1, stream, seed=rows + K + pad, accumulate=acc,
                    row_stride=G.row_bytes(T.Q8_0, K) + pad)
     assert e <= REL_L2
